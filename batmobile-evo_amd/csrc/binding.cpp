@@ -1,0 +1,550 @@
+// _batmobile: PyTorch-ROCm extension module over libbatmobile_hip.so.
+//
+// Replaces reference python/bindings.cpp (module `_batmobile`, :597-811): same
+// function names, argument names, defaults, argument checks (TORCH_CHECK ->
+// Python RuntimeError), output allocation (torch::empty on the input's device)
+// and stream (the caller's current stream).  Host code only: every launch goes
+// through the C ABI declared in include/batmobile_hip.h.
+//
+// Extensions beyond the reference surface (documented per function below):
+// spherical_harmonics_normalized(+_backward), sh_tp_scatter and neighbor_list.
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <cstdint>
+#include <string>
+#include <tuple>
+
+#include "batmobile_hip.h"
+
+namespace {
+
+void check_device(const torch::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+// Stream of the tensor's device; checks the tensor first, so a CPU tensor gives
+// the argument error before any HIP call is made.
+hipStream_t current_stream(const torch::Tensor& t) {
+    TORCH_CHECK(t.is_cuda(), "inputs must be CUDA tensors");
+    return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+template <typename T>
+const T* cptr(const torch::Tensor& t, const char* name) {
+    check_device(t, name);
+    return t.data_ptr<T>();
+}
+template <typename T>
+T* mptr(torch::Tensor& t, const char* name) {
+    check_device(t, name);
+    return t.data_ptr<T>();
+}
+
+void check_status(int rc, const char* what) {
+    if (rc == BATMOBILE_HIP_OK) return;
+    if (rc == BATMOBILE_HIP_ERR_ARG) TORCH_CHECK(false, what, ": invalid argument");
+    if (rc == BATMOBILE_HIP_ERR_WORKSPACE) TORCH_CHECK(false, what, ": workspace too small");
+    TORCH_CHECK(false, "HIP error in ", what, ": ", hipGetErrorString(static_cast<hipError_t>(rc)));
+}
+
+// 16-byte aligned contiguous view (the MFMA kernels read float4 rows).
+torch::Tensor aligned16(const torch::Tensor& t) {
+    if ((reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0) return t;
+    return t.clone(at::MemoryFormat::Contiguous);
+}
+
+torch::TensorOptions f32_like(const torch::Tensor& t) {
+    return torch::TensorOptions().dtype(torch::kFloat32).device(t.device());
+}
+
+// ---------------------------------------------------------------------------
+// spherical harmonics (reference bindings.cpp:43-114, 236-280)
+// ---------------------------------------------------------------------------
+void check_vectors(const torch::Tensor& v) {
+    TORCH_CHECK(v.dim() == 2, "edge_vectors must be 2D");
+    TORCH_CHECK(v.size(1) == 3, "edge_vectors must have shape [N, 3]");
+    TORCH_CHECK(v.dtype() == torch::kFloat32, "edge_vectors must be float32");
+}
+
+torch::Tensor sh_impl(const torch::Tensor& v, int64_t L_max, int normalize) {
+    check_vectors(v);
+    TORCH_CHECK(L_max >= 0 && L_max <= 6, "L_max must be in [0, 6]");
+    const int64_t N = v.size(0);
+    torch::Tensor Y = torch::empty({N, (L_max + 1) * (L_max + 1)}, f32_like(v));
+    if (N == 0) return Y;
+    const c10::DeviceGuard guard(v.device());
+    check_status(batteries_spherical_harmonics(cptr<float>(v, "edge_vectors"),
+                                               mptr<float>(Y, "Y_lm"), N, (int)L_max, normalize,
+                                               current_stream(v)),
+                 "spherical_harmonics");
+    return Y;
+}
+
+torch::Tensor spherical_harmonics(const torch::Tensor& edge_vectors, int64_t L_max) {
+    return sh_impl(edge_vectors, L_max, 0);
+}
+
+// Extension: SH of v / max(|v|, 1e-10) in one pass (the normalisation of
+// reference python/batmobile/autograd.py:46-58 fused into the kernel).
+torch::Tensor spherical_harmonics_normalized(const torch::Tensor& edge_vectors, int64_t L_max) {
+    return sh_impl(edge_vectors, L_max, 1);
+}
+
+void spherical_harmonics_inplace(const torch::Tensor& edge_vectors, torch::Tensor& Y_lm,
+                                 int64_t L_max) {
+    check_vectors(edge_vectors);
+    TORCH_CHECK(L_max >= 0 && L_max <= 6, "L_max must be in [0, 6]");
+    const int64_t N = edge_vectors.size(0);
+    const int64_t K = (L_max + 1) * (L_max + 1);
+    TORCH_CHECK(Y_lm.dim() == 2, "Y_lm must be 2D");
+    TORCH_CHECK(Y_lm.size(0) == N, "Y_lm must have N rows");
+    TORCH_CHECK(Y_lm.size(1) == K, "Y_lm must have (L_max+1)^2 columns");
+    TORCH_CHECK(Y_lm.dtype() == torch::kFloat32, "Y_lm must be float32");
+    if (N == 0) return;
+    const c10::DeviceGuard guard(edge_vectors.device());
+    check_status(batteries_spherical_harmonics(cptr<float>(edge_vectors, "edge_vectors"),
+                                               mptr<float>(Y_lm, "Y_lm"), N, (int)L_max, 0,
+                                               current_stream(edge_vectors)),
+                 "spherical_harmonics_inplace");
+}
+
+torch::Tensor sh_backward_impl(const torch::Tensor& v, const torch::Tensor& g, int normalize) {
+    check_vectors(v);
+    TORCH_CHECK(g.dim() == 2, "grad_Y_lm must be 2D");
+    TORCH_CHECK(v.size(0) == g.size(0), "Batch sizes must match");
+    TORCH_CHECK(g.dtype() == torch::kFloat32, "grad_Y_lm must be float32");
+    int L_max = -1;
+    for (int l = 0; l <= 6; ++l)
+        if ((l + 1) * (l + 1) == g.size(1)) L_max = l;
+    TORCH_CHECK(L_max >= 0, "Invalid number of components: ", g.size(1));
+    const int64_t N = v.size(0);
+    torch::Tensor out = torch::empty({N, 3}, f32_like(v));
+    if (N == 0) return out;
+    const c10::DeviceGuard guard(v.device());
+    check_status(batteries_spherical_harmonics_backward(
+                     cptr<float>(v, "edge_vectors"), cptr<float>(g, "grad_Y_lm"),
+                     mptr<float>(out, "grad_xyz"), N, L_max, normalize, current_stream(v)),
+                 "spherical_harmonics_backward");
+    return out;
+}
+
+torch::Tensor spherical_harmonics_backward(const torch::Tensor& edge_vectors,
+                                           const torch::Tensor& grad_Y_lm) {
+    return sh_backward_impl(edge_vectors, grad_Y_lm, 0);
+}
+
+// Extension: gradient w.r.t. the raw vector of spherical_harmonics_normalized.
+torch::Tensor spherical_harmonics_normalized_backward(const torch::Tensor& edge_vectors,
+                                                      const torch::Tensor& grad_Y_lm) {
+    return sh_backward_impl(edge_vectors, grad_Y_lm, 1);
+}
+
+// ---------------------------------------------------------------------------
+// tensor products (reference bindings.cpp:120-227, 285-393)
+// ---------------------------------------------------------------------------
+torch::Tensor tensor_product_simple(const torch::Tensor& input1, const torch::Tensor& input2) {
+    TORCH_CHECK(input1.dim() == 2, "input1 must be 2D [N, 16]");
+    TORCH_CHECK(input2.dim() == 2, "input2 must be 2D [N, 16]");
+    TORCH_CHECK(input1.size(1) == 16, "input1 must have 16 components (L_max=3)");
+    TORCH_CHECK(input2.size(1) == 16, "input2 must have 16 components (L_max=3)");
+    TORCH_CHECK(input1.size(0) == input2.size(0), "input1 and input2 must have same N");
+    TORCH_CHECK(input1.dtype() == torch::kFloat32, "input1 must be float32");
+    TORCH_CHECK(input2.dtype() == torch::kFloat32, "input2 must be float32");
+    const int64_t N = input1.size(0);
+    torch::Tensor out = torch::empty({N, 16}, f32_like(input1));
+    if (N == 0) return out;
+    const c10::DeviceGuard guard(input1.device());
+    check_status(batteries_tensor_product_simple_l3(cptr<float>(input1, "input1"),
+                                                    cptr<float>(input2, "input2"),
+                                                    mptr<float>(out, "output"), N,
+                                                    current_stream(input1)),
+                 "tensor_product_simple");
+    return out;
+}
+
+torch::Tensor tensor_product(const torch::Tensor& input1, const torch::Tensor& input2,
+                             const torch::Tensor& weights) {
+    TORCH_CHECK(input1.dim() == 3, "input1 must be 3D [N, C_in, 16]");
+    TORCH_CHECK(input2.dim() == 2, "input2 must be 2D [N, 16]");
+    TORCH_CHECK(weights.dim() == 3, "weights must be 3D [num_paths, C_in, C_out]");
+    TORCH_CHECK(input1.size(2) == 16, "input1 must have 16 components (L_max=3)");
+    TORCH_CHECK(input2.size(1) == 16, "input2 must have 16 components (L_max=3)");
+    TORCH_CHECK(input1.size(0) == input2.size(0), "input1 and input2 must have same N");
+    TORCH_CHECK(input1.dtype() == torch::kFloat32, "input1 must be float32");
+    TORCH_CHECK(input2.dtype() == torch::kFloat32, "input2 must be float32");
+    TORCH_CHECK(weights.dtype() == torch::kFloat32, "weights must be float32");
+    const int64_t N = input1.size(0);
+    const int64_t C_in = input1.size(1);
+    const int64_t C_out = weights.size(2);
+    const int num_paths = batteries_get_num_paths_l3();
+    TORCH_CHECK(weights.size(0) == num_paths, "weights must have ", num_paths, " paths");
+    TORCH_CHECK(weights.size(1) == C_in, "weights C_in must match input1");
+    TORCH_CHECK(C_in > 0 && C_out > 0, "C_in and C_out must be positive");
+    torch::Tensor out = torch::empty({N, C_out, 16}, f32_like(input1));
+    if (N == 0) return out;
+    const c10::DeviceGuard guard(input1.device());
+    check_status(batteries_tensor_product_l3(cptr<float>(input1, "input1"),
+                                             cptr<float>(input2, "input2"),
+                                             cptr<float>(weights, "weights"),
+                                             mptr<float>(out, "output"), N, (int)C_in, (int)C_out,
+                                             current_stream(input1)),
+                 "tensor_product");
+    return out;
+}
+
+torch::Tensor get_tp_path_info() {
+    const int n = batteries_get_num_paths_l3();
+    torch::Tensor info = torch::empty({n, 3}, torch::TensorOptions().dtype(torch::kInt32));
+    batteries_get_path_info_l3(info.data_ptr<int>());
+    return info;
+}
+
+int get_tp_num_paths() { return batteries_get_num_paths_l3(); }
+
+std::tuple<torch::Tensor, torch::Tensor> tensor_product_simple_backward(
+    const torch::Tensor& input1, const torch::Tensor& input2, const torch::Tensor& grad_output) {
+    TORCH_CHECK(input1.dim() == 2 && input1.size(1) == 16, "input1 must be [N, 16]");
+    TORCH_CHECK(input2.dim() == 2 && input2.size(1) == 16, "input2 must be [N, 16]");
+    TORCH_CHECK(grad_output.dim() == 2 && grad_output.size(1) == 16,
+                "grad_output must be [N, 16]");
+    TORCH_CHECK(input1.size(0) == input2.size(0), "Batch sizes must match");
+    TORCH_CHECK(input1.size(0) == grad_output.size(0), "Batch sizes must match");
+    TORCH_CHECK(input1.dtype() == torch::kFloat32 && input2.dtype() == torch::kFloat32 &&
+                    grad_output.dtype() == torch::kFloat32,
+                "inputs must be float32");
+    const int64_t N = input1.size(0);
+    torch::Tensor g1 = torch::empty({N, 16}, f32_like(input1));
+    torch::Tensor g2 = torch::empty({N, 16}, f32_like(input1));
+    if (N == 0) return {g1, g2};
+    const c10::DeviceGuard guard(input1.device());
+    check_status(batteries_tensor_product_simple_backward_l3(
+                     cptr<float>(input1, "input1"), cptr<float>(input2, "input2"),
+                     cptr<float>(grad_output, "grad_output"), mptr<float>(g1, "grad_input1"),
+                     mptr<float>(g2, "grad_input2"), N, current_stream(input1)),
+                 "tensor_product_simple_backward");
+    return {g1, g2};
+}
+
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> tensor_product_backward(
+    const torch::Tensor& input1, const torch::Tensor& input2, const torch::Tensor& weights,
+    const torch::Tensor& grad_output, bool needs_input1_grad, bool needs_input2_grad,
+    bool needs_weights_grad) {
+    TORCH_CHECK(input1.dim() == 3, "input1 must be 3D [N, C_in, 16]");
+    TORCH_CHECK(input2.dim() == 2, "input2 must be 2D [N, 16]");
+    TORCH_CHECK(weights.dim() == 3, "weights must be 3D [num_paths, C_in, C_out]");
+    TORCH_CHECK(grad_output.dim() == 3, "grad_output must be 3D [N, C_out, 16]");
+    const int64_t N = input1.size(0);
+    const int64_t C_in = input1.size(1);
+    const int64_t C_out = weights.size(2);
+    const int num_paths = batteries_get_num_paths_l3();
+    TORCH_CHECK(weights.size(0) == num_paths, "weights must have ", num_paths, " paths");
+    TORCH_CHECK(input1.size(2) == 16 && input2.size(1) == 16, "inputs must have 16 components");
+    TORCH_CHECK(input2.size(0) == N && grad_output.size(0) == N, "Batch sizes must match");
+    TORCH_CHECK(weights.size(1) == C_in, "weights C_in must match input1");
+    TORCH_CHECK(grad_output.size(1) == C_out && grad_output.size(2) == 16,
+                "grad_output must be [N, C_out, 16]");
+    TORCH_CHECK(input1.dtype() == torch::kFloat32 && input2.dtype() == torch::kFloat32 &&
+                    weights.dtype() == torch::kFloat32 && grad_output.dtype() == torch::kFloat32,
+                "inputs must be float32");
+    TORCH_CHECK(C_out <= 256, "C_out must be <= 256");
+    auto opt = f32_like(input1);
+    torch::Tensor g1, g2, gW;
+    if (needs_input1_grad) g1 = torch::empty({N, C_in, 16}, opt);
+    if (needs_input2_grad) g2 = torch::empty({N, 16}, opt);
+    if (needs_weights_grad) gW = torch::empty({num_paths, C_in, C_out}, opt);
+    if (N == 0) {
+        if (!g1.defined()) g1 = torch::empty({0, C_in, 16}, opt);
+        if (!g2.defined()) g2 = torch::empty({0, 16}, opt);
+        if (!gW.defined()) gW = torch::zeros({num_paths, C_in, C_out}, opt);
+        else gW.zero_();
+        return {g1, g2, gW};
+    }
+    const c10::DeviceGuard guard(input1.device());
+    torch::Tensor ws;
+    size_t wsb = 0;
+    if (needs_weights_grad) {
+        wsb = batteries_tensor_product_backward_workspace_bytes(N, (int)C_in, (int)C_out);
+        ws = torch::empty({(int64_t)((wsb + 3) / 4)}, opt);
+    }
+    check_status(batteries_tensor_product_backward_l3(
+                     cptr<float>(input1, "input1"), cptr<float>(input2, "input2"),
+                     cptr<float>(weights, "weights"), cptr<float>(grad_output, "grad_output"),
+                     needs_input1_grad ? mptr<float>(g1, "grad_input1") : nullptr,
+                     needs_input2_grad ? mptr<float>(g2, "grad_input2") : nullptr,
+                     needs_weights_grad ? mptr<float>(gW, "grad_weights") : nullptr, N, (int)C_in,
+                     (int)C_out, ws.defined() ? ws.data_ptr() : nullptr, wsb,
+                     current_stream(input1)),
+                 "tensor_product_backward");
+    return {g1, g2, gW};
+}
+
+// ---------------------------------------------------------------------------
+// message passing (reference bindings.cpp:402-595)
+// ---------------------------------------------------------------------------
+std::tuple<torch::Tensor, torch::Tensor> edge_index_to_csr(const torch::Tensor& edge_index,
+                                                           int64_t N_atoms) {
+    TORCH_CHECK(edge_index.dim() == 2, "edge_index must be 2D [2, N_edges]");
+    TORCH_CHECK(edge_index.size(0) == 2, "edge_index first dim must be 2");
+    TORCH_CHECK(edge_index.dtype() == torch::kInt64, "edge_index must be int64");
+    TORCH_CHECK(N_atoms >= 0, "N_atoms must be non-negative");
+    const int64_t E = edge_index.size(1);
+    auto opt = torch::TensorOptions().dtype(torch::kInt64).device(edge_index.device());
+    torch::Tensor row_ptr = torch::empty({N_atoms + 1}, opt);
+    torch::Tensor col_idx = torch::empty({E}, opt);
+    const c10::DeviceGuard guard(edge_index.device());
+    const size_t wsb = batteries_edge_index_to_csr_workspace_bytes(N_atoms);
+    torch::Tensor ws = torch::empty({std::max<int64_t>(1, N_atoms)}, opt);
+    check_status(batteries_edge_index_to_csr(cptr<int64_t>(edge_index, "edge_index"),
+                                             mptr<int64_t>(row_ptr, "row_ptr"),
+                                             mptr<int64_t>(col_idx, "col_idx"), N_atoms, E,
+                                             ws.data_ptr(), wsb, current_stream(edge_index)),
+                 "edge_index_to_csr");
+    return {row_ptr, col_idx};
+}
+
+void check_features(const torch::Tensor& x, const char* name) {
+    TORCH_CHECK(x.dim() == 3, name, " must be 3D [N_atoms, C, 16]");
+    TORCH_CHECK(x.size(2) == 16, name, " must have 16 irrep components");
+    TORCH_CHECK(x.dtype() == torch::kFloat32, name, " must be float32");
+    TORCH_CHECK(x.size(1) > 0, name, " must have at least one channel");
+}
+
+torch::Tensor fused_message_passing_simple(const torch::Tensor& node_features,
+                                           const torch::Tensor& edge_vectors,
+                                           const torch::Tensor& edge_index,
+                                           const torch::Tensor& row_ptr,
+                                           const torch::Tensor& col_idx) {
+    check_features(node_features, "node_features");
+    TORCH_CHECK(edge_vectors.dim() == 2, "edge_vectors must be 2D [N_edges, 3]");
+    TORCH_CHECK(edge_vectors.size(1) == 3, "edge_vectors must have shape [N_edges, 3]");
+    TORCH_CHECK(edge_index.dim() == 2, "edge_index must be 2D [2, N_edges]");
+    TORCH_CHECK(edge_index.size(0) == 2, "edge_index first dim must be 2");
+    TORCH_CHECK(edge_vectors.dtype() == torch::kFloat32, "edge_vectors must be float32");
+    TORCH_CHECK(edge_index.dtype() == torch::kInt64, "edge_index must be int64");
+    TORCH_CHECK(row_ptr.dtype() == torch::kInt64, "row_ptr must be int64");
+    TORCH_CHECK(col_idx.dtype() == torch::kInt64, "col_idx must be int64");
+    const int64_t N = node_features.size(0);
+    const int64_t E = edge_vectors.size(0);
+    const int64_t C = node_features.size(1);
+    TORCH_CHECK(edge_index.size(1) == E, "edge_index must have N_edges columns");
+    TORCH_CHECK(row_ptr.numel() == N + 1, "row_ptr must have N_atoms + 1 entries");
+    TORCH_CHECK(col_idx.numel() == E, "col_idx must have N_edges entries");
+    torch::Tensor out = torch::empty({N, C, 16}, f32_like(node_features));
+    if (N == 0) return out;
+    const c10::DeviceGuard guard(node_features.device());
+    torch::Tensor x = aligned16(node_features);
+    check_status(batteries_fused_message_passing_simple(
+                     cptr<float>(x, "node_features"), cptr<float>(edge_vectors, "edge_vectors"),
+                     cptr<int64_t>(edge_index, "edge_index"), cptr<int64_t>(row_ptr, "row_ptr"),
+                     cptr<int64_t>(col_idx, "col_idx"), mptr<float>(out, "output"), N, E, (int)C,
+                     current_stream(node_features)),
+                 "fused_message_passing_simple");
+    return out;
+}
+
+torch::Tensor fused_message_passing(const torch::Tensor& node_features,
+                                    const torch::Tensor& edge_vectors,
+                                    const torch::Tensor& weights, const torch::Tensor& row_ptr,
+                                    const torch::Tensor& col_idx) {
+    check_features(node_features, "node_features");
+    TORCH_CHECK(edge_vectors.dim() == 2, "edge_vectors must be 2D [N_edges, 3]");
+    TORCH_CHECK(edge_vectors.size(1) == 3, "edge_vectors must have shape [N_edges, 3]");
+    TORCH_CHECK(weights.dim() == 2, "weights must be 2D [C_in, C_out]");
+    TORCH_CHECK(edge_vectors.dtype() == torch::kFloat32, "edge_vectors must be float32");
+    TORCH_CHECK(weights.dtype() == torch::kFloat32, "weights must be float32");
+    TORCH_CHECK(row_ptr.dtype() == torch::kInt64, "row_ptr must be int64");
+    TORCH_CHECK(col_idx.dtype() == torch::kInt64, "col_idx must be int64");
+    const int64_t N = node_features.size(0);
+    const int64_t E = edge_vectors.size(0);
+    const int64_t C_in = node_features.size(1);
+    const int64_t C_out = weights.size(1);
+    TORCH_CHECK(weights.size(0) == C_in, "weights first dim must match C_in");
+    TORCH_CHECK(row_ptr.numel() == N + 1, "row_ptr must have N_atoms + 1 entries");
+    TORCH_CHECK(col_idx.numel() == E, "col_idx must have N_edges entries");
+    torch::Tensor out = torch::empty({N, C_out, 16}, f32_like(node_features));
+    if (N == 0) return out;
+    const c10::DeviceGuard guard(node_features.device());
+    torch::Tensor x = aligned16(node_features);
+    const size_t wsb = batteries_fused_message_passing_workspace_bytes(N, (int)C_in);
+    torch::Tensor ws = torch::empty({N, C_in, 16}, f32_like(node_features));
+    check_status(batteries_fused_message_passing(
+                     cptr<float>(x, "node_features"), cptr<float>(edge_vectors, "edge_vectors"),
+                     cptr<float>(weights, "weights"), cptr<int64_t>(row_ptr, "row_ptr"),
+                     cptr<int64_t>(col_idx, "col_idx"), mptr<float>(out, "output"), N, E,
+                     (int)C_in, (int)C_out, ws.data_ptr(), wsb, current_stream(node_features)),
+                 "fused_message_passing");
+    return out;
+}
+
+torch::Tensor fused_sh_tp_simple(const torch::Tensor& edge_vectors,
+                                 const torch::Tensor& node_features,
+                                 const torch::Tensor& source_idx) {
+    TORCH_CHECK(edge_vectors.dim() == 2, "edge_vectors must be 2D [N_edges, 3]");
+    TORCH_CHECK(edge_vectors.size(1) == 3, "edge_vectors must have shape [N_edges, 3]");
+    check_features(node_features, "node_features");
+    TORCH_CHECK(source_idx.dim() == 1, "source_idx must be 1D [N_edges]");
+    TORCH_CHECK(edge_vectors.dtype() == torch::kFloat32, "edge_vectors must be float32");
+    TORCH_CHECK(source_idx.dtype() == torch::kInt64, "source_idx must be int64");
+    const int64_t E = edge_vectors.size(0);
+    const int64_t C = node_features.size(1);
+    TORCH_CHECK(source_idx.size(0) == E, "source_idx must have N_edges elements");
+    torch::Tensor msg = torch::empty({E, C, 16}, f32_like(node_features));
+    if (E == 0) return msg;
+    const c10::DeviceGuard guard(node_features.device());
+    torch::Tensor x = aligned16(node_features);
+    check_status(batteries_fused_sh_tp_simple(cptr<float>(edge_vectors, "edge_vectors"),
+                                              cptr<float>(x, "node_features"),
+                                              cptr<int64_t>(source_idx, "source_idx"),
+                                              mptr<float>(msg, "messages"), E, (int)C, 0,
+                                              current_stream(node_features)),
+                 "fused_sh_tp_simple");
+    return msg;
+}
+
+// Extension: out[d] = sum_{k in CSR row d} TP_simple(X[source_idx[e_k]], Y(v_{e_k})),
+// e_k = perm[k] if perm is given else k; normalize=True evaluates Y at v/|v|.
+// One kernel, no messages tensor, no atomics.
+torch::Tensor sh_tp_scatter(const torch::Tensor& edge_vectors, const torch::Tensor& node_features,
+                            const torch::Tensor& source_idx, const torch::Tensor& row_ptr,
+                            const c10::optional<torch::Tensor>& perm, bool normalize) {
+    check_vectors(edge_vectors);
+    check_features(node_features, "node_features");
+    TORCH_CHECK(source_idx.dim() == 1 && source_idx.dtype() == torch::kInt64,
+                "source_idx must be int64 [N_edges]");
+    TORCH_CHECK(row_ptr.dim() == 1 && row_ptr.dtype() == torch::kInt64 && row_ptr.numel() >= 1,
+                "row_ptr must be int64 [N_dst + 1]");
+    const int64_t E = edge_vectors.size(0);
+    const int64_t N_dst = row_ptr.numel() - 1;
+    const int64_t C = node_features.size(1);
+    TORCH_CHECK(source_idx.numel() == E, "source_idx must have N_edges elements");
+    const int64_t* pp = nullptr;
+    if (perm.has_value() && perm->defined()) {
+        TORCH_CHECK(perm->dtype() == torch::kInt64 && perm->numel() == E,
+                    "perm must be int64 [N_edges]");
+        pp = cptr<int64_t>(*perm, "perm");
+    }
+    torch::Tensor out = torch::empty({N_dst, C, 16}, f32_like(node_features));
+    if (N_dst == 0) return out;
+    const c10::DeviceGuard guard(node_features.device());
+    torch::Tensor x = aligned16(node_features);
+    check_status(batteries_sh_tp_scatter_csr(cptr<float>(edge_vectors, "edge_vectors"),
+                                             cptr<float>(x, "node_features"),
+                                             cptr<int64_t>(source_idx, "source_idx"), pp,
+                                             cptr<int64_t>(row_ptr, "row_ptr"),
+                                             mptr<float>(out, "output"), N_dst, E, (int)C,
+                                             normalize ? 1 : 0, current_stream(node_features)),
+                 "sh_tp_scatter");
+    return out;
+}
+
+// Extension (torch-level form of the reference's ctypes neighbor list):
+// returns (edge_index int64 [2, E] with row 0 = i, row 1 = j sorted by (i, j),
+// edge_vectors [E, 3] = minimum-image pos[j] - pos[i], row_offsets int64 [N+1]).
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
+    const torch::Tensor& positions, const torch::Tensor& cell, double cutoff, bool self_loops) {
+    TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
+    TORCH_CHECK(positions.dtype() == torch::kFloat32, "positions must be float32");
+    TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
+    check_device(positions, "positions");
+    const int64_t N = positions.size(0);
+    torch::Tensor cell_cpu = cell.detach().to(torch::kCPU, torch::kFloat32).contiguous();
+    const float* h = cell_cpu.data_ptr<float>();
+    const float box[3] = {h[0], h[4], h[8]};
+    const float rc = (float)cutoff;
+    const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, rc);
+    TORCH_CHECK(wsb > 0, "invalid cell or cutoff");
+    auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(positions.device());
+    auto i32 = torch::TensorOptions().dtype(torch::kInt32).device(positions.device());
+    const c10::DeviceGuard guard(positions.device());
+    hipStream_t s = current_stream(positions);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
+    torch::Tensor total = torch::empty({1}, i64);
+    check_status(batteries_neighbor_list_count(cptr<float>(positions, "positions"), box, N, rc,
+                                               self_loops ? 1 : 0, ws.data_ptr(), wsb,
+                                               total.data_ptr<int64_t>(), s),
+                 "neighbor_list");
+    const int64_t E = total.item<int64_t>();  // one host sync, as in the reference
+    torch::Tensor src = torch::empty({E}, i32);
+    torch::Tensor dst = torch::empty({E}, i32);
+    torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
+    torch::Tensor offsets = torch::empty({N + 1}, i64);
+    check_status(batteries_neighbor_list_write(cptr<float>(positions, "positions"), box, N, rc,
+                                               self_loops ? 1 : 0, ws.data_ptr(), wsb,
+                                               src.data_ptr<int>(), dst.data_ptr<int>(),
+                                               vec.data_ptr<float>(), offsets.data_ptr<int64_t>(),
+                                               s),
+                 "neighbor_list");
+    torch::Tensor edge_index = torch::stack({src.to(torch::kInt64), dst.to(torch::kInt64)}, 0);
+    return {edge_index, vec, offsets};
+}
+
+torch::Tensor selftest_mfma_16x16x4(const torch::Tensor& A, const torch::Tensor& B) {
+    TORCH_CHECK(A.numel() == 64 && B.numel() == 64 && A.dtype() == torch::kFloat32 &&
+                    B.dtype() == torch::kFloat32,
+                "A [16,4] and B [4,16] float32");
+    torch::Tensor D = torch::empty({16, 16}, f32_like(A));
+    const c10::DeviceGuard guard(A.device());
+    check_status(batteries_selftest_mfma_16x16x4(cptr<float>(A, "A"), cptr<float>(B, "B"),
+                                                 mptr<float>(D, "D"), current_stream(A)),
+                 "selftest_mfma_16x16x4");
+    return D;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_batmobile, m) {
+    namespace py = pybind11;
+    m.doc() = "batmobile on MI355X: HIP kernels for equivariant message passing";
+    m.def("spherical_harmonics", &spherical_harmonics, py::arg("edge_vectors"), py::arg("L_max"),
+          "Real spherical harmonics Y_lm [N, (L_max+1)^2] of edge_vectors [N, 3], L_max in [0, 6]");
+    m.def("spherical_harmonics_inplace", &spherical_harmonics_inplace, py::arg("edge_vectors"),
+          py::arg("Y_lm"), py::arg("L_max"),
+          "Compute spherical harmonics with pre-allocated output buffer");
+    m.def("tensor_product_simple", &tensor_product_simple, py::arg("input1"), py::arg("input2"),
+          "Simple 34-path CG tensor product [N,16] x [N,16] -> [N,16]");
+    m.def("tensor_product", &tensor_product, py::arg("input1"), py::arg("input2"),
+          py::arg("weights"),
+          "Channel-weighted tensor product [N,C_in,16] x [N,16], W [34,C_in,C_out] -> [N,C_out,16]");
+    m.def("get_tp_path_info", &get_tp_path_info,
+          "Tensor product path info as [num_paths, 3] int32 (l1, l2, l_out)");
+    m.def("get_tp_num_paths", &get_tp_num_paths, "Number of tensor product paths for L_max=3");
+    m.def("spherical_harmonics_backward", &spherical_harmonics_backward, py::arg("edge_vectors"),
+          py::arg("grad_Y_lm"), "Backward of spherical_harmonics w.r.t. edge_vectors");
+    m.def("tensor_product_simple_backward", &tensor_product_simple_backward, py::arg("input1"),
+          py::arg("input2"), py::arg("grad_output"), "(grad_input1, grad_input2)");
+    m.def("tensor_product_backward", &tensor_product_backward, py::arg("input1"),
+          py::arg("input2"), py::arg("weights"), py::arg("grad_output"),
+          py::arg("needs_input1_grad") = true, py::arg("needs_input2_grad") = true,
+          py::arg("needs_weights_grad") = true,
+          "(grad_input1, grad_input2, grad_weights); skipped gradients are None");
+    m.def("edge_index_to_csr", &edge_index_to_csr, py::arg("edge_index"), py::arg("N_atoms"),
+          "COO edge_index [2, E] -> (row_ptr [N+1], col_idx [E]) grouped by target");
+    m.def("fused_message_passing_simple", &fused_message_passing_simple,
+          py::arg("node_features"), py::arg("edge_vectors"), py::arg("edge_index"),
+          py::arg("row_ptr"), py::arg("col_idx"), "SH -> TP -> scatter_add in one kernel");
+    m.def("fused_message_passing", &fused_message_passing, py::arg("node_features"),
+          py::arg("edge_vectors"), py::arg("weights"), py::arg("row_ptr"), py::arg("col_idx"),
+          "Fused message passing with dense channel-mixing weights [C_in, C_out]");
+    m.def("fused_sh_tp_simple", &fused_sh_tp_simple, py::arg("edge_vectors"),
+          py::arg("node_features"), py::arg("source_idx"),
+          "Fused SH + simple TP -> messages [N_edges, C, 16]");
+    // extensions
+    m.def("spherical_harmonics_normalized", &spherical_harmonics_normalized,
+          py::arg("edge_vectors"), py::arg("L_max"),
+          "spherical_harmonics of v / max(|v|, 1e-10), normalisation fused");
+    m.def("spherical_harmonics_normalized_backward", &spherical_harmonics_normalized_backward,
+          py::arg("edge_vectors"), py::arg("grad_Y_lm"),
+          "gradient of spherical_harmonics_normalized w.r.t. the raw vectors");
+    m.def("sh_tp_scatter", &sh_tp_scatter, py::arg("edge_vectors"), py::arg("node_features"),
+          py::arg("source_idx"), py::arg("row_ptr"), py::arg("perm") = py::none(),
+          py::arg("normalize") = false,
+          "Fused SH + simple TP + scatter-add over CSR rows (no messages tensor, no atomics)");
+    m.def("neighbor_list", &neighbor_list, py::arg("positions"), py::arg("cell"),
+          py::arg("cutoff"), py::arg("self_loops") = false,
+          "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], row_offsets)");
+    m.def("selftest_mfma_16x16x4", &selftest_mfma_16x16x4, py::arg("A"), py::arg("B"),
+          "D = A @ B through one v_mfma_f32_16x16x4f32 (lane-layout self test)");
+}

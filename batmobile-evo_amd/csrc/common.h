@@ -1,0 +1,176 @@
+// Shared device helpers for the batmobile MI355X (gfx950) kernels.
+//
+// All Clebsch-Gordan and spherical-harmonic constants come from
+// generated_tables.h and are folded into straight-line code at compile time
+// (static_for over constexpr tables), so no kernel reads a coefficient from
+// memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <utility>
+
+#include "generated_tables.h"
+
+namespace bmhip {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// compile-time loop: f(std::integral_constant<int, i>) for i in [0, N)
+// ---------------------------------------------------------------------------
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__host__ __device__ constexpr int sh_dim(int l) { return (l + 1) * (l + 1); }
+
+// ---------------------------------------------------------------------------
+// Real spherical harmonics (e3nn component normalisation, y polar axis) of a
+// (not necessarily unit) vector, as the recurrence
+//   Y_{l+1}[M] = sum c * Y_l[m] * r_j .
+// Same polynomials as reference spherical_harmonics.cu:56-256.
+// ---------------------------------------------------------------------------
+template <int L>
+__device__ __forceinline__ void sh_forward(float x, float y, float z, float* Y) {
+    Y[0] = 1.0f;
+    const float r[3] = {x, y, z};
+    static_for<kSHTermStart[L]>([&](auto tt) {
+        constexpr int t = decltype(tt)::value;
+        constexpr SHTerm T = kSHTerms[t];
+        constexpr int l = [] {
+            int ll = 0;
+            while (kSHTermStart[ll + 1] <= t) ++ll;
+            return ll;
+        }();
+        constexpr bool first = (t == kSHTermStart[l]) || (kSHTerms[t > 0 ? t - 1 : 0].M != T.M);
+        constexpr int out = sh_dim(l) + T.M;
+        constexpr int in = l * l + T.m;
+        if constexpr (first) {
+            Y[out] = (T.c * Y[in]) * r[T.j];
+        } else {
+            Y[out] = fmaf(T.c * Y[in], r[T.j], Y[out]);
+        }
+    });
+}
+
+// Reverse-mode gradient of sh_forward: g (dL/dY, clobbered) -> dL/d(x,y,z).
+template <int L>
+__device__ __forceinline__ void sh_backward(float x, float y, float z, const float* Y, float* g,
+                                            float& gx, float& gy, float& gz) {
+    const float r[3] = {x, y, z};
+    float gr[3] = {0.0f, 0.0f, 0.0f};
+    constexpr int NT = kSHTermStart[L];
+    static_for<NT>([&](auto tt) {
+        constexpr int t = NT - 1 - decltype(tt)::value;  // reverse order
+        constexpr SHTerm T = kSHTerms[t];
+        constexpr int l = [] {
+            int ll = 0;
+            while (kSHTermStart[ll + 1] <= t) ++ll;
+            return ll;
+        }();
+        constexpr int out = sh_dim(l) + T.M;
+        constexpr int in = l * l + T.m;
+        const float go = g[out] * T.c;
+        gr[T.j] = fmaf(go, Y[in], gr[T.j]);
+        if constexpr (in != 0) g[in] = fmaf(go, r[T.j], g[in]);
+    });
+    gx = gr[0];
+    gy = gr[1];
+    gz = gr[2];
+}
+
+// u = v / max(|v|, 1e-10): SphericalHarmonicsFunction's normalisation
+// (reference python/batmobile/autograd.py:46-52).
+__device__ __forceinline__ float normalize3(float& x, float& y, float& z) {
+    const float r = fmaxf(sqrtf(x * x + y * y + z * z), 1e-10f);
+    const float inv = 1.0f / r;
+    x *= inv;
+    y *= inv;
+    z *= inv;
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Simple tensor product pieces (34 paths, 611 entries, L<=3).
+// ---------------------------------------------------------------------------
+
+// out[o] = sum c * x[a] * y[b]
+__device__ __forceinline__ void tp_simple(const float* x, const float* y, float* out) {
+#pragma unroll
+    for (int o = 0; o < 16; ++o) out[o] = 0.0f;
+    static_for<kNumEntries>([&](auto kk) {
+        constexpr CGEntry e = kCG[decltype(kk)::value];
+        out[e.o] = fmaf(e.c * y[e.b], x[e.a], out[e.o]);
+    });
+}
+
+// gx[a] = sum c * g[o] * y[b];  gy[b] = sum c * g[o] * x[a]
+__device__ __forceinline__ void tp_simple_backward(const float* x, const float* y, const float* g,
+                                                   float* gx, float* gy) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        gx[i] = 0.0f;
+        gy[i] = 0.0f;
+    }
+    static_for<kNumEntries>([&](auto kk) {
+        constexpr CGEntry e = kCG[decltype(kk)::value];
+        const float cg = e.c * g[e.o];
+        gx[e.a] = fmaf(cg, y[e.b], gx[e.a]);
+        gy[e.b] = fmaf(cg, x[e.a], gy[e.b]);
+    });
+}
+
+// Edge operator M(y)[o][a] = sum_b c * y[b], so that tp_simple(x, y) = M x.
+// Row o only (compile-time), written to m[0..15].
+template <int O>
+__device__ __forceinline__ void edge_operator_row(const float* y, float* m) {
+#pragma unroll
+    for (int a = 0; a < 16; ++a) m[a] = 0.0f;
+    static_for<kNumEntries>([&](auto kk) {
+        constexpr CGEntry e = kCG[decltype(kk)::value];
+        if constexpr (e.o == O) m[e.a] = fmaf(e.c, y[e.b], m[e.a]);
+    });
+}
+
+// Per-path products: t[q] = sum_{(a,b) in slot q} c * x[a] * cy  with y given.
+// cyq is not precomputed here; used by the weighted kernels.
+__device__ __forceinline__ void tp_per_path(const float* x, const float* y, float* t) {
+#pragma unroll
+    for (int q = 0; q < kNumSlots; ++q) t[q] = 0.0f;
+    static_for<kNumEntries>([&](auto kk) {
+        constexpr CGEntry e = kCG[decltype(kk)::value];
+        t[e.q] = fmaf(e.c * y[e.b], x[e.a], t[e.q]);
+    });
+}
+
+// Adjoint of tp_per_path: given h[q] = dL/dt[q],
+//   gx[a] += sum c * h[q] * y[b];  gy[b] += sum c * h[q] * x[a]
+__device__ __forceinline__ void tp_per_path_backward(const float* x, const float* y, const float* h,
+                                                     float* gx, float* gy) {
+    static_for<kNumEntries>([&](auto kk) {
+        constexpr CGEntry e = kCG[decltype(kk)::value];
+        const float ch = e.c * h[e.q];
+        gx[e.a] = fmaf(ch, y[e.b], gx[e.a]);
+        gy[e.b] = fmaf(ch, x[e.a], gy[e.b]);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// small helpers
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace bmhip
+
+// Status codes returned by the C ABI (0 = success).
+#define BM_OK 0
+#define BM_ERR_ARG -1
+#define BM_ERR_WORKSPACE -2

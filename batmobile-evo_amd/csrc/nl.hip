@@ -1,0 +1,432 @@
+// Cell-list neighbor list with periodic (orthorhombic) boundaries, and the
+// exclusive prefix scan used by it and by the CSR conversion.
+//
+// Replaces reference src/neighbor_list/neighbor_list.cu:18-478.
+// Same geometry as the reference: box = cell diagonal, bins per axis =
+// max(3, int(L / r_c)), bin = min(int(wrap(p) / b), bins - 1) with
+// wrap(p) = p - floorf(p * (1/L)) * L, minimum image d -= rintf(d * (1/L)) * L,
+// keep d.d <= r_c^2 (inclusive), j != i unless self loops, emit src = i,
+// dst = j, vec = d grouped by i.
+//
+// Unlike the reference the result is deterministic: atoms inside a bin are
+// ordered by index and each atom's neighbors are sorted by j, so the output is
+// sorted by (i, j).  All distance arithmetic is evaluated without FMA
+// contraction in one fixed order, so the kept pairs are a function of the
+// fp32 inputs alone.
+#include "common.h"
+#include "batmobile_hip.h"
+
+#include <cstring>
+#include <vector>
+
+namespace bmhip {
+
+struct BinCfg {
+    int nb[3];
+    float bin[3];
+    float box[3];
+    float inv[3];
+    int total;
+};
+
+static BinCfg make_bin_cfg(const float box[3], float cutoff) {
+    BinCfg c;
+    for (int d = 0; d < 3; ++d) {
+        c.box[d] = box[d];
+        c.inv[d] = 1.0f / box[d];
+        const int n = (int)(box[d] / cutoff);
+        c.nb[d] = n > 3 ? n : 3;
+        c.bin[d] = box[d] / (float)c.nb[d];
+    }
+    c.total = c.nb[0] * c.nb[1] * c.nb[2];
+    return c;
+}
+
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ void bin_coords(float px, float py, float pz, const BinCfg& c,
+                                           int* b) {
+    const float p[3] = {px, py, pz};
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        const float t = p[d] * c.inv[d];
+        const float fl = floorf(t) * c.box[d];
+        const float wpos = p[d] - fl;
+        const int v = (int)(wpos / c.bin[d]);
+        b[d] = v < c.nb[d] - 1 ? v : c.nb[d] - 1;
+    }
+}
+
+__device__ __forceinline__ float min_image(const float* pi, const float* pj, const BinCfg& c,
+                                           float* d) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float t = pj[k] - pi[k];
+        const float s = t * c.inv[k];
+        const float r = rintf(s);
+        const float m = r * c.box[k];
+        d[k] = t - m;
+    }
+    const float xx = d[0] * d[0];
+    const float yy = d[1] * d[1];
+    const float zz = d[2] * d[2];
+    const float s = xx + yy;
+    return s + zz;
+}
+
+#pragma clang fp contract(on)
+
+__device__ __forceinline__ int wrap_bin(int b, int n) { return (b + n) % n; }
+
+__global__ void nl_zero_i32_kernel(int* __restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+__global__ void nl_assign_kernel(const float* __restrict__ pos, BinCfg c, int* __restrict__ bin_of,
+                                 int* __restrict__ bin_count, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int b[3];
+    bin_coords(pos[i * 3], pos[i * 3 + 1], pos[i * 3 + 2], c, b);
+    const int k = b[0] + b[1] * c.nb[0] + b[2] * c.nb[0] * c.nb[1];
+    bin_of[i] = k;
+    atomicAdd(bin_count + k, 1);
+}
+
+__global__ void nl_place_kernel(const int* __restrict__ bin_of, const int64_t* __restrict__ bin_start,
+                                int* __restrict__ cursor, int* __restrict__ order, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int k = bin_of[i];
+    const int pos = atomicAdd(cursor + k, 1);
+    order[bin_start[k] + pos] = (int)i;
+}
+
+// ascending atom index inside each bin
+__global__ void nl_sort_bins_kernel(const int64_t* __restrict__ bin_start, int* __restrict__ order,
+                                    int total) {
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= total) return;
+    const int64_t s = bin_start[k], e = bin_start[k + 1];
+    for (int64_t i = s + 1; i < e; ++i) {
+        const int v = order[i];
+        int64_t j = i - 1;
+        while (j >= s && order[j] > v) {
+            order[j + 1] = order[j];
+            --j;
+        }
+        order[j + 1] = v;
+    }
+}
+
+template <bool WRITE>
+__global__ void nl_stencil_kernel(const float* __restrict__ pos, BinCfg c, float rc2,
+                                  int self_loops, const int64_t* __restrict__ bin_start,
+                                  const int* __restrict__ order, int64_t* __restrict__ counts,
+                                  const int64_t* __restrict__ offsets, int* __restrict__ esrc,
+                                  int* __restrict__ edst, float* __restrict__ evec, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float pi[3] = {pos[i * 3], pos[i * 3 + 1], pos[i * 3 + 2]};
+    int b[3];
+    bin_coords(pi[0], pi[1], pi[2], c, b);
+    int64_t w = WRITE ? offsets[i] : 0;
+    int64_t cnt = 0;
+    for (int dz = -1; dz <= 1; ++dz)
+        for (int dy = -1; dy <= 1; ++dy)
+            for (int dx = -1; dx <= 1; ++dx) {
+                const int k = wrap_bin(b[0] + dx, c.nb[0]) + wrap_bin(b[1] + dy, c.nb[1]) * c.nb[0] +
+                              wrap_bin(b[2] + dz, c.nb[2]) * c.nb[0] * c.nb[1];
+                for (int64_t s = bin_start[k]; s < bin_start[k + 1]; ++s) {
+                    const int j = order[s];
+                    if (!self_loops && j == (int)i) continue;
+                    const float pj[3] = {pos[(int64_t)j * 3], pos[(int64_t)j * 3 + 1],
+                                         pos[(int64_t)j * 3 + 2]};
+                    float d[3];
+                    if (min_image(pi, pj, c, d) <= rc2) {
+                        if constexpr (WRITE) {
+                            esrc[w] = (int)i;
+                            edst[w] = j;
+                            evec[w * 3 + 0] = d[0];
+                            evec[w * 3 + 1] = d[1];
+                            evec[w * 3 + 2] = d[2];
+                            ++w;
+                        } else {
+                            ++cnt;
+                        }
+                    }
+                }
+            }
+    if constexpr (!WRITE) counts[i] = cnt;
+}
+
+// sort each atom's neighbors by j (insertion sort; ~30 entries)
+__global__ void nl_sort_rows_kernel(const int64_t* __restrict__ offsets, int* __restrict__ edst,
+                                    float* __restrict__ evec, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t s = offsets[i], e = offsets[i + 1];
+    for (int64_t a = s + 1; a < e; ++a) {
+        const int v = edst[a];
+        const float v0 = evec[a * 3], v1 = evec[a * 3 + 1], v2 = evec[a * 3 + 2];
+        int64_t j = a - 1;
+        while (j >= s && edst[j] > v) {
+            edst[j + 1] = edst[j];
+            evec[(j + 1) * 3] = evec[j * 3];
+            evec[(j + 1) * 3 + 1] = evec[j * 3 + 1];
+            evec[(j + 1) * 3 + 2] = evec[j * 3 + 2];
+            --j;
+        }
+        edst[j + 1] = v;
+        evec[(j + 1) * 3] = v0;
+        evec[(j + 1) * 3 + 1] = v1;
+        evec[(j + 1) * 3 + 2] = v2;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// exclusive scan: out[0..n] (out[n] = total), one workgroup, chunked, fixed order
+// ---------------------------------------------------------------------------
+constexpr int kScanBlock = 1024;
+
+template <typename TI>
+__global__ __launch_bounds__(kScanBlock) void scan_exclusive_kernel(const TI* __restrict__ in,
+                                                                    int64_t* __restrict__ out,
+                                                                    int64_t n) {
+    __shared__ int64_t buf[kScanBlock];
+    __shared__ int64_t carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (int64_t base = 0; base < n; base += kScanBlock) {
+        const int64_t i = base + threadIdx.x;
+        const int64_t v = i < n ? (int64_t)in[i] : 0;
+        buf[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < kScanBlock; off <<= 1) {
+            const int64_t add = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
+            __syncthreads();
+            buf[threadIdx.x] += add;
+            __syncthreads();
+        }
+        const int64_t incl = buf[threadIdx.x];
+        if (i < n) out[i] = carry + incl - v;
+        __syncthreads();
+        if (threadIdx.x == kScanBlock - 1) carry += incl;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[n] = carry;
+}
+
+static int scan_i64(const int64_t* in, int64_t* out, int64_t n, hipStream_t s) {
+    scan_exclusive_kernel<int64_t><<<1, kScanBlock, 0, s>>>(in, out, n);
+    return (int)hipGetLastError();
+}
+static int scan_i32(const int* in, int64_t* out, int64_t n, hipStream_t s) {
+    scan_exclusive_kernel<int><<<1, kScanBlock, 0, s>>>(in, out, n);
+    return (int)hipGetLastError();
+}
+
+// Workspace layout for a neighbor-list build of n atoms (all 256-B aligned):
+//   bin_of int[n] | bin_count int[total] | bin_start i64[total+1] | order int[n]
+//   | counts i64[n] | offsets i64[n+1]
+struct NlLayout {
+    size_t bin_of, bin_count, bin_start, order, counts, offsets, total_bytes;
+};
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+static NlLayout nl_layout(int64_t n, int total_bins) {
+    NlLayout L;
+    size_t o = 0;
+    L.bin_of = o; o = align256(o + sizeof(int) * (size_t)n);
+    L.bin_count = o; o = align256(o + sizeof(int) * (size_t)total_bins);
+    L.bin_start = o; o = align256(o + sizeof(int64_t) * ((size_t)total_bins + 1));
+    L.order = o; o = align256(o + sizeof(int) * (size_t)n);
+    L.counts = o; o = align256(o + sizeof(int64_t) * (size_t)n);
+    L.offsets = o; o = align256(o + sizeof(int64_t) * ((size_t)n + 1));
+    L.total_bytes = o;
+    return L;
+}
+
+static bool valid_box(const float box[3], float cutoff) {
+    if (!(cutoff > 0.0f)) return false;
+    for (int d = 0; d < 3; ++d)
+        if (!(box[d] > 0.0f)) return false;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    return (int64_t)c.nb[0] * c.nb[1] * c.nb[2] < (int64_t)1 << 30;
+}
+
+}  // namespace bmhip
+
+using namespace bmhip;
+
+extern "C" int batteries_exclusive_scan_i64(const int64_t* in, int64_t* out, int64_t n,
+                                            hipStream_t stream) {
+    if (n < 0) return BM_ERR_ARG;
+    return scan_i64(in, out, n, stream);
+}
+
+extern "C" size_t batteries_neighbor_list_workspace_bytes(int64_t N, const float* box,
+                                                          float cutoff) {
+    if (N < 0 || !box || !valid_box(box, cutoff)) return 0;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    return nl_layout(N, c.total).total_bytes;
+}
+
+extern "C" int batteries_neighbor_list_count(const float* positions, const float* box, int64_t N,
+                                             float cutoff, int self_loops, void* workspace,
+                                             size_t workspace_bytes, int64_t* d_num_edges,
+                                             hipStream_t stream) {
+    if (N < 0 || !box || !valid_box(box, cutoff)) return BM_ERR_ARG;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    const NlLayout L = nl_layout(N, c.total);
+    if (!workspace || workspace_bytes < L.total_bytes) return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    int* bin_of = reinterpret_cast<int*>(ws + L.bin_of);
+    int* bin_count = reinterpret_cast<int*>(ws + L.bin_count);
+    int64_t* bin_start = reinterpret_cast<int64_t*>(ws + L.bin_start);
+    int* order = reinterpret_cast<int*>(ws + L.order);
+    int64_t* counts = reinterpret_cast<int64_t*>(ws + L.counts);
+    int64_t* offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
+    const int B = 256;
+    nl_zero_i32_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_count, c.total);
+    if (N > 0)
+        nl_assign_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(positions, c, bin_of, bin_count,
+                                                                     N);
+    int rc = scan_i32(bin_count, bin_start, c.total, stream);
+    if (rc != BM_OK) return rc;
+    nl_zero_i32_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_count, c.total);
+    if (N > 0) {
+        nl_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(bin_of, bin_start, bin_count,
+                                                                    order, N);
+        nl_sort_bins_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_start, order,
+                                                                              c.total);
+        nl_stencil_kernel<false><<<(unsigned)ceil_div(N, B), B, 0, stream>>>(
+            positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
+            nullptr, nullptr, N);
+    }
+    rc = scan_i64(counts, offsets, N, stream);
+    if (rc != BM_OK) return rc;
+    if (d_num_edges) {
+        hipError_t e = hipMemcpyAsync(d_num_edges, offsets + N, sizeof(int64_t),
+                                      hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess) return (int)e;
+    }
+    return (int)hipGetLastError();
+}
+
+extern "C" int batteries_neighbor_list_write(const float* positions, const float* box, int64_t N,
+                                             float cutoff, int self_loops, void* workspace,
+                                             size_t workspace_bytes, int* edge_src, int* edge_dst,
+                                             float* edge_vectors, int64_t* row_offsets,
+                                             hipStream_t stream) {
+    if (N < 0 || !box || !valid_box(box, cutoff)) return BM_ERR_ARG;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    const NlLayout L = nl_layout(N, c.total);
+    if (!workspace || workspace_bytes < L.total_bytes) return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    const int64_t* bin_start = reinterpret_cast<const int64_t*>(ws + L.bin_start);
+    const int* order = reinterpret_cast<const int*>(ws + L.order);
+    const int64_t* offsets = reinterpret_cast<const int64_t*>(ws + L.offsets);
+    const int B = 256;
+    if (N > 0) {
+        nl_stencil_kernel<true><<<(unsigned)ceil_div(N, B), B, 0, stream>>>(
+            positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, edge_src,
+            edge_dst, edge_vectors, N);
+        nl_sort_rows_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(offsets, edge_dst,
+                                                                        edge_vectors, N);
+    }
+    if (row_offsets) {
+        hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
+                                      hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess) return (int)e;
+    }
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Reference-compatible C ABI (src/neighbor_list/neighbor_list.cu:456-478,
+// include/neighbor_list.cuh:25-33): library-owned device buffers, freed by
+// neighbor_list_free; cell [3,3] in device memory; one host sync for E.
+// ---------------------------------------------------------------------------
+extern "C" int neighbor_list_cuda(const float* positions, const float* cell, int64_t N,
+                                  float cutoff, bool self_loops, NeighborListResult* result,
+                                  hipStream_t stream) {
+    if (!result) return BM_ERR_ARG;
+    result->edge_index = nullptr;
+    result->edge_vectors = nullptr;
+    result->d_edge_index = nullptr;
+    result->d_edge_vectors = nullptr;
+    result->num_edges = 0;
+    if (N == 0) return BM_OK;
+    if (N < 0 || !positions || !cell) return BM_ERR_ARG;
+    float h_cell[9];
+    hipError_t e = hipMemcpy(h_cell, cell, sizeof(h_cell), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return (int)e;
+    const float box[3] = {h_cell[0], h_cell[4], h_cell[8]};
+    if (!valid_box(box, cutoff)) return BM_ERR_ARG;
+    const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, cutoff);
+    void* ws = nullptr;
+    int64_t* d_total = nullptr;
+    e = hipMalloc(&ws, wsb);
+    if (e != hipSuccess) return (int)e;
+    e = hipMalloc(&d_total, sizeof(int64_t));
+    if (e != hipSuccess) {
+        (void)hipFree(ws);
+        return (int)e;
+    }
+    int rc = batteries_neighbor_list_count(positions, box, N, cutoff, self_loops ? 1 : 0, ws, wsb,
+                                           d_total, stream);
+    int64_t total = 0;
+    if (rc == BM_OK) {
+        e = hipMemcpyAsync(&total, d_total, sizeof(int64_t), hipMemcpyDeviceToHost, stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        rc = (int)e;
+    }
+    if (rc == BM_OK && total > 0) {
+        int* d_ei = nullptr;
+        float* d_vec = nullptr;
+        e = hipMalloc(&d_ei, sizeof(int) * 2 * (size_t)total);
+        if (e == hipSuccess) e = hipMalloc(&d_vec, sizeof(float) * 3 * (size_t)total);
+        if (e != hipSuccess) {
+            if (d_ei) (void)hipFree(d_ei);
+            rc = (int)e;
+        } else {
+            rc = batteries_neighbor_list_write(positions, box, N, cutoff, self_loops ? 1 : 0, ws, wsb,
+                                               d_ei, d_ei + total, d_vec, nullptr, stream);
+            if (rc == BM_OK) rc = (int)hipStreamSynchronize(stream);
+            if (rc == BM_OK) {
+                result->d_edge_index = d_ei;
+                result->d_edge_vectors = d_vec;
+                result->edge_index = d_ei;
+                result->edge_vectors = d_vec;
+                result->num_edges = total;
+            } else {
+                (void)hipFree(d_ei);
+                (void)hipFree(d_vec);
+            }
+        }
+    }
+    (void)hipFree(ws);
+    (void)hipFree(d_total);
+    return rc;
+}
+
+extern "C" void neighbor_list_free(NeighborListResult* result) {
+    if (!result) return;
+    if (result->d_edge_index) (void)hipFree(result->d_edge_index);
+    if (result->d_edge_vectors) (void)hipFree(result->d_edge_vectors);
+    result->d_edge_index = nullptr;
+    result->d_edge_vectors = nullptr;
+    result->edge_index = nullptr;
+    result->edge_vectors = nullptr;
+    result->num_edges = 0;
+}
+
+extern "C" size_t neighbor_list_estimate_memory(int64_t N, float density, float cutoff) {
+    // same estimate as reference neighbor_list.cu:442-451
+    const float vol = (4.0f / 3.0f) * 3.14159f * cutoff * cutoff * cutoff;
+    const int avg = (int)(density * vol) + 1;
+    const size_t edge_memory = (size_t)N * avg * (2 * sizeof(int) + 3 * sizeof(float));
+    const size_t temp_memory = (size_t)N * sizeof(int) * 4;
+    return edge_memory + temp_memory;
+}

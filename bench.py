@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Benchmark: fused SH + TP + scatter-add, BASELINE configs[3] (simple variant).
+
+Workload (one "step" = one pass of the hot path over the whole system):
+  N = 5000 atoms uniform in a periodic cube of side (N / rho)^(1/3) = 44.356 A,
+  rho = 30 / (4/3 pi 5^3); cutoff 5.0 A inclusive, no self loops -> E ~ 1.5e5
+  directed edges from the GPU cell-list neighbor list, sorted by destination;
+  edge vectors r_dst - r_src (minimum image), normalised inside the kernel;
+  node features X [5000, 64, 16] ~ N(0, 1) fp32.
+  step: out[d] = sum_{e -> d} TP_simple(X[src_e], Y_lm(v_e / |v_e|))  [5000, 64, 16]
+  (batmobile.sh_tp_scatter: one kernel, inputs resident in HBM).
+
+Prints ONE JSON line (rank 0).  value = edges/s over the timed region.
+`roofline` uses the survey's algorithmic byte count for this path,
+  B = E * (12 + 8 + 64 C) + N * (64 C + 8)
+(edge vector, source index, gathered source row; output row and row pointer),
+divided by the kernel's average duration from HIP events on the launch stream;
+`roofline_mfma` gives the same duration against the fp32 MFMA peak with the
+kernel's flop count E * (2 * 256 * C + 2 * 611) (16x16 edge operator applied to
+C channels, plus building it from the 611 CG entries).
+`cpu_baseline` times the reference's float32 PyTorch composition on the host
+cores (oracle/cpu_path.py) on the same workload.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "batmobile-evo_amd", "python"))
+sys.path.insert(0, REPO)
+
+METRIC = "fused SH+TP+scatter edges/s (N=5k,C=64,~30 nbr) + % of HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
+N_ATOMS, CHANNELS, CUTOFF = 5000, 64, 5.0
+RHO = 30.0 / (4.0 / 3.0 * math.pi * CUTOFF ** 3)
+SEED = 3
+
+
+def make_workload(torch, bm, dev):
+    g = torch.Generator().manual_seed(SEED)
+    L = (N_ATOMS / RHO) ** (1.0 / 3.0)
+    pos = torch.rand(N_ATOMS, 3, generator=g) * L
+    cell = torch.diag(torch.tensor([L, L, L]))
+    x = torch.randn(N_ATOMS, CHANNELS, 16, generator=g)
+    ei, vec, row_ptr = bm.neighbor_list(pos.to(dev), cell, CUTOFF, False)
+    # NL rows are (i, j) sorted by (i, j); the message edge j -> i has vector r_i - r_j
+    src, dst, evec = ei[1].contiguous(), ei[0].contiguous(), (-vec).contiguous()
+    return dict(pos=pos, cell=cell, L=L, x=x.to(dev), src=src, dst=dst, vec=evec, row_ptr=row_ptr)
+
+
+def time_nl(torch, bm, dev, w, reps=5):
+    pos = w["pos"].to(dev)
+    bm.neighbor_list(pos, w["cell"], CUTOFF, False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        bm.neighbor_list(pos, w["cell"], CUTOFF, False)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def time_reference_composition(torch, bm, dev, w, reps=10):
+    """The reference's own timed pipeline on these kernels: fused_sh_tp_simple
+    (messages [E,C,16]) then torch index_add_ (benchmarks/benchmark_fused_sh_tp.py:103-109)."""
+    vn = w["vec"] / w["vec"].norm(dim=1, keepdim=True)
+
+    def once():
+        m = bm.fused_sh_tp_simple(vn, w["x"], w["src"])
+        return torch.zeros(N_ATOMS, CHANNELS, 16, device=dev).index_add_(0, w["dst"], m)
+
+    once()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        once()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def cpu_baseline(torch, w, gpu_out):
+    import numpy as np
+
+    from oracle import cpu_path
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    vec, x = w["vec"].cpu(), w["x"].cpu()
+    src, dst = w["src"].cpu(), w["dst"].cpu()
+    e = vec.shape[0]
+    out = cpu_path.sh_tp_scatter(vec, x, src, dst, N_ATOMS)      # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (len(times) < 3 or time.perf_counter() - t_start < 20.0):
+        t0 = time.perf_counter()
+        out = cpu_path.sh_tp_scatter(vec, x, src, dst, N_ATOMS)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    err = float((out - gpu_out.cpu()).abs().max() / gpu_out.abs().max().cpu())
+    return {
+        "value": e / med,
+        "unit": "edges/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"full configs[3] workload (E={e}, C={CHANNELS}), float32 torch on CPU "
+                  f"(SH polynomials -> per-edge CG einsum -> index_add_), median of {len(times)} "
+                  f"after 1 warm-up, {med * 1e3:.1f} ms/step",
+        "cpu_vs_gpu_normwise_err": err,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
+              "(every box here has one MI355X; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import batmobile as bm
+    dev = torch.device("cuda:0")
+    w = make_workload(torch, bm, dev)
+    E = int(w["src"].numel())
+
+    def step():
+        return bm.sh_tp_scatter(w["vec"], w["x"], w["src"], w["row_ptr"], None, True)
+
+    for _ in range(a.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()      # the stream the kernel is launched on
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(a.steps):
+        out = step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = ev0.elapsed_time(ev1) / a.steps
+    ms_per_step = wall / a.steps * 1e3
+
+    C = CHANNELS
+    bytes_alg = E * (12 + 8 + 64 * C) + N_ATOMS * (64 * C + 8)
+    flops_alg = E * (2 * 256 * C + 2 * 611)
+    achieved_gbs = bytes_alg / (kernel_ms * 1e-3) / 1e9
+    achieved_tf = flops_alg / (kernel_ms * 1e-3) / 1e12
+
+    extra = {}
+    extra["neighbor_list_ms"] = round(time_nl(torch, bm, dev, w), 4)
+    extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
+
+    res = {
+        "metric": METRIC,
+        "value": E / (ms_per_step * 1e-3),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (uniform periodic positions, N(0,1) features; seeded)",
+        "config": {
+            "workload": "configs[3] fused SH+TP+scatter, simple variant: N=5000 atoms, C=64, "
+                        "cutoff 5.0 A (~30 nbr), edges sorted by destination, in-kernel normalisation",
+            "N_atoms": N_ATOMS, "C": C, "E": E, "box_A": round(w["L"], 4), "seed": SEED,
+            "kernel": "mp_simple_mfma_kernel<SCATTER, NORM> (batmobile.sh_tp_scatter)",
+            "reference_published_rtx3090_ms": 5.935,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": None,
+            "algorithmic_bytes_per_launch": bytes_alg, "kernel_ms": kernel_ms,
+        },
+        "roofline_mfma": {
+            "bound": "mfma", "achieved": achieved_tf, "peak": MFMA_FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": achieved_tf / MFMA_FP32_PEAK_TFLOPS,
+            "algorithmic_flops_per_launch": flops_alg,
+        },
+        "also": extra,
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(torch, w, out)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+/*
+ * batmobile_hip.h -- C ABI of libbatmobile_hip.so, the MI355X (gfx950) HIP
+ * implementation of batmobile's equivariant message-passing path.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless marked "host".
+ *   - Tensors are dense, row-major, fp32 (int64 for indices) as described.
+ *   - Work is enqueued on `stream` and is asynchronous unless stated.
+ *   - Return value: 0 on success, a hipError_t value (> 0) on a launch/runtime
+ *     error, BM_ERR_ARG (-1) for invalid arguments, BM_ERR_WORKSPACE (-2) for a
+ *     missing or too small workspace.
+ *   - No function allocates device memory except the reference-compatible
+ *     neighbor_list_cuda(); where scratch is needed the caller passes a
+ *     workspace whose size is given by the matching *_workspace_bytes().
+ *
+ * Each entry point names the reference function it replaces
+ * (paths relative to the reference repository).
+ */
+#ifndef BATMOBILE_HIP_H_
+#define BATMOBILE_HIP_H_
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BATMOBILE_HIP_OK 0
+#define BATMOBILE_HIP_ERR_ARG -1
+#define BATMOBILE_HIP_ERR_WORKSPACE -2
+
+/* ---------------------------------------------------------------------------
+ * Spherical harmonics, L_max in [0, 6]
+ * ------------------------------------------------------------------------- */
+
+/* Y_lm[N, (L_max+1)^2] of edge_vectors[N, 3].  normalize = 0 evaluates the
+ * polynomials on the vectors as given (reference behaviour); normalize = 1
+ * first divides each vector by max(|v|, 1e-10).
+ * Replaces batteries::spherical_harmonics_dispatch,
+ * src/spherical_harmonics/spherical_harmonics.cu:296-314 (bound at
+ * python/bindings.cpp:43-78 and, for the pre-allocated output, :83-114). */
+int batteries_spherical_harmonics(const float* edge_vectors, float* Y_lm, int64_t N, int L_max,
+                                  int normalize, hipStream_t stream);
+
+/* grad_xyz[N, 3] = sum_lm grad_Y_lm[N, lm] * dY_lm/d(x,y,z).  With normalize = 1
+ * the input is the raw vector and the result is chained through v/|v|
+ * (python/batmobile/autograd.py:62-92).
+ * Replaces batteries::spherical_harmonics_backward_dispatch,
+ * src/spherical_harmonics/spherical_harmonics_backward.cu:440-463 (bound at
+ * python/bindings.cpp:236-280); also covers L_max 4..6, which the reference
+ * kernel rejects. */
+int batteries_spherical_harmonics_backward(const float* edge_vectors, const float* grad_Y_lm,
+                                           float* grad_xyz, int64_t N, int L_max, int normalize,
+                                           hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 34-path L<=3 Clebsch-Gordan tensor products
+ * ------------------------------------------------------------------------- */
+
+/* 34.  Replaces batteries::get_num_paths_l3, src/tensor_product/tensor_product.cu:203-205. */
+int batteries_get_num_paths_l3(void);
+
+/* path_info (host) [34, 3] = (l1, l2, l_out).  Replaces batteries::get_path_info_l3,
+ * src/tensor_product/tensor_product.cu:207-214. */
+void batteries_get_path_info_l3(int* path_info);
+
+/* output[N,16] = sum c * input1[N,16]_a * input2[N,16]_b.  Replaces
+ * batteries::tensor_product_simple_l3, src/tensor_product/tensor_product.cu:159-176. */
+int batteries_tensor_product_simple_l3(const float* input1, const float* input2, float* output,
+                                       int64_t N, hipStream_t stream);
+
+/* (grad_input1, grad_input2)[N,16].  Replaces batteries::tensor_product_simple_backward_l3,
+ * src/tensor_product/tensor_product_backward.cu:1007-1026. */
+int batteries_tensor_product_simple_backward_l3(const float* input1, const float* input2,
+                                                const float* grad_output, float* grad_input1,
+                                                float* grad_input2, int64_t N, hipStream_t stream);
+
+/* output[N, C_out, 16] = sum_p sum_ci weights[p, ci, co] * TP_p(input1[N, C_in, 16], input2[N, 16]).
+ * Replaces batteries::tensor_product_l3, src/tensor_product/tensor_product.cu:178-201. */
+int batteries_tensor_product_l3(const float* input1, const float* input2, const float* weights,
+                                float* output, int64_t N, int C_in, int C_out, hipStream_t stream);
+
+/* Workspace for batteries_tensor_product_backward_l3 with grad_weights != NULL. */
+size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in, int C_out);
+
+/* Exact adjoint of batteries_tensor_product_l3.  Any of grad_input1 [N,C_in,16],
+ * grad_input2 [N,16], grad_weights [34,C_in,C_out] may be NULL (not computed).
+ * grad_weights is a deterministic reduction over rows; N = 0 gives zeros.
+ * C_out <= 256.  Replaces batteries::tensor_product_backward_l3,
+ * src/tensor_product/tensor_product_backward.cu:948-1005 (bound at
+ * python/bindings.cpp:325-393). */
+int batteries_tensor_product_backward_l3(const float* input1, const float* input2,
+                                         const float* weights, const float* grad_output,
+                                         float* grad_input1, float* grad_input2,
+                                         float* grad_weights, int64_t N, int C_in, int C_out,
+                                         void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused SH + TP, scatter-add, CSR
+ * ------------------------------------------------------------------------- */
+
+/* messages[E, C, 16] = TP_simple(node_features[source_idx[e], C, 16], Y(edge_vectors[e])).
+ * normalize as in batteries_spherical_harmonics (0 = reference behaviour).
+ * node_features and messages must be 16-byte aligned.
+ * Replaces batteries::fused_sh_tp_simple, src/message_passing/fused_sh_tp.cu:125-146. */
+int batteries_fused_sh_tp_simple(const float* edge_vectors, const float* node_features,
+                                 const int64_t* source_idx, float* messages, int64_t N_edges,
+                                 int C, int normalize, hipStream_t stream);
+
+/* Fused SH + TP + scatter-add into destinations, one pass, no atomics,
+ * deterministic:
+ *   node_output[d, C, 16] = sum_{k in [row_ptr[d], row_ptr[d+1])}
+ *        TP_simple(node_features[source_idx[e_k]], Y(edge_vectors[e_k])),
+ *   e_k = perm ? perm[k] : k.
+ * Destinations with no edges get zeros.  No counterpart as a single call in the
+ * reference: it is the composition fused_sh_tp_simple -> index_add_
+ * (benchmarks/benchmark_fused_sh_tp.py:96-98,105-107) and the engine of
+ * batteries::fused_message_passing_simple below. */
+int batteries_sh_tp_scatter_csr(const float* edge_vectors, const float* node_features,
+                                const int64_t* source_idx, const int64_t* perm,
+                                const int64_t* row_ptr, float* node_output, int64_t N_dst,
+                                int64_t N_edges, int C, int normalize, hipStream_t stream);
+
+/* node_output[N_atoms, C, 16]; CSR slot k is edge col_idx[k], whose source is
+ * edge_index[0, col_idx[k]] and vector edge_vectors[col_idx[k]].
+ * Replaces batteries::fused_message_passing_simple,
+ * src/message_passing/fused_message_passing.cu:257-280. */
+int batteries_fused_message_passing_simple(const float* node_features, const float* edge_vectors,
+                                           const int64_t* edge_index, const int64_t* row_ptr,
+                                           const int64_t* col_idx, float* node_output,
+                                           int64_t N_atoms, int64_t N_edges, int C,
+                                           hipStream_t stream);
+
+/* Workspace for batteries_fused_message_passing. */
+size_t batteries_fused_message_passing_workspace_bytes(int64_t N_atoms, int C_in);
+
+/* node_output[N_atoms, C_out, 16] = sum_ci weights[ci, co] * S[t, ci, :] where S is
+ * the simple fused pass with source atom col_idx[k] and vector edge_vectors[k] for
+ * CSR slot k (the reference kernel's indexing, fused_message_passing.cu:332-337).
+ * Replaces batteries::fused_message_passing,
+ * src/message_passing/fused_message_passing.cu:376-400. */
+int batteries_fused_message_passing(const float* node_features, const float* edge_vectors,
+                                    const float* weights, const int64_t* row_ptr,
+                                    const int64_t* col_idx, float* node_output, int64_t N_atoms,
+                                    int64_t N_edges, int C_in, int C_out, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace for batteries_edge_index_to_csr. */
+size_t batteries_edge_index_to_csr_workspace_bytes(int64_t N_atoms);
+
+/* row_ptr[N_atoms+1] and col_idx[E] (original edge ids grouped by target
+ * edge_index[1, e], ascending inside each row).  Replaces
+ * batteries::edge_index_to_csr, src/message_passing/fused_message_passing.cu:108-165. */
+int batteries_edge_index_to_csr(const int64_t* edge_index, int64_t* row_ptr, int64_t* col_idx,
+                                int64_t N_atoms, int64_t N_edges, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
+
+/* out[0..n] = exclusive prefix sum of in[0..n-1], out[n] = total (one
+ * workgroup, fixed order).  Replaces the cub::DeviceScan::ExclusiveSum calls of
+ * src/neighbor_list/neighbor_list.cu:332-336,356-360 and
+ * src/message_passing/fused_message_passing.cu:140-151. */
+int batteries_exclusive_scan_i64(const int64_t* in, int64_t* out, int64_t n, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Cell-list neighbor list (orthorhombic PBC)
+ * ------------------------------------------------------------------------- */
+
+/* Workspace for the two-phase build; box (host) = cell diagonal. 0 if invalid. */
+size_t batteries_neighbor_list_workspace_bytes(int64_t N, const float* box, float cutoff);
+
+/* Phase 1: bins, per-atom counts, offsets; writes E to *d_num_edges (device,
+ * may be NULL).  Steps :261-366 of batteries::neighbor_list_cuda,
+ * src/neighbor_list/neighbor_list.cu. */
+int batteries_neighbor_list_count(const float* positions, const float* box, int64_t N,
+                                  float cutoff, int self_loops, void* workspace,
+                                  size_t workspace_bytes, int64_t* d_num_edges, hipStream_t stream);
+
+/* Phase 2 (same workspace, after phase 1): edge_src[E] = i, edge_dst[E] = j,
+ * edge_vectors[E,3] = minimum-image pos[j] - pos[i], sorted by (i, j);
+ * row_offsets[N+1] (may be NULL) = start of each i.  Steps :367-402 of
+ * batteries::neighbor_list_cuda. */
+int batteries_neighbor_list_write(const float* positions, const float* box, int64_t N,
+                                  float cutoff, int self_loops, void* workspace,
+                                  size_t workspace_bytes, int* edge_src, int* edge_dst,
+                                  float* edge_vectors, int64_t* row_offsets, hipStream_t stream);
+
+/* Result of neighbor_list_cuda; same layout as include/neighbor_list.cuh:25-33. */
+typedef struct NeighborListResult {
+    int* edge_index;      /* [2, num_edges] int32: row 0 = src i, row 1 = dst j */
+    float* edge_vectors;  /* [num_edges, 3] */
+    int64_t num_edges;
+    int* d_edge_index;    /* owned by the library, released by neighbor_list_free */
+    float* d_edge_vectors;
+} NeighborListResult;
+
+/* Reference-compatible entry points (same names and arguments):
+ * src/neighbor_list/neighbor_list.cu:458-468, :470-472, :474-476.
+ * cell is a device [3,3] matrix; the call synchronises once to size the output
+ * and allocates it (freed by neighbor_list_free). */
+int neighbor_list_cuda(const float* positions, const float* cell, int64_t N, float cutoff,
+                       bool self_loops, NeighborListResult* result, hipStream_t stream);
+void neighbor_list_free(NeighborListResult* result);
+size_t neighbor_list_estimate_memory(int64_t N, float density, float cutoff);
+
+/* ---------------------------------------------------------------------------
+ * Self test (no reference counterpart): D[16,16] = A[16,4] B[4,16] through one
+ * v_mfma_f32_16x16x4f32 with the lane layout the kernels above assume.
+ * ------------------------------------------------------------------------- */
+int batteries_selftest_mfma_16x16x4(const float* A, const float* B, float* D, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BATMOBILE_HIP_H_ */

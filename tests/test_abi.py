@@ -1,0 +1,93 @@
+"""The C ABI library and the extension module: load, exports, argument errors (CPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(REPO, "batmobile-evo_amd", "lib", "libbatmobile_hip.so")
+HEADER = os.path.join(REPO, "include", "batmobile_hip.h")
+
+
+def _declared_functions():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    names = re.findall(r"^\s*(?:int|void|size_t)\s+(\w+)\s*\(", txt, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_the_path():
+    names = _declared_functions()
+    for n in ("batteries_spherical_harmonics", "batteries_tensor_product_l3",
+              "batteries_tensor_product_backward_l3", "batteries_sh_tp_scatter_csr",
+              "batteries_fused_sh_tp_simple", "batteries_edge_index_to_csr",
+              "neighbor_list_cuda", "neighbor_list_free", "neighbor_list_estimate_memory"):
+        assert n in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_host_only_entry_points():
+    lib = ctypes.CDLL(LIB)
+    assert lib.batteries_get_num_paths_l3() == 34
+    info = (ctypes.c_int * 102)()
+    lib.batteries_get_path_info_l3(info)
+    assert list(info[:9]) == [0, 0, 0, 0, 1, 1, 0, 2, 2]
+    lib.neighbor_list_estimate_memory.restype = ctypes.c_size_t
+    lib.neighbor_list_estimate_memory.argtypes = [ctypes.c_int64, ctypes.c_float, ctypes.c_float]
+    assert lib.neighbor_list_estimate_memory(1000, 0.05, 5.0) > 0
+    lib.batteries_neighbor_list_workspace_bytes.restype = ctypes.c_size_t
+    lib.batteries_neighbor_list_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_void_p,
+                                                            ctypes.c_float]
+    box = (ctypes.c_float * 3)(20.0, 20.0, 20.0)
+    assert lib.batteries_neighbor_list_workspace_bytes(100, box, 5.0) > 0
+    bad = (ctypes.c_float * 3)(20.0, -1.0, 20.0)
+    assert lib.batteries_neighbor_list_workspace_bytes(100, bad, 5.0) == 0
+
+
+def test_extension_module_names(bm):
+    import _batteries
+    import batmobile
+    ref_names = ["spherical_harmonics", "spherical_harmonics_inplace", "tensor_product_simple",
+                 "tensor_product", "get_tp_path_info", "get_tp_num_paths",
+                 "spherical_harmonics_backward", "tensor_product_simple_backward",
+                 "tensor_product_backward", "edge_index_to_csr", "fused_message_passing_simple",
+                 "fused_message_passing", "fused_sh_tp_simple"]
+    for n in ref_names:
+        assert getattr(bm, n) is getattr(_batteries, n)
+        assert hasattr(batmobile, n)
+    for n in ("SphericalHarmonicsFunction", "TensorProductSimpleFunction", "TensorProductFunction",
+              "spherical_harmonics_autograd", "tensor_product_autograd"):
+        assert hasattr(batmobile, n)
+    info = bm.get_tp_path_info()
+    assert info.dtype == torch.int32 and tuple(info.shape) == (34, 3) and info.device.type == "cpu"
+    assert bm.get_tp_num_paths() == 34
+
+
+@pytest.mark.parametrize("call", [
+    lambda b: b.spherical_harmonics(torch.zeros(4, 3), 3),                       # CPU tensor
+    lambda b: b.spherical_harmonics(torch.zeros(4, 3), 7),                       # L range
+    lambda b: b.spherical_harmonics(torch.zeros(4, 2), 3),                       # shape
+    lambda b: b.spherical_harmonics(torch.zeros(4, 3, dtype=torch.float64), 3),  # dtype
+    lambda b: b.tensor_product_simple(torch.zeros(4, 16), torch.zeros(5, 16)),
+    lambda b: b.tensor_product(torch.zeros(4, 2, 16), torch.zeros(4, 16), torch.zeros(33, 2, 3)),
+    lambda b: b.tensor_product(torch.zeros(4, 2, 16), torch.zeros(4, 16), torch.zeros(34, 3, 3)),
+    lambda b: b.tensor_product_backward(torch.zeros(4, 2, 16), torch.zeros(4, 16),
+                                        torch.zeros(34, 2, 3), torch.zeros(4, 5, 16)),
+    lambda b: b.spherical_harmonics_backward(torch.zeros(4, 3), torch.zeros(4, 15)),
+    lambda b: b.fused_sh_tp_simple(torch.zeros(4, 3), torch.zeros(2, 3, 16),
+                                   torch.zeros(4, dtype=torch.int32)),
+    lambda b: b.edge_index_to_csr(torch.zeros(3, 4, dtype=torch.int64), 5),
+    lambda b: b.fused_message_passing(torch.zeros(2, 3, 16), torch.zeros(4, 3), torch.zeros(4, 5),
+                                      torch.zeros(3, dtype=torch.int64),
+                                      torch.zeros(4, dtype=torch.int64)),
+])
+def test_argument_errors_raise_runtime_error(bm, call):
+    with pytest.raises(RuntimeError):
+        call(bm)

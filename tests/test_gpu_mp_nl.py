@@ -1,0 +1,213 @@
+"""GPU parity: fused SH+TP(+scatter), CSR conversion and the neighbor list.
+
+Float outputs within 1e-5 normwise of the float64 oracle; neighbor lists
+bit-exact (indices and fp32 vectors) against the C restatement of the
+reference cell list after sorting by (i, j); CSR bit-exact.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import dst_sorted_edges, gen, normwise_err, periodic_box, unit_vectors
+from oracle import mp as omp
+from oracle import nl as onl
+
+pytestmark = pytest.mark.gpu
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(REPO, "batmobile-evo_amd", "lib", "libbatmobile_hip.so")
+
+
+def _random_graph(n, e, c, seed):
+    vec = unit_vectors(e, seed)
+    x = torch.randn(n, c, 16, generator=gen(seed + 1))
+    src = torch.randint(0, n, (e,), generator=gen(seed + 2))
+    dst = torch.randint(0, n, (e,), generator=gen(seed + 3))
+    return vec, x, src, dst
+
+
+@pytest.mark.parametrize("n,e,c", [(100, 1000, 16), (50, 333, 64), (20, 77, 5), (10, 64, 128), (7, 1, 1)])
+def test_fused_sh_tp_simple(bm, dev, n, e, c):
+    vec, x, src, _ = _random_graph(n, e, c, 100 + c)
+    msg = bm.fused_sh_tp_simple(vec.to(dev), x.to(dev), src.to(dev)).cpu().numpy()
+    want = omp.fused_sh_tp_simple(vec.double().numpy(), x.double().numpy(), src.numpy())
+    assert msg.shape == (e, c, 16)
+    assert normwise_err(msg, want) <= 1e-5
+
+
+def test_fused_vs_unfused_composition(bm, dev):
+    """benchmarks/benchmark_fused_sh_tp.py:114-156: fused == SH -> gather -> TP_simple."""
+    n, e, c = 300, 4000, 32
+    vec, x, src, dst = _random_graph(n, e, c, 7)
+    vec, x, src = vec.to(dev), x.to(dev), src.to(dev)
+    fused = bm.fused_sh_tp_simple(vec, x, src)
+    y = bm.spherical_harmonics(vec, 3)
+    unf = bm.tensor_product_simple(x[src].reshape(e * c, 16),
+                                   y.unsqueeze(1).expand(-1, c, -1).reshape(e * c, 16)).reshape(e, c, 16)
+    assert (fused - unf).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("n,e,c,normalize", [(500, 6000, 64, False), (200, 3000, 16, True),
+                                             (64, 500, 3, False), (33, 2000, 80, True)])
+def test_sh_tp_scatter_random_graph(bm, dev, n, e, c, normalize):
+    vec, x, src, dst = _random_graph(n, e, c, 9)
+    if normalize:
+        vec = vec * (1.0 + torch.rand(e, 1, generator=gen(5)) * 4.0)
+    order = torch.argsort(dst, stable=True)
+    rp = torch.zeros(n + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(torch.bincount(dst, minlength=n), 0)
+    # permuted edge data (perm = CSR order), as fused_message_passing_simple uses it
+    out = bm.sh_tp_scatter(vec.to(dev), x.to(dev), src.to(dev), rp.to(dev), order.to(dev), normalize)
+    want = omp.sh_tp_scatter(vec.double().numpy(), x.double().numpy(), src.numpy(), dst.numpy(), n,
+                             normalize=normalize)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    # the same edges stored in CSR order, no permutation
+    out2 = bm.sh_tp_scatter(vec[order].to(dev), x.to(dev), src[order].to(dev), rp.to(dev), None, normalize)
+    assert torch.equal(out, out2)
+
+
+def test_sh_tp_scatter_empty_rows_and_edges(bm, dev):
+    n, c = 40, 16
+    x = torch.randn(n, c, 16, generator=gen(3)).to(dev)
+    # every other destination has no edges; also a destination with 150 edges (> one batch)
+    dst = torch.cat([torch.arange(0, n, 2).repeat_interleave(3), torch.full((150,), 5)])
+    dst, _ = torch.sort(dst)
+    e = dst.numel()
+    src = torch.randint(0, n, (e,), generator=gen(4))
+    vec = unit_vectors(e, 5)
+    rp = torch.zeros(n + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(torch.bincount(dst, minlength=n), 0)
+    out = bm.sh_tp_scatter(vec.to(dev), x, src.to(dev), rp.to(dev)).cpu()
+    want = omp.sh_tp_scatter(vec.double().numpy(), x.cpu().double().numpy(), src.numpy(), dst.numpy(), n)
+    assert normwise_err(out, want) <= 1e-5
+    assert torch.count_nonzero(out[1::2]).item() == 0
+    # no edges at all -> zeros
+    z = bm.sh_tp_scatter(vec[:0].to(dev), x, src[:0].to(dev), torch.zeros(n + 1, dtype=torch.int64, device=dev))
+    assert torch.count_nonzero(z).item() == 0 and tuple(z.shape) == (n, c, 16)
+
+
+def test_edge_index_to_csr(bm, dev):
+    n, e = 1000, 30000
+    ei = torch.stack([torch.randint(0, n, (e,), generator=gen(1)), torch.randint(0, n - 10, (e,), generator=gen(2))])
+    rp, ci = bm.edge_index_to_csr(ei.to(dev), n)
+    wrp, wci = omp.edge_index_to_csr(ei.numpy(), n)
+    np.testing.assert_array_equal(rp.cpu().numpy(), wrp)
+    np.testing.assert_array_equal(ci.cpu().numpy(), wci)
+    rp0, ci0 = bm.edge_index_to_csr(ei[:, :0].to(dev), 7)
+    assert rp0.cpu().tolist() == [0] * 8 and ci0.numel() == 0
+
+
+def test_fused_message_passing_simple(bm, dev):
+    n, e, c = 400, 8000, 32
+    vec, x, src, dst = _random_graph(n, e, c, 21)
+    ei = torch.stack([src, dst]).to(dev)
+    rp, ci = bm.edge_index_to_csr(ei, n)
+    out = bm.fused_message_passing_simple(x.to(dev), vec.to(dev), ei, rp, ci).cpu()
+    want = omp.scatter_add(omp.fused_sh_tp_simple(vec.double().numpy(), x.double().numpy(), src.numpy()),
+                           dst.numpy(), n)
+    assert normwise_err(out, want) <= 1e-5
+    # and against the reference's own composition: fused_sh_tp_simple -> index_add_
+    msg = bm.fused_sh_tp_simple(vec.to(dev), x.to(dev), src.to(dev))
+    ref = torch.zeros(n, c, 16, device=dev).index_add_(0, dst.to(dev), msg).cpu()
+    assert normwise_err(out, ref.numpy()) <= 1e-5
+
+
+def test_fused_message_passing_dense_weights(bm, dev):
+    n, e, cin, cout = 120, 2000, 16, 24
+    vec = unit_vectors(e, 31)
+    x = torch.randn(n, cin, 16, generator=gen(32))
+    w = torch.randn(cin, cout, generator=gen(33)) / 4.0
+    tgt, _ = torch.sort(torch.randint(0, n, (e,), generator=gen(34)))
+    rp = torch.zeros(n + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(torch.bincount(tgt, minlength=n), 0)
+    col = torch.randint(0, n, (e,), generator=gen(35))
+    out = bm.fused_message_passing(x.to(dev), vec.to(dev), w.to(dev), rp.to(dev), col.to(dev)).cpu()
+    want = omp.fused_message_passing(x.double().numpy(), vec.double().numpy(), w.double().numpy(),
+                                     rp.numpy(), col.numpy())
+    assert normwise_err(out, want) <= 1e-5
+
+
+def _nl_gpu(bm, dev, pos, cell, cutoff=5.0, self_loops=False):
+    ei, vec, off = bm.neighbor_list(pos.to(dev), cell, cutoff, self_loops)
+    return ei.cpu().numpy(), vec.cpu().numpy(), off.cpu().numpy()
+
+
+@pytest.mark.parametrize("n", [100, 1000, 5000, 50000])
+def test_neighbor_list_bit_exact(bm, dev, n):
+    pos, cell = periodic_box(n, 3 if n == 5000 else n)
+    ei, vec, off = _nl_gpu(bm, dev, pos, cell)
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
+    np.testing.assert_array_equal(ei[0], s)
+    np.testing.assert_array_equal(ei[1], d)
+    np.testing.assert_array_equal(vec, v)      # bit-exact fp32
+    np.testing.assert_array_equal(off, np.concatenate([[0], np.cumsum(np.bincount(s, minlength=n))]))
+    if n <= 1000:
+        bs, bd, bv = onl.brute_force(pos.numpy(), cell.numpy(), 5.0)
+        np.testing.assert_array_equal(ei[0], bs)
+        np.testing.assert_array_equal(vec, bv)
+
+
+def test_neighbor_list_small_box_self_loops_and_lattice(bm, dev):
+    pos, cell = periodic_box(40, 8)           # box ~ 8.8 A: 3 bins of < r_c
+    ei, vec, _ = _nl_gpu(bm, dev, pos, cell, 5.0, True)
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0, True)
+    np.testing.assert_array_equal(ei, np.stack([s, d]))
+    np.testing.assert_array_equal(vec, v)
+    g = torch.arange(6, dtype=torch.float32) * 2.0 + 0.5
+    lat = torch.stack(torch.meshgrid(g, g, g, indexing="ij"), -1).reshape(-1, 3)
+    ei, vec, _ = _nl_gpu(bm, dev, lat, torch.diag(torch.tensor([12.0, 12.0, 12.0])), 2.0)
+    assert np.bincount(ei[0], minlength=216).tolist() == [6] * 216
+
+
+def test_neighbor_list_reference_c_abi(bm, dev):
+    """ctypes use as in reference benchmarks/benchmark_neighbor_list.py:18-47."""
+
+    class Result(ctypes.Structure):
+        _fields_ = [("edge_index", ctypes.c_void_p), ("edge_vectors", ctypes.c_void_p),
+                    ("num_edges", ctypes.c_int64), ("d_edge_index", ctypes.c_void_p),
+                    ("d_edge_vectors", ctypes.c_void_p)]
+
+    lib = ctypes.CDLL(LIB)
+    lib.neighbor_list_cuda.restype = ctypes.c_int
+    lib.neighbor_list_cuda.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
+                                       ctypes.c_bool, ctypes.POINTER(Result), ctypes.c_void_p]
+    lib.neighbor_list_free.argtypes = [ctypes.POINTER(Result)]
+    pos, cell = periodic_box(2000, 4)
+    pd, cd = pos.to(dev).contiguous(), cell.to(dev).contiguous()
+    torch.cuda.synchronize()
+    res = Result()
+    rc = lib.neighbor_list_cuda(pd.data_ptr(), cd.data_ptr(), 2000, 5.0, False, ctypes.byref(res), None)
+    assert rc == 0
+    e = res.num_edges
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
+    assert e == len(s)
+    # copy the library-owned buffers out through torch
+    ei = torch.empty(2 * e, dtype=torch.int32, device=dev)
+    vv = torch.empty(e * 3, dtype=torch.float32, device=dev)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(ei.data_ptr(), res.d_edge_index, 8 * e, 3) == 0
+    assert hip.hipMemcpy(vv.data_ptr(), res.d_edge_vectors, 12 * e, 3) == 0
+    lib.neighbor_list_free(ctypes.byref(res))
+    assert res.num_edges == 0 and not res.d_edge_index
+    ei = ei.cpu().numpy().reshape(2, e)
+    np.testing.assert_array_equal(ei[0], s)
+    np.testing.assert_array_equal(ei[1], d)
+    np.testing.assert_array_equal(vv.cpu().numpy().reshape(e, 3), v)
+
+
+def test_config4_scatter_full_size(bm, dev):
+    """configs[3] geometry: N = 5000, ~30 neighbours, C = 64, edges sorted by destination."""
+    pos, cell = periodic_box(5000, 3)
+    ei, vec, off = bm.neighbor_list(pos.to(dev), cell, 5.0, False)
+    src, dst, v = dst_sorted_edges(ei[0], ei[1], vec)
+    x = torch.randn(5000, 64, 16, generator=gen(13)).to(dev)
+    out = bm.sh_tp_scatter(v, x, src, off, None, True)
+    want = omp.sh_tp_scatter(v.cpu().double().numpy(), x.cpu().double().numpy(), src.cpu().numpy(),
+                             dst.cpu().numpy(), 5000, normalize=True)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    # deterministic: bitwise identical on a second run
+    assert torch.equal(out, bm.sh_tp_scatter(v, x, src, off, None, True))

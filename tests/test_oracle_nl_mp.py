@@ -1,0 +1,108 @@
+"""Pins the neighbor-list oracle (oracle/nl_ref.c) and the message-passing oracle."""
+import numpy as np
+import pytest
+
+from oracle import mp, nl, sh, tp
+
+RHO = 30.0 / (4.0 / 3.0 * np.pi * 5.0 ** 3)
+
+
+def _box(n, seed):
+    L = (n / RHO) ** (1.0 / 3.0)
+    pos = (np.random.default_rng(seed).random((n, 3)) * L).astype(np.float32)
+    return pos, np.diag([L, L, L]).astype(np.float32)
+
+
+@pytest.mark.parametrize("n", [10, 100, 1000])
+def test_cell_list_equals_brute_force(n):
+    pos, cell = _box(n, n)
+    a = nl.cell_list(pos, cell, 5.0)
+    b = nl.brute_force(pos, cell, 5.0)
+    for u, v in zip(a, b):
+        np.testing.assert_array_equal(u, v)
+
+
+def test_self_loops_and_symmetry():
+    pos, cell = _box(300, 1)
+    s, d, v = nl.cell_list(pos, cell, 5.0, self_loops=True)
+    assert np.sum(s == d) == 300
+    s, d, v = nl.cell_list(pos, cell, 5.0)
+    fwd = {(int(i), int(j)): v[k] for k, (i, j) in enumerate(zip(s, d))}
+    for (i, j), vec in fwd.items():
+        np.testing.assert_array_equal(fwd[(j, i)], -vec)   # exact negation
+
+
+def test_cubic_lattice_known_answer():
+    # simple cubic lattice, spacing 2.0, 6^3 sites in a 12 A box: 6 neighbours at
+    # r = 2 (inclusive cutoff), 6 + 12 at r = 2*sqrt(2) + eps
+    g = np.arange(6) * 2.0 + 0.5
+    pos = np.stack(np.meshgrid(g, g, g, indexing="ij"), -1).reshape(-1, 3).astype(np.float32)
+    cell = np.diag([12.0, 12.0, 12.0]).astype(np.float32)
+    s, _, v = nl.cell_list(pos, cell, 2.0)
+    assert np.bincount(s, minlength=216).tolist() == [6] * 216
+    np.testing.assert_allclose(np.linalg.norm(v, axis=1), 2.0)
+    s, _, _ = nl.cell_list(pos, cell, 2.0 * np.sqrt(2.0) + 1e-3)
+    assert np.bincount(s, minlength=216).tolist() == [18] * 216
+
+
+def test_fused_equals_composition():
+    rng = np.random.default_rng(0)
+    n, e, c = 40, 300, 5
+    vec = rng.normal(size=(e, 3))
+    x = rng.normal(size=(n, c, 16))
+    src = rng.integers(0, n, e)
+    dst = rng.integers(0, n, e)
+    msg = mp.fused_sh_tp_simple(vec, x, src)
+    y = sh.spherical_harmonics(vec, 3)
+    for k in range(0, e, 37):
+        np.testing.assert_allclose(msg[k], tp.tensor_product_simple(x[src[k]], np.repeat(y[k:k + 1], c, 0)),
+                                   rtol=1e-12, atol=1e-12)
+    out = mp.scatter_add(msg, dst, n)
+    np.testing.assert_allclose(mp.sh_tp_scatter(vec, x, src, dst, n), out, rtol=1e-12, atol=1e-12)
+    # CSR single-kernel semantics (fused_message_passing.cu:174-255) agree as well
+    ei = np.stack([src, dst])
+    rp, ci = mp.edge_index_to_csr(ei, n)
+    np.testing.assert_allclose(mp.fused_message_passing_simple(x, vec, ei, rp, ci), out,
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_csr_is_stable_and_complete():
+    rng = np.random.default_rng(1)
+    ei = np.stack([rng.integers(0, 20, 200), rng.integers(0, 20, 200)])
+    rp, ci = mp.edge_index_to_csr(ei, 25)
+    assert rp[0] == 0 and rp[-1] == 200 and len(rp) == 26
+    for t in range(25):
+        row = ci[rp[t]:rp[t + 1]]
+        assert (ei[1, row] == t).all() and (np.diff(row) > 0).all()
+
+
+def test_dense_weight_message_passing():
+    rng = np.random.default_rng(2)
+    n, e, ci_, co = 12, 60, 3, 4
+    vec = rng.normal(size=(e, 3))
+    x = rng.normal(size=(n, ci_, 16))
+    w = rng.normal(size=(ci_, co))
+    tgt = np.sort(rng.integers(0, n, e))
+    rp = np.concatenate([[0], np.cumsum(np.bincount(tgt, minlength=n))])
+    col = rng.integers(0, n, e)     # read as source atoms by the reference kernel
+    got = mp.fused_message_passing(x, vec, w, rp, col)
+    want = np.zeros((n, co, 16))
+    for k in range(e):
+        t = tp.tensor_product_simple(x[col[k]], np.repeat(sh.spherical_harmonics(vec[k:k + 1], 3), ci_, 0))
+        want[tgt[k]] += np.einsum("io,ic->co", t, w)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_weighted_message_passing_matches_per_edge_loop():
+    rng = np.random.default_rng(3)
+    n, e, ci_, co = 10, 40, 2, 3
+    vec = rng.normal(size=(e, 3))
+    x = rng.normal(size=(n, ci_, 16))
+    w = rng.normal(size=(34, ci_, co))
+    src, dst = rng.integers(0, n, e), rng.integers(0, n, e)
+    got = mp.weighted_message_passing(vec, x, w, src, dst, n)
+    u, _ = sh.normalize(vec)
+    want = np.zeros((n, co, 16))
+    for k in range(e):
+        want[dst[k]] += tp.tensor_product(x[src[k]][None], sh.spherical_harmonics(u[k:k + 1], 3), w)[0]
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
