@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kMpBlock, 2) void mp_simple_mfma_kernel(
                             *reinterpret_cast<const float4*>(sM + j * kMStride + i16 * 16 + 4 * g);
                         if constexpr (SCATTER) {
                             const int64_t k = kb + j;
-                            while (k >= rp_next) {
+                            while (k >= rp_next && d_cur + 1 < d1) {
                                 flush(d_cur);
                                 ++d_cur;
                                 rp_next = row_ptr[d_cur + 1];

@@ -53,7 +53,10 @@ __device__ __forceinline__ void bin_coords(float px, float py, float pz, const B
         const float fl = floorf(t) * c.box[d];
         const float wpos = p[d] - fl;
         const int v = (int)(wpos / c.bin[d]);
-        b[d] = v < c.nb[d] - 1 ? v : c.nb[d] - 1;
+        // upper clamp as the reference (neighbor_list.cu:48-50); the lower clamp only
+        // guards non-finite input (a finite wrapped position never gives v < 0)
+        const int hi = v < c.nb[d] - 1 ? v : c.nb[d] - 1;
+        b[d] = hi > 0 ? hi : 0;
     }
 }
 

@@ -117,6 +117,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before the workload, run 5 plain device copies of this many MiB "
+                         "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
@@ -127,6 +130,13 @@ def main():
 
     import batmobile as bm
     dev = torch.device("cuda:0")
+    if a.calibrate_copy_mib > 0:
+        n = a.calibrate_copy_mib * (1 << 20) // 4
+        s, d = torch.ones(n, device=dev), torch.empty(n, device=dev)
+        for _ in range(5):
+            d.copy_(s)
+        torch.cuda.synchronize()
+        del s, d
     w = make_workload(torch, bm, dev)
     E = int(w["src"].numel())
 

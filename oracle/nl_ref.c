@@ -52,7 +52,8 @@ static void bin_coords(const float* p, const Cfg* c, int* out) {
         float t = p[d] * c->inv[d];
         float w = p[d] - floorf(t) * c->box[d];
         int b = (int)(w / c->bin[d]);
-        out[d] = b < c->nb[d] - 1 ? b : c->nb[d] - 1;
+        int hi = b < c->nb[d] - 1 ? b : c->nb[d] - 1;
+        out[d] = hi > 0 ? hi : 0;  /* lower clamp: the kernel's guard for non-finite input */
     }
 }
 

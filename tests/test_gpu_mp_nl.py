@@ -72,8 +72,8 @@ def test_sh_tp_scatter_random_graph(bm, dev, n, e, c, normalize):
 def test_sh_tp_scatter_empty_rows_and_edges(bm, dev):
     n, c = 40, 16
     x = torch.randn(n, c, 16, generator=gen(3)).to(dev)
-    # every other destination has no edges; also a destination with 150 edges (> one batch)
-    dst = torch.cat([torch.arange(0, n, 2).repeat_interleave(3), torch.full((150,), 5)])
+    # odd destinations have no edges; destination 6 has 153 edges (> one 64-edge batch)
+    dst = torch.cat([torch.arange(0, n, 2).repeat_interleave(3), torch.full((150,), 6)])
     dst, _ = torch.sort(dst)
     e = dst.numel()
     src = torch.randint(0, n, (e,), generator=gen(4))
