@@ -398,7 +398,8 @@ torch::Tensor fused_sh_tp_simple(const torch::Tensor& edge_vectors,
     check_status(batteries_fused_sh_tp_simple(cptr<float>(edge_vectors, "edge_vectors"),
                                               cptr<float>(x, "node_features"),
                                               cptr<int64_t>(source_idx, "source_idx"),
-                                              mptr<float>(msg, "messages"), E, (int)C, 0,
+                                              mptr<float>(msg, "messages"), node_features.size(0),
+                                              E, (int)C, 0,
                                               current_stream(node_features)),
                  "fused_sh_tp_simple");
     return msg;
@@ -434,9 +435,112 @@ torch::Tensor sh_tp_scatter(const torch::Tensor& edge_vectors, const torch::Tens
                                              cptr<float>(x, "node_features"),
                                              cptr<int64_t>(source_idx, "source_idx"), pp,
                                              cptr<int64_t>(row_ptr, "row_ptr"),
-                                             mptr<float>(out, "output"), N_dst, E, (int)C,
-                                             normalize ? 1 : 0, current_stream(node_features)),
+                                             mptr<float>(out, "output"), node_features.size(0),
+                                             N_dst, E, (int)C, normalize ? 1 : 0,
+                                             current_stream(node_features)),
                  "sh_tp_scatter");
+    return out;
+}
+
+// Extension: atoms in Morton order of a 32^3 grid over the (orthorhombic) box.
+torch::Tensor spatial_order(const torch::Tensor& positions, const torch::Tensor& cell) {
+    TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
+    TORCH_CHECK(positions.dtype() == torch::kFloat32, "positions must be float32");
+    TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
+    check_device(positions, "positions");
+    const int64_t N = positions.size(0);
+    torch::Tensor cell_cpu = cell.detach().to(torch::kCPU, torch::kFloat32).contiguous();
+    const float* h = cell_cpu.data_ptr<float>();
+    const float box[3] = {h[0], h[4], h[8]};
+    auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(positions.device());
+    torch::Tensor order = torch::empty({N}, i64);
+    if (N == 0) return order;
+    const c10::DeviceGuard guard(positions.device());
+    const size_t wsb = batteries_spatial_order_workspace_bytes(N);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
+    check_status(batteries_spatial_order(cptr<float>(positions, "positions"), box, N,
+                                         ws.data_ptr(), wsb, order.data_ptr<int64_t>(),
+                                         current_stream(positions)),
+                 "spatial_order");
+    return order;
+}
+
+// Extension: processing schedule of the fused scatter for a CSR graph
+// (row_ptr over destinations, optional col_perm as in fused_message_passing_simple)
+// and a destination order.  Returns (row_ptr_s, edge_perm, row_dst, n_blocks,
+// rows_per_block) for sh_tp_scatter_scheduled.
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t> mp_schedule(
+    const torch::Tensor& row_ptr, const torch::Tensor& order, int64_t C,
+    const c10::optional<torch::Tensor>& col_perm) {
+    TORCH_CHECK(row_ptr.dim() == 1 && row_ptr.dtype() == torch::kInt64 && row_ptr.numel() >= 1,
+                "row_ptr must be int64 [N_dst + 1]");
+    const int64_t N = row_ptr.numel() - 1;
+    TORCH_CHECK(order.dim() == 1 && order.dtype() == torch::kInt64 && order.numel() == N,
+                "order must be int64 [N_dst]");
+    TORCH_CHECK(C > 0, "C must be positive");
+    check_device(row_ptr, "row_ptr");
+    check_device(order, "order");
+    int nb = 0, rpb = 0;
+    check_status(batteries_mp_schedule_shape(N, (int)C, &nb, &rpb), "mp_schedule");
+    const int64_t E = row_ptr[N].item<int64_t>();
+    const int64_t* cp = nullptr;
+    if (col_perm.has_value() && col_perm->defined()) {
+        TORCH_CHECK(col_perm->dtype() == torch::kInt64 && col_perm->numel() == E,
+                    "col_perm must be int64 [N_edges]");
+        cp = cptr<int64_t>(*col_perm, "col_perm");
+    }
+    auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(row_ptr.device());
+    const int64_t ns = (int64_t)nb * rpb;
+    torch::Tensor rps = torch::empty({ns + 1}, i64);
+    torch::Tensor dst = torch::empty({ns}, i64);
+    torch::Tensor ep = torch::empty({E}, i64);
+    const c10::DeviceGuard guard(row_ptr.device());
+    const size_t wsb = batteries_mp_schedule_workspace_bytes(nb, rpb);
+    torch::Tensor ws = torch::empty({ns}, i64);
+    check_status(batteries_mp_schedule(cptr<int64_t>(row_ptr, "row_ptr"), cp,
+                                       cptr<int64_t>(order, "order"), N, E, (int)C, nb, rpb,
+                                       rps.data_ptr<int64_t>(), dst.data_ptr<int64_t>(),
+                                       ep.data_ptr<int64_t>(), ws.data_ptr(), wsb,
+                                       current_stream(row_ptr)),
+                 "mp_schedule");
+    return {rps, ep, dst, (int64_t)nb, (int64_t)rpb};
+}
+
+// Extension: sh_tp_scatter driven by an mp_schedule (same result, spatial order).
+torch::Tensor sh_tp_scatter_scheduled(const torch::Tensor& edge_vectors,
+                                      const torch::Tensor& node_features,
+                                      const torch::Tensor& source_idx,
+                                      const torch::Tensor& row_ptr_s,
+                                      const torch::Tensor& edge_perm, const torch::Tensor& row_dst,
+                                      int64_t n_blocks, int64_t rows_per_block, int64_t N_dst,
+                                      bool normalize) {
+    check_vectors(edge_vectors);
+    check_features(node_features, "node_features");
+    const int64_t E = edge_vectors.size(0);
+    const int64_t C = node_features.size(1);
+    TORCH_CHECK(source_idx.dtype() == torch::kInt64 && source_idx.numel() == E,
+                "source_idx must be int64 [N_edges]");
+    TORCH_CHECK(edge_perm.dtype() == torch::kInt64 && edge_perm.numel() == E,
+                "edge_perm must be int64 [N_edges]");
+    TORCH_CHECK(n_blocks > 0 && n_blocks % 8 == 0 && rows_per_block > 0, "invalid schedule shape");
+    const int64_t ns = n_blocks * rows_per_block;
+    TORCH_CHECK(row_ptr_s.dtype() == torch::kInt64 && row_ptr_s.numel() == ns + 1,
+                "row_ptr_s must be int64 [n_blocks * rows_per_block + 1]");
+    TORCH_CHECK(row_dst.dtype() == torch::kInt64 && row_dst.numel() == ns,
+                "row_dst must be int64 [n_blocks * rows_per_block]");
+    TORCH_CHECK(N_dst >= 0 && N_dst <= ns, "N_dst out of range");
+    torch::Tensor out = torch::empty({N_dst, C, 16}, f32_like(node_features));
+    if (N_dst == 0) return out;
+    const c10::DeviceGuard guard(node_features.device());
+    torch::Tensor x = aligned16(node_features);
+    check_status(batteries_sh_tp_scatter_scheduled(
+                     cptr<float>(edge_vectors, "edge_vectors"), cptr<float>(x, "node_features"),
+                     cptr<int64_t>(source_idx, "source_idx"), cptr<int64_t>(row_ptr_s, "row_ptr_s"),
+                     cptr<int64_t>(edge_perm, "edge_perm"), cptr<int64_t>(row_dst, "row_dst"),
+                     (int)n_blocks, (int)rows_per_block, mptr<float>(out, "output"),
+                     node_features.size(0), E, (int)C, normalize ? 1 : 0,
+                     current_stream(node_features)),
+                 "sh_tp_scatter_scheduled");
     return out;
 }
 
@@ -545,6 +649,17 @@ PYBIND11_MODULE(_batmobile, m) {
     m.def("neighbor_list", &neighbor_list, py::arg("positions"), py::arg("cell"),
           py::arg("cutoff"), py::arg("self_loops") = false,
           "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], row_offsets)");
+    m.def("spatial_order", &spatial_order, py::arg("positions"), py::arg("cell"),
+          "Atoms sorted by the Morton code of their cell (32^3 grid over the box)");
+    m.def("mp_schedule", &mp_schedule, py::arg("row_ptr"), py::arg("order"), py::arg("C"),
+          py::arg("col_perm") = py::none(),
+          "Spatial processing schedule for sh_tp_scatter_scheduled: "
+          "(row_ptr_s, edge_perm, row_dst, n_blocks, rows_per_block)");
+    m.def("sh_tp_scatter_scheduled", &sh_tp_scatter_scheduled, py::arg("edge_vectors"),
+          py::arg("node_features"), py::arg("source_idx"), py::arg("row_ptr_s"),
+          py::arg("edge_perm"), py::arg("row_dst"), py::arg("n_blocks"),
+          py::arg("rows_per_block"), py::arg("N_dst"), py::arg("normalize") = false,
+          "sh_tp_scatter processed in the order of an mp_schedule (same result)");
     m.def("selftest_mfma_16x16x4", &selftest_mfma_16x16x4, py::arg("A"), py::arg("B"),
           "D = A @ B through one v_mfma_f32_16x16x4f32 (lane-layout self test)");
 }

@@ -28,6 +28,8 @@ constexpr int kMpBlock = 256;
 constexpr int kBatch = 64;        // edges per LDS batch
 constexpr int kMStride = 260;     // floats per edge operator in LDS (256 + pad)
 constexpr int kChanGroup = 64;    // channels per workgroup (4 waves x 16)
+constexpr int kPrefetch = 16;     // source-row gathers in flight per lane
+constexpr int kMaxRowsPerBlock = 64;    // destinations per workgroup (row_ptr slice in LDS)
 
 // Phase 1: lane j of wave w builds rows 4w..4w+3 of M for edge j of the batch.
 template <int W>
@@ -44,17 +46,36 @@ __device__ __forceinline__ void build_rows(const float* Y, float* sMj) {
     });
 }
 
-template <bool NORM>
-__device__ __forceinline__ void phase1_build(const float* __restrict__ vec,
+// One edge of a batch as seen by the lane that owns it in phase 1.
+struct EdgeRec {
+    float x, y, z;
+    int src;  // source row (node counts are < 2^31)
+};
+
+__device__ __forceinline__ EdgeRec load_edge(const float* __restrict__ vec,
                                              const int64_t* __restrict__ perm,
-                                             const int64_t* __restrict__ src_idx, int64_t k0,
-                                             int nb, float* sM, int64_t* sSrc) {
+                                             const int64_t* __restrict__ src_idx, int64_t k,
+                                             int64_t e1) {
+    EdgeRec r{0.f, 0.f, 0.f, 0};
+    if (k < e1) {
+        const int64_t e = perm ? perm[k] : k;
+        r.x = vec[e * 3 + 0];
+        r.y = vec[e * 3 + 1];
+        r.z = vec[e * 3 + 2];
+        r.src = (int)src_idx[e];
+    }
+    return r;
+}
+
+// Phase 1 of a batch: lane j < nb of wave w builds rows 4w..4w+3 of the
+// operator of its edge into sM (no global memory access: the edge was loaded
+// into registers during the previous batch).
+template <bool NORM>
+__device__ __forceinline__ void phase1_build(EdgeRec r, int nb, float* sM) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     if (lane < nb) {
-        const int64_t k = k0 + lane;
-        const int64_t e = perm ? perm[k] : k;
-        float x = vec[e * 3 + 0], y = vec[e * 3 + 1], z = vec[e * 3 + 2];
+        float x = r.x, y = r.y, z = r.z;
         if constexpr (NORM) normalize3(x, y, z);
         float Y[16];
         sh_forward<3>(x, y, z, Y);
@@ -65,7 +86,6 @@ __device__ __forceinline__ void phase1_build(const float* __restrict__ vec,
             case 2: build_rows<2>(Y, sMj); break;
             default: build_rows<3>(Y, sMj); break;
         }
-        if (w == 0) sSrc[lane] = src_idx[e];
     }
 }
 
@@ -77,24 +97,71 @@ __device__ __forceinline__ v4f mfma4(const float4 m, const float4 xv, v4f acc) {
     return acc;
 }
 
-// One lane's slice of source row src: X[src, c, 4g .. 4g+3]; zero when c >= C.
-__device__ __forceinline__ float4 load_x(const float* __restrict__ X, int64_t src, int c, int C,
-                                         int g) {
-    if (c < C) return *reinterpret_cast<const float4*>(X + (src * C + c) * 16 + 4 * g);
-    return make_float4(0.f, 0.f, 0.f, 0.f);
+// Gather of one lane's float4 of source row `src` at byte offset `voff` inside
+// the row.  BUF: raw buffer load with the row offset in a scalar register (X
+// below 4 GiB); otherwise a 64-bit global load.
+constexpr int kBufferDword3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3
+
+template <bool BUF>
+__device__ __forceinline__ float4 gather(const float* __restrict__ X, __amdgpu_buffer_rsrc_t rsrc,
+                                         int voff, int src, uint32_t row_bytes) {
+    if constexpr (BUF) {
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        const v4i r = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, (int)((uint32_t)src * row_bytes), 0);
+        return make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                           __int_as_float(r.w));
+    } else {
+        return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(X) +
+                                                (int64_t)src * row_bytes + voff);
+    }
 }
 
-constexpr int kPrefetch = 4;
+// Is k the first edge of one of the rows described by sRow[0..n] (k < sRow[n])?
+__device__ __forceinline__ bool row_starts_at(const int64_t* sRow, int n, int64_t k) {
+    int lo = 0, hi = n;  // first index with sRow[idx] >= k
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sRow[mid] < k) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo < n && sRow[lo] == k;
+}
 
-// SCATTER: out[d, c, :] = sum over the CSR row of d.  MESSAGES: out[e, c, :] per edge.
-template <bool SCATTER, bool NORM>
-__global__ __launch_bounds__(kMpBlock, 2) void mp_simple_mfma_kernel(
+// Is k1 the end (exclusive) of one of the rows described by sRow[0..n]?
+__device__ __forceinline__ bool row_ends_at(const int64_t* sRow, int n, int64_t k1) {
+    int lo = 0, hi = n + 1;  // first index with sRow[idx] >= k1
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sRow[mid] < k1) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo <= n && sRow[lo] == k1;
+}
+
+// SCATTER: out[d, c, :] = sum over the CSR row of d, for the items_per_block
+// (scheduled) rows of this workgroup.  MESSAGES: out[e, c, :] per edge, for the
+// items_per_block (a multiple of kBatch) edges of this workgroup.
+//
+// Phase 2 walks the batch edge by edge with wave-uniform control only:
+//   - the operator fragment of edge j+1 is read from LDS while edge j's four
+//     MFMAs run;
+//   - source rows come through a register ring of kPrefetch float4 per lane:
+//     slot u holds the edge at distance u (mod kPrefetch) from the batch start,
+//     and loads for the next batch's first edges are issued in this batch, so
+//     kPrefetch gathers stay in flight across batch boundaries;
+//   - row ends inside the batch are a 64-bit mask (ballot in phase 1): the
+//     per-edge test is one scalar bit test; flushing is the rare path.
+template <bool SCATTER, bool NORM, bool BUF>
+__global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
     const float* __restrict__ vec, const float* __restrict__ X, const int64_t* __restrict__ src_idx,
     const int64_t* __restrict__ perm, const int64_t* __restrict__ row_ptr,
-    float* __restrict__ out, int64_t n_items, int64_t n_edges, int C, int items_per_block,
-    int n_logical) {
+    const int64_t* __restrict__ row_dst, float* __restrict__ out, int64_t n_items,
+    int64_t n_edges, int C, int items_per_block, int n_logical, uint32_t x_bytes) {
+    static_assert(kBatch % kPrefetch == 0, "batch must be a multiple of the prefetch depth");
+    static_assert(kBatch == 64, "one edge per lane in phase 1");
     __shared__ __attribute__((aligned(16))) float sM[kBatch * kMStride];
-    __shared__ int64_t sSrc[kBatch];
+    __shared__ int64_t sRow[kMaxRowsPerBlock + 1];
+    __shared__ int64_t sDst[kMaxRowsPerBlock];
 
     // XCD-aware mapping: consecutive logical blocks land on the same XCD.
     const int per_xcd = (n_logical + 7) / 8;
@@ -107,71 +174,295 @@ __global__ __launch_bounds__(kMpBlock, 2) void mp_simple_mfma_kernel(
     const int i16 = lane & 15;    // channel within the tile / operator row
     const int c = blockIdx.y * kChanGroup + w * 16 + i16;
     const bool tile_live = blockIdx.y * kChanGroup + w * 16 < C;
+    const uint32_t row_bytes = (uint32_t)C * 64u;
+    // lanes past the last channel read a valid channel; their output column is never stored
+    const int voff = (c < C ? c : C - 1) * 64 + g * 16;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), (short)0, BUF ? (int)x_bytes : 0, kBufferDword3);
 
     int64_t e0, e1, d0 = 0, d1 = 0;
+    int nrows = 0;
     if constexpr (SCATTER) {
         d0 = (int64_t)logical * items_per_block;
         d1 = min<int64_t>(n_items, d0 + items_per_block);
-        e0 = row_ptr[d0];
-        e1 = row_ptr[d1];
+        nrows = (int)(d1 - d0);
+        for (int i = threadIdx.x; i <= nrows; i += kMpBlock) {
+            sRow[i] = row_ptr[d0 + i];
+            if (i < nrows) sDst[i] = row_dst ? row_dst[d0 + i] : d0 + i;
+        }
+        __syncthreads();
+        e0 = sRow[0];
+        e1 = sRow[nrows];
     } else {
-        e0 = (int64_t)logical * kBatch;
-        e1 = min<int64_t>(n_edges, e0 + kBatch);
+        e0 = (int64_t)logical * items_per_block;
+        e1 = min<int64_t>(n_edges, e0 + items_per_block);
     }
 
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    int64_t d_cur = d0;
-    int64_t rp_next = SCATTER ? row_ptr[d0 + 1] : 0;
+    const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+    v4f acc = zero4;
+    int d_cur = 0;  // current row, relative to d0
 
-    auto flush = [&](int64_t row) {
-        if (c < C) {
-            float4* o = reinterpret_cast<float4*>(out + (row * C + c) * 16 + 4 * g);
-            *o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    auto store_v = [&](int64_t orow, const v4f& v) {
+        if (c < C && orow >= 0)
+            *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) =
+                make_float4(v[0], v[1], v[2], v[3]);
+    };
+    // zeros for the empty rows starting at d_cur
+    auto skip_empty = [&]() {
+        while (d_cur < nrows && sRow[d_cur + 1] == sRow[d_cur]) {
+            store_v(sDst[d_cur], zero4);
+            ++d_cur;
         }
-        acc = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    if constexpr (SCATTER) {
+        if (tile_live) skip_empty();
+    }
+    // One edge: four MFMAs into the row accumulator (started from zero on the
+    // first edge of a row, so the accumulator is never written outside MFMAs),
+    // then the row's store when the edge ends it.
+    auto edge = [&](int j, int64_t kb, const float4& m, const float4& xv, uint64_t starts,
+                    uint64_t ends) {
+        if constexpr (SCATTER) {
+            if ((starts >> j) & 1ull) acc = mfma4(m, xv, zero4);
+            else acc = mfma4(m, xv, acc);
+            if ((ends >> j) & 1ull) {
+                store_v(sDst[d_cur], acc);
+                ++d_cur;
+                skip_empty();
+            }
+        } else {
+            store_v(kb + j, mfma4(m, xv, zero4));
+        }
     };
 
+    EdgeRec cur = load_edge(vec, perm, src_idx, e0 + lane, e1);
+    float4 ring[kPrefetch];
+    bool first = true;
     for (int64_t kb = e0; kb < e1; kb += kBatch) {
         const int nb = (int)min<int64_t>(kBatch, e1 - kb);
+        const int lim = (int)min<int64_t>(e1 - kb, 4 * kBatch);  // prefetch bound, batch-relative
         __syncthreads();
-        phase1_build<NORM>(vec, perm, src_idx, kb, nb, sM, sSrc);
+        phase1_build<NORM>(cur, nb, sM);
+        uint64_t starts = 0, ends = 0;
+        if constexpr (SCATTER) {
+            starts = __ballot(lane < nb && row_starts_at(sRow, nrows, kb + lane));
+            ends = __ballot(lane < nb && row_ends_at(sRow, nrows, kb + lane + 1));
+        }
         __syncthreads();
+        // the next batch's edges, in flight during this batch's phase 2
+        const EdgeRec nxt = load_edge(vec, perm, src_idx, kb + kBatch + lane, e1);
         if (tile_live) {
-            float4 xb[kPrefetch];
+            if (first) {
 #pragma unroll
-            for (int u = 0; u < kPrefetch; ++u)
-                xb[u] = (u < nb) ? load_x(X, sSrc[u], c, C, g) : make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int jj = 0; jj < nb; jj += kPrefetch) {
+                for (int u = 0; u < kPrefetch; ++u)
+                    if (u < nb)
+                        ring[u] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, u),
+                                              row_bytes);
+                first = false;
+            }
+            const float* mrow = sM + i16 * 16 + 4 * g;
+            float4 mr[2];
+            mr[0] = *reinterpret_cast<const float4*>(mrow);
+            if (lim >= kBatch + kPrefetch) {
+                // full batch whose prefetch targets all exist: fully unrolled, no checks
+                static_for<kBatch>([&](auto jj) {
+                    constexpr int j = decltype(jj)::value;
+                    constexpr int u = j % kPrefetch;
+                    if constexpr (j + 1 < kBatch)
+                        mr[(j + 1) & 1] = *reinterpret_cast<const float4*>(mrow + (j + 1) * kMStride);
+                    edge(j, kb, mr[j & 1], ring[u], starts, ends);
+                    constexpr int jn = j + kPrefetch;
+                    const int s = jn < kBatch ? __builtin_amdgcn_readlane(cur.src, jn)
+                                              : __builtin_amdgcn_readlane(nxt.src, jn - kBatch);
+                    ring[u] = gather<BUF>(X, xr, voff, s, row_bytes);
+                });
+            } else {
+                for (int jj = 0; jj < nb; jj += kPrefetch) {
 #pragma unroll
-                for (int u = 0; u < kPrefetch; ++u) {
-                    const int j = jj + u;
-                    if (j < nb) {
-                        const float4 xv = xb[u];
-                        if (j + kPrefetch < nb) xb[u] = load_x(X, sSrc[j + kPrefetch], c, C, g);
-                        const float4 m =
-                            *reinterpret_cast<const float4*>(sM + j * kMStride + i16 * 16 + 4 * g);
-                        if constexpr (SCATTER) {
-                            const int64_t k = kb + j;
-                            while (k >= rp_next && d_cur + 1 < d1) {
-                                flush(d_cur);
-                                ++d_cur;
-                                rp_next = row_ptr[d_cur + 1];
+                    for (int u = 0; u < kPrefetch; ++u) {
+                        const int j = jj + u;
+                        if (j < nb) {
+                            if (j + 1 < nb)
+                                mr[(u + 1) & 1] =
+                                    *reinterpret_cast<const float4*>(mrow + (j + 1) * kMStride);
+                            edge(j, kb, mr[u & 1], ring[u], starts, ends);
+                            const int jn = j + kPrefetch;
+                            if (jn < lim) {
+                                const int s = jn < nb ? __builtin_amdgcn_readlane(cur.src, jn)
+                                                      : __builtin_amdgcn_readlane(nxt.src, jn - nb);
+                                ring[u] = gather<BUF>(X, xr, voff, s, row_bytes);
                             }
-                            acc = mfma4(m, xv, acc);
-                        } else {
-                            acc = mfma4(m, xv, v4f{0.f, 0.f, 0.f, 0.f});
-                            flush(kb + j);
                         }
                     }
                 }
             }
         }
+        cur = nxt;
     }
     if constexpr (SCATTER) {
-        if (tile_live) {
-            while (d_cur < d1) {
-                flush(d_cur);
+        if (tile_live)
+            while (d_cur < nrows) {
+                store_v(sDst[d_cur], zero4);
                 ++d_cur;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Scatter kernel: out[d, c, :] = sum over the CSR row of d, for the
+// rows_per_block (<= kScatterRows, scheduled) rows of this workgroup.
+//
+// Same operator/MFMA scheme as above, arranged so that the compiler can keep
+// kRing gathers in flight: on gfx9 loads and stores share one counter and may
+// complete out of order, so a store between a gather and its use -- or a gather
+// issued under a data-dependent condition -- makes the compiler drain every
+// outstanding gather before the next MFMA.  Hence the edge loop has neither:
+//   - every batch is kSBatch edges fully unrolled, and every edge issues the
+//     gather for the edge kRing = kSBatch positions ahead (past the block's last
+//     edge it gathers row 0 of the same tensor, a valid address whose value is
+//     never used: edges past the end only touch the accumulator after the
+//     block's last row has been staged);
+//   - a finished row is staged in LDS (the workgroup owns at most kScatterRows
+//     rows) and all rows are written to HBM once, after the last batch.
+// Row boundaries are per-batch 64-bit masks built with ballots in phase 1:
+// `starts` selects a zero C operand for the first MFMA of a row (the
+// accumulator is never written outside MFMAs), `ends` triggers the staging.
+// ---------------------------------------------------------------------------
+constexpr int kSBatch = 32;       // edges per batch (operators in LDS)
+constexpr int kRing = kSBatch;    // gathers in flight per lane
+constexpr int kScatterRows = 10;  // rows per workgroup (all staged in LDS)
+
+template <bool NORM, bool BUF, bool PERM>
+__global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
+    const float* __restrict__ vec, const float* __restrict__ X, const int64_t* __restrict__ src_idx,
+    const int64_t* __restrict__ perm, const int64_t* __restrict__ row_ptr,
+    const int64_t* __restrict__ row_dst, float* __restrict__ out, int64_t n_rows, int C,
+    int rows_per_block, int n_logical, uint32_t x_bytes) {
+    static_assert(kSBatch % 2 == 0 && kSBatch <= 64, "one edge per lane in phase 1");
+    __shared__ __attribute__((aligned(16))) float sM[kSBatch * kMStride];
+    __shared__ float4 sStage[4][kScatterRows][64];
+    __shared__ int64_t sRow[kScatterRows + 1];
+    __shared__ int64_t sDst[kScatterRows];
+
+    const int per_xcd = (n_logical + 7) / 8;
+    const int logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (logical >= n_logical) return;
+
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
+    const int c = blockIdx.y * kChanGroup + w * 16 + i16;
+    const bool tile_live = blockIdx.y * kChanGroup + w * 16 < C;
+    const uint32_t row_bytes = (uint32_t)C * 64u;
+    const int voff = (c < C ? c : C - 1) * 64 + g * 16;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), (short)0, BUF ? (int)x_bytes : 0, kBufferDword3);
+
+    const int64_t d0 = (int64_t)logical * rows_per_block;
+    const int nrows = (int)(min<int64_t>(n_rows, d0 + rows_per_block) - d0);
+    for (int i = threadIdx.x; i <= nrows; i += kMpBlock) {
+        sRow[i] = row_ptr[d0 + i];
+        if (i < nrows) sDst[i] = row_dst ? row_dst[d0 + i] : d0 + i;
+    }
+    __syncthreads();
+    const int64_t e0 = sRow[0], e1 = sRow[nrows];
+
+    // Edge records move through a three-stage pipeline so that no wait is on a
+    // load younger than the gathers in flight: the edge id of batch b+3 (one
+    // load when PERM) and the record of batch b+2 are issued during batch b; the
+    // record of batch b+1 (its source rows feed this batch's gathers) and of
+    // batch b (phase 1) were issued one and two batches earlier.
+    auto edge_id = [&](int64_t kbatch) -> int64_t {
+        const int64_t k = kbatch + lane;
+        if (lane >= kSBatch || k >= e1) return -1;
+        if constexpr (PERM) return perm[k];
+        else return k;
+    };
+    auto record = [&](int64_t e) {
+        EdgeRec r{0.f, 0.f, 0.f, 0};
+        if (e >= 0) {
+            r.x = vec[e * 3 + 0];
+            r.y = vec[e * 3 + 1];
+            r.z = vec[e * 3 + 2];
+            r.src = (int)src_idx[e];
+        }
+        return r;
+    };
+
+    const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+    v4f acc = zero4;
+
+    EdgeRec cur = record(edge_id(e0));
+    EdgeRec nxt = record(edge_id(e0 + kSBatch));
+    int64_t id2 = edge_id(e0 + 2 * kSBatch);
+    // Every wave runs the edge loop, also one whose 16 channels are all past C
+    // (its lanes read channel C-1 and never store): a branch around the loop
+    // would make the loop-carried records look like the youngest loads on one
+    // path, and the compiler would drain every gather at the loop latch.
+    // (The guard encloses the ring fill and the loop together for the same
+    // reason: the loop header is reached only after the ring fill.)
+    float4 ring[kRing];
+    if (e0 < e1) {
+    static_for<kRing>([&](auto uu) {
+        constexpr int u = decltype(uu)::value;
+        ring[u] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, u), row_bytes);
+    });
+    for (int64_t kb = e0; kb < e1; kb += kSBatch) {
+        const int nb = (int)min<int64_t>(kSBatch, e1 - kb);
+        __syncthreads();
+        phase1_build<NORM>(cur, nb, sM);
+        // row of each edge of the batch (for staging) and the batch's row boundaries
+        int my_row = 0;
+        bool is_start = false, is_end = false;
+        if (lane < nb) {
+            const int64_t k = kb + lane;
+            int lo = 0, hi = nrows;  // last row with sRow[row] <= k
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (sRow[mid] <= k) lo = mid;
+                else hi = mid - 1;
+            }
+            my_row = lo;
+            is_start = sRow[lo] == k;
+            is_end = sRow[lo + 1] == k + 1;
+        }
+        const uint64_t starts = __ballot(is_start);
+        const uint64_t ends = __ballot(is_end);
+        __syncthreads();
+        const EdgeRec nn = record(id2);
+        id2 = edge_id(kb + 3 * kSBatch);
+        // keep these loads ahead of the gathers: sunk below them, they would be
+        // the youngest loads when the next batch needs them
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const float* mrow = sM + i16 * 16 + 4 * g;
+            float4 mr[2];
+            mr[0] = *reinterpret_cast<const float4*>(mrow);
+            static_for<kSBatch>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
+                if constexpr (j + 1 < kSBatch)
+                    mr[(j + 1) & 1] = *reinterpret_cast<const float4*>(mrow + (j + 1) * kMStride);
+                if ((starts >> j) & 1ull) acc = mfma4(mr[j & 1], ring[j], zero4);
+                else acc = mfma4(mr[j & 1], ring[j], acc);
+                ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, j), row_bytes);
+                if ((ends >> j) & 1ull) {
+                    const int r = __builtin_amdgcn_readlane(my_row, j);
+                    sStage[w][r][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                }
+            });
+        }
+        cur = nxt;
+        nxt = nn;
+    }
+    }
+    if (tile_live) {
+        for (int r = 0; r < nrows; ++r) {
+            const int64_t orow = sDst[r];
+            if (c < C && orow >= 0) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (sRow[r + 1] > sRow[r]) v = sStage[w][r][lane];
+                *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
             }
         }
     }
@@ -270,57 +561,113 @@ extern "C" int batteries_selftest_mfma_16x16x4(const float* A, const float* B, f
     return (int)hipGetLastError();
 }
 
-static int launch_mp_simple(bool scatter, bool norm, const float* vec, const float* X,
-                            const int64_t* src_idx, const int64_t* perm, const int64_t* row_ptr,
-                            float* out, int64_t n_items, int64_t n_edges, int C,
-                            int items_per_block, hipStream_t s) {
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Workgroups per XCD resident at once: 2 per compute unit (the LDS of one
+// workgroup is under 80 KB of the 160 KB), spread over the channel groups.
+static int blocks_per_xcd(int C) {
+    const int groups = (int)ceil_div(C, kChanGroup);
+    return std::max(1, 2 * device_cu_count() / groups / 8);
+}
+
+// Launch with an explicit split: n_logical workgroups (a multiple of 8), each
+// owning `per` consecutive destinations (SCATTER) or edges (MESSAGES).
+static int launch_mp(bool scatter, bool norm, const float* vec, const float* X, int64_t n_src,
+                     const int64_t* src_idx, const int64_t* perm, const int64_t* row_ptr,
+                     const int64_t* row_dst, float* out, int64_t n_items, int64_t n_edges, int C,
+                     int64_t per, int64_t n_logical, hipStream_t s) {
     if (C <= 0) return BM_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(out)) & 15) return BM_ERR_ARG;
-    int n_logical;
-    if (scatter) {
-        if (items_per_block <= 0) items_per_block = 1;
-        n_logical = (int)ceil_div(n_items, items_per_block);
-    } else {
-        n_logical = (int)ceil_div(n_edges, kBatch);
-    }
     if (n_logical == 0) return BM_OK;
-    const int per_xcd = (n_logical + 7) / 8;
-    dim3 grid((unsigned)(per_xcd * 8), (unsigned)ceil_div(C, kChanGroup));
-#define BM_LAUNCH(SC, NO)                                                                      \
-    mp_simple_mfma_kernel<SC, NO><<<grid, kMpBlock, 0, s>>>(vec, X, src_idx, perm, row_ptr, out, \
-                                                            n_items, n_edges, C,               \
-                                                            items_per_block, n_logical)
+    if (per <= 0 || per > INT32_MAX || n_logical > INT32_MAX / 8) return BM_ERR_ARG;
+    if (scatter && per > kScatterRows) return BM_ERR_ARG;
+    if (n_src <= 0 || n_src > INT32_MAX) return BM_ERR_ARG;
+    const int groups = (int)ceil_div(C, kChanGroup);
+    const int64_t per_xcd = (n_logical + 7) / 8;
+    dim3 grid((unsigned)(per_xcd * 8), (unsigned)groups);
+    const int64_t xb = n_src * (int64_t)C * 64;
+    const bool buf = xb <= (int64_t)INT32_MAX;
+    const uint32_t x_bytes = buf ? (uint32_t)xb : 0u;
+#define BM_LAUNCH(NO, BU)                                                                    \
+    mp_simple_mfma_kernel<false, NO, BU><<<grid, kMpBlock, 0, s>>>(                           \
+        vec, X, src_idx, perm, row_ptr, row_dst, out, n_items, n_edges, C, (int)per,          \
+        (int)n_logical, x_bytes)
+#define BM_LAUNCH_SC(NO, BU, PE)                                                             \
+    mp_scatter_kernel<NO, BU, PE><<<grid, kMpBlock, 0, s>>>(vec, X, src_idx, perm, row_ptr,   \
+                                                            row_dst, out, n_items, C,         \
+                                                            (int)per, (int)n_logical, x_bytes)
+#define BM_LAUNCH_SC2(NO, BU) \
+    do { if (perm) BM_LAUNCH_SC(NO, BU, true); else BM_LAUNCH_SC(NO, BU, false); } while (0)
     if (scatter) {
-        if (norm) BM_LAUNCH(true, true); else BM_LAUNCH(true, false);
+        if (norm) {
+            if (buf) BM_LAUNCH_SC2(true, true); else BM_LAUNCH_SC2(true, false);
+        } else {
+            if (buf) BM_LAUNCH_SC2(false, true); else BM_LAUNCH_SC2(false, false);
+        }
     } else {
-        if (norm) BM_LAUNCH(false, true); else BM_LAUNCH(false, false);
+        if (norm) {
+            if (buf) BM_LAUNCH(true, true); else BM_LAUNCH(true, false);
+        } else {
+            if (buf) BM_LAUNCH(false, true); else BM_LAUNCH(false, false);
+        }
     }
+#undef BM_LAUNCH_SC2
+#undef BM_LAUNCH_SC
 #undef BM_LAUNCH
     return (int)hipGetLastError();
 }
 
+// Default split: one resident wave of workgroups, each owning a contiguous range.
+static int launch_mp_simple(bool scatter, bool norm, const float* vec, const float* X,
+                            int64_t n_src, const int64_t* src_idx, const int64_t* perm,
+                            const int64_t* row_ptr, float* out, int64_t n_items, int64_t n_edges,
+                            int C, hipStream_t s) {
+    const int64_t target = (int64_t)8 * blocks_per_xcd(C);
+    int64_t per;
+    if (scatter) {
+        per = std::min<int64_t>(kScatterRows, std::max<int64_t>(1, ceil_div(n_items, target)));
+    } else {
+        per = std::max<int64_t>(1, ceil_div(ceil_div(n_edges, kBatch), target)) * kBatch;
+    }
+    const int64_t n_logical = scatter ? ceil_div(n_items, per) : ceil_div(n_edges, per);
+    return launch_mp(scatter, norm, vec, X, n_src, src_idx, perm, row_ptr, nullptr, out, n_items,
+                     n_edges, C, per, n_logical, s);
+}
+
 extern "C" int batteries_fused_sh_tp_simple(const float* edge_vectors, const float* node_features,
                                             const int64_t* source_idx, float* messages,
-                                            int64_t N_edges, int C, int normalize,
+                                            int64_t N_nodes, int64_t N_edges, int C, int normalize,
                                             hipStream_t stream) {
-    if (N_edges < 0 || C <= 0) return BM_ERR_ARG;
+    if (N_edges < 0 || N_nodes < 0 || C <= 0) return BM_ERR_ARG;
     if (N_edges == 0) return BM_OK;
-    return launch_mp_simple(false, normalize != 0, edge_vectors, node_features, source_idx, nullptr,
-                            nullptr, messages, 0, N_edges, C, 0, stream);
+    return launch_mp_simple(false, normalize != 0, edge_vectors, node_features, N_nodes, source_idx,
+                            nullptr, nullptr, messages, 0, N_edges, C, stream);
 }
 
 extern "C" int batteries_sh_tp_scatter_csr(const float* edge_vectors, const float* node_features,
                                            const int64_t* source_idx, const int64_t* perm,
                                            const int64_t* row_ptr, float* node_output,
-                                           int64_t N_dst, int64_t N_edges, int C, int normalize,
-                                           hipStream_t stream) {
-    if (N_dst < 0 || N_edges < 0 || C <= 0) return BM_ERR_ARG;
+                                           int64_t N_src, int64_t N_dst, int64_t N_edges, int C,
+                                           int normalize, hipStream_t stream) {
+    if (N_src < 0 || N_dst < 0 || N_edges < 0 || C <= 0) return BM_ERR_ARG;
     if (N_dst == 0) return BM_OK;
-    // about one 64-edge batch of whole destinations per workgroup
-    const int64_t avg = N_dst > 0 ? ceil_div(N_edges, N_dst) : 1;
-    const int per = (int)std::max<int64_t>(1, kBatch / std::max<int64_t>(1, avg));
-    return launch_mp_simple(true, normalize != 0, edge_vectors, node_features, source_idx, perm,
-                            row_ptr, node_output, N_dst, N_edges, C, per, stream);
+    if (N_src == 0 && N_edges > 0) return BM_ERR_ARG;
+    return launch_mp_simple(true, normalize != 0, edge_vectors, node_features,
+                            std::max<int64_t>(N_src, 1), source_idx, perm, row_ptr, node_output,
+                            N_dst, N_edges, C, stream);
 }
 
 extern "C" int batteries_fused_message_passing_simple(const float* node_features,
@@ -332,7 +679,7 @@ extern "C" int batteries_fused_message_passing_simple(const float* node_features
                                                       hipStream_t stream) {
     // edge data of CSR slot k: e = col_idx[k], src = edge_index[0, e], vector = edge_vectors[e]
     return batteries_sh_tp_scatter_csr(edge_vectors, node_features, edge_index, col_idx, row_ptr,
-                                       node_output, N_atoms, N_edges, C, 0, stream);
+                                       node_output, N_atoms, N_atoms, N_edges, C, 0, stream);
 }
 
 extern "C" size_t batteries_fused_message_passing_workspace_bytes(int64_t N_atoms, int C_in) {
@@ -354,7 +701,7 @@ extern "C" int batteries_fused_message_passing(const float* node_features,
     // edge vector = edge_vectors[k] for CSR slot k.
     float* S = static_cast<float*>(workspace);
     int rc = batteries_sh_tp_scatter_csr(edge_vectors, node_features, col_idx, nullptr, row_ptr, S,
-                                         N_atoms, N_edges, C_in, 0, stream);
+                                         N_atoms, N_atoms, N_edges, C_in, 0, stream);
     if (rc != BM_OK) return rc;
     dense_mix_kernel<<<(unsigned)N_atoms, 256, 0, stream>>>(S, weights, node_output, N_atoms, C_in,
                                                             C_out);
@@ -393,4 +740,111 @@ extern "C" int batteries_edge_index_to_csr(const int64_t* edge_index, int64_t* r
                                                                                N_atoms);
     }
     return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Destination schedule: the fused scatter kernel runs n_blocks workgroups of
+// rows_per_block scheduled rows.  Scheduled row q of workgroup b = q / R at
+// position t = q % R processes destination order[m] with
+//     m = x*P*R + k + t*P,   x = b / P (the XCD), k = b % P, P = n_blocks / 8,
+// so each XCD works on one contiguous eighth of the spatial order and its
+// resident workgroups step through consecutive rows of it together: the rows
+// in flight on an XCD stay spatially compact and their source rows stay in L2.
+// ---------------------------------------------------------------------------
+namespace bmhip {
+
+__global__ void sched_rows_kernel(const int64_t* __restrict__ row_ptr,
+                                  const int64_t* __restrict__ order, int64_t* __restrict__ row_dst,
+                                  int64_t* __restrict__ deg, int64_t n_dst, int64_t n_sched, int P,
+                                  int R, int Q) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n_sched) return;
+    const int64_t b = q / R, t = q - b * R;
+    const int64_t x = b / P, k = b - x * P;
+    // workgroups of an XCD run in generations of Q resident ones; generation
+    // `gen` owns a contiguous chunk of Qg * R positions, interleaved by row
+    const int64_t gen = k / Q, kk = k - gen * Q;
+    const int64_t Qg = std::min<int64_t>(Q, P - gen * Q);
+    const int64_t m = x * P * R + gen * Q * R + kk + t * Qg;
+    const int64_t d = m < n_dst ? order[m] : -1;
+    const bool ok = d >= 0 && d < n_dst;
+    row_dst[q] = ok ? d : -1;
+    deg[q] = ok ? row_ptr[d + 1] - row_ptr[d] : 0;
+}
+
+__global__ void sched_edges_kernel(const int64_t* __restrict__ row_ptr,
+                                   const int64_t* __restrict__ col_perm,
+                                   const int64_t* __restrict__ row_dst,
+                                   const int64_t* __restrict__ row_ptr_s,
+                                   int64_t* __restrict__ edge_perm, int64_t n_sched) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n_sched) return;
+    const int64_t d = row_dst[q];
+    if (d < 0) return;
+    const int64_t s0 = row_ptr[d], n = row_ptr[d + 1] - s0, o = row_ptr_s[q];
+    for (int64_t i = 0; i < n; ++i) edge_perm[o + i] = col_perm ? col_perm[s0 + i] : s0 + i;
+}
+
+}  // namespace bmhip
+
+extern "C" int batteries_mp_schedule_shape(int64_t N_dst, int C, int* n_blocks,
+                                           int* rows_per_block) {
+    if (N_dst < 0 || C <= 0 || !n_blocks || !rows_per_block) return BM_ERR_ARG;
+    int64_t P = blocks_per_xcd(C);
+    int64_t R = std::max<int64_t>(1, ceil_div(N_dst, 8 * P));
+    if (R > kScatterRows) {
+        R = kScatterRows;
+        P = ceil_div(N_dst, 8 * R);
+    }
+    if (8 * P > INT32_MAX) return BM_ERR_ARG;
+    *n_blocks = (int)(8 * P);
+    *rows_per_block = (int)R;
+    return BM_OK;
+}
+
+extern "C" size_t batteries_mp_schedule_workspace_bytes(int n_blocks, int rows_per_block) {
+    return sizeof(int64_t) * (size_t)n_blocks * (size_t)rows_per_block;
+}
+
+extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_perm,
+                                     const int64_t* order, int64_t N_dst, int64_t N_edges, int C,
+                                     int n_blocks, int rows_per_block, int64_t* row_ptr_s,
+                                     int64_t* row_dst, int64_t* edge_perm, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+    if (N_dst < 0 || N_edges < 0 || C <= 0 || n_blocks <= 0 || n_blocks % 8 ||
+        rows_per_block <= 0 || rows_per_block > kScatterRows)
+        return BM_ERR_ARG;
+    const int64_t n_sched = (int64_t)n_blocks * rows_per_block;
+    if (n_sched < N_dst) return BM_ERR_ARG;
+    if (!workspace || workspace_bytes < batteries_mp_schedule_workspace_bytes(n_blocks, rows_per_block))
+        return BM_ERR_WORKSPACE;
+    int64_t* deg = static_cast<int64_t*>(workspace);
+    const int B = 256;
+    const int P = n_blocks / 8;
+    const int Q = std::min(P, blocks_per_xcd(C));
+    sched_rows_kernel<<<(unsigned)ceil_div(n_sched, B), B, 0, stream>>>(
+        row_ptr, order, row_dst, deg, N_dst, n_sched, P, rows_per_block, Q);
+    int rc = batteries_exclusive_scan_i64(deg, row_ptr_s, n_sched, stream);
+    if (rc != BM_OK) return rc;
+    sched_edges_kernel<<<(unsigned)ceil_div(n_sched, B), B, 0, stream>>>(row_ptr, col_perm, row_dst,
+                                                                        row_ptr_s, edge_perm, n_sched);
+    return (int)hipGetLastError();
+}
+
+extern "C" int batteries_sh_tp_scatter_scheduled(const float* edge_vectors,
+                                                 const float* node_features,
+                                                 const int64_t* source_idx,
+                                                 const int64_t* row_ptr_s,
+                                                 const int64_t* edge_perm, const int64_t* row_dst,
+                                                 int n_blocks, int rows_per_block,
+                                                 float* node_output, int64_t N_src,
+                                                 int64_t N_edges, int C, int normalize,
+                                                 hipStream_t stream) {
+    if (N_src < 0 || N_edges < 0 || C <= 0 || n_blocks <= 0 || n_blocks % 8 || rows_per_block <= 0)
+        return BM_ERR_ARG;
+    if (N_src == 0 && N_edges > 0) return BM_ERR_ARG;
+    const int64_t n_sched = (int64_t)n_blocks * rows_per_block;
+    return launch_mp(true, normalize != 0, edge_vectors, node_features, std::max<int64_t>(N_src, 1),
+                     source_idx, edge_perm, row_ptr_s, row_dst, node_output, n_sched, N_edges, C,
+                     rows_per_block, n_blocks, stream);
 }

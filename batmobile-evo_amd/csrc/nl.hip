@@ -347,6 +347,86 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
 }
 
 // ---------------------------------------------------------------------------
+// Spatial (Morton) order of atoms: positions wrapped into the box, quantised to
+// a 32^3 grid, keyed by the 15-bit Morton code of the cell; counting sort by key
+// with ascending atom index inside a cell (deterministic).
+// ---------------------------------------------------------------------------
+constexpr int kMortonBits = 5;
+constexpr int kMortonCells = 1 << (3 * kMortonBits);
+
+__device__ __forceinline__ int spread3(int v) {
+    int r = 0;
+#pragma unroll
+    for (int b = 0; b < kMortonBits; ++b) r |= ((v >> b) & 1) << (3 * b);
+    return r;
+}
+
+__global__ void morton_key_kernel(const float* __restrict__ pos, float bx, float by, float bz,
+                                  int* __restrict__ key, int* __restrict__ count, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float box[3] = {bx, by, bz};
+    int q[3];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        const float p = pos[i * 3 + d];
+        const float w = p - floorf(p / box[d]) * box[d];
+        int v = (int)(w / box[d] * (float)(1 << kMortonBits));
+        v = v < 0 ? 0 : (v > (1 << kMortonBits) - 1 ? (1 << kMortonBits) - 1 : v);
+        q[d] = v;
+    }
+    const int k = spread3(q[0]) | (spread3(q[1]) << 1) | (spread3(q[2]) << 2);
+    key[i] = k;
+    atomicAdd(count + k, 1);
+}
+
+__global__ void morton_place_kernel(const int* __restrict__ key, const int64_t* __restrict__ start,
+                                    int* __restrict__ cursor, int* __restrict__ tmp, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int k = key[i];
+    tmp[start[k] + atomicAdd(cursor + k, 1)] = (int)i;
+}
+
+__global__ void morton_finish_kernel(const int* __restrict__ tmp, int64_t* __restrict__ order,
+                                     int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) order[i] = tmp[i];
+}
+
+extern "C" size_t batteries_spatial_order_workspace_bytes(int64_t N) {
+    if (N < 0) return 0;
+    return align256(sizeof(int) * (size_t)N) * 2 + align256(sizeof(int) * kMortonCells) +
+           align256(sizeof(int64_t) * (kMortonCells + 1));
+}
+
+extern "C" int batteries_spatial_order(const float* positions, const float* box, int64_t N,
+                                       void* workspace, size_t workspace_bytes, int64_t* order,
+                                       hipStream_t stream) {
+    if (N < 0 || !box || !(box[0] > 0.f) || !(box[1] > 0.f) || !(box[2] > 0.f)) return BM_ERR_ARG;
+    if (N == 0) return BM_OK;
+    if (!workspace || workspace_bytes < batteries_spatial_order_workspace_bytes(N))
+        return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    int* key = reinterpret_cast<int*>(ws);
+    int* tmp = reinterpret_cast<int*>(ws + align256(sizeof(int) * (size_t)N));
+    int* count = reinterpret_cast<int*>(ws + 2 * align256(sizeof(int) * (size_t)N));
+    int64_t* start = reinterpret_cast<int64_t*>(ws + 2 * align256(sizeof(int) * (size_t)N) +
+                                                align256(sizeof(int) * kMortonCells));
+    const int B = 256;
+    nl_zero_i32_kernel<<<kMortonCells / B, B, 0, stream>>>(count, kMortonCells);
+    morton_key_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(positions, box[0], box[1], box[2],
+                                                                  key, count, N);
+    int rc = scan_i32(count, start, kMortonCells, stream);
+    if (rc != BM_OK) return rc;
+    nl_zero_i32_kernel<<<kMortonCells / B, B, 0, stream>>>(count, kMortonCells);
+    morton_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(key, start, count, tmp, N);
+    nl_sort_bins_kernel<<<kMortonCells / B, B, 0, stream>>>(start, tmp, kMortonCells);
+    morton_finish_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(tmp, order, N);
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Reference-compatible C ABI (src/neighbor_list/neighbor_list.cu:456-478,
 // include/neighbor_list.cuh:25-33): library-owned device buffers, freed by
 // neighbor_list_free; cell [3,3] in device memory; one host sync for E.

@@ -50,7 +50,11 @@ from _batteries import (  # noqa: E402
     spherical_harmonics_normalized_backward,
     sh_tp_scatter,
     neighbor_list,
+    spatial_order,
+    mp_schedule,
+    sh_tp_scatter_scheduled,
 )
+from .graph import Graph  # noqa: E402
 
 # Autograd-compatible wrappers (reference __init__.py:35-44)
 from .autograd import (  # noqa: E402
@@ -91,4 +95,8 @@ __all__ = [
     "spherical_harmonics_normalized_backward",
     "sh_tp_scatter",
     "neighbor_list",
+    "spatial_order",
+    "mp_schedule",
+    "sh_tp_scatter_scheduled",
+    "Graph",
 ]

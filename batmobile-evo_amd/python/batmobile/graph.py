@@ -1,0 +1,48 @@
+"""A periodic atom graph prepared once for the fused message-passing kernels.
+
+Not a reference API: it bundles what the reference callers do by hand
+(benchmarks/benchmark_e2e_mace.py:192-278 neighbor list, :308-356 SH -> TP ->
+scatter) into GPU-resident tensors that the fused kernel consumes directly:
+
+  src, dst, vec   edges grouped by destination (dst ascending, src ascending within),
+                  vec = minimum-image r_dst - r_src
+  row_ptr         CSR row pointer over destinations [N + 1]
+  schedule        spatial processing order of the destinations (mp_schedule)
+
+The neighbor relation of a cell list is symmetric, so the neighbor list sorted
+by (i, j) read with roles swapped is exactly the edge list sorted by destination,
+with vectors negated (exactly, in fp32).
+"""
+import torch
+
+import _batmobile
+
+
+class Graph:
+    def __init__(self, positions, cell, cutoff, channels, self_loops=False):
+        ei, vec, off = _batmobile.neighbor_list(positions, cell, float(cutoff), bool(self_loops))
+        self.n_atoms = positions.shape[0]
+        self.src = ei[1].contiguous()
+        self.dst = ei[0].contiguous()
+        self.vec = (-vec).contiguous()
+        self.row_ptr = off
+        self.channels = int(channels)
+        self.order = _batmobile.spatial_order(positions, cell)
+        (self.row_ptr_s, self.edge_perm, self.row_dst, self.n_blocks,
+         self.rows_per_block) = _batmobile.mp_schedule(self.row_ptr, self.order, self.channels)
+
+    @property
+    def num_edges(self):
+        return int(self.src.numel())
+
+    def sh_tp_scatter(self, node_features, normalize=True):
+        """out[d] = sum_{e -> d} TP_simple(X[src_e], Y_lm(v_e)); one kernel, spatial schedule."""
+        assert node_features.shape[1] == self.channels, "schedule was built for another C"
+        return _batmobile.sh_tp_scatter_scheduled(
+            self.vec, node_features, self.src, self.row_ptr_s, self.edge_perm, self.row_dst,
+            self.n_blocks, self.rows_per_block, self.n_atoms, normalize)
+
+    def sh_tp_scatter_index_order(self, node_features, normalize=True):
+        """The same sum, destinations processed in index order (no schedule)."""
+        return _batmobile.sh_tp_scatter(self.vec, node_features, self.src, self.row_ptr, None,
+                                        normalize)

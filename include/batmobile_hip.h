@@ -105,15 +105,17 @@ int batteries_tensor_product_backward_l3(const float* input1, const float* input
  * Fused SH + TP, scatter-add, CSR
  * ------------------------------------------------------------------------- */
 
-/* messages[E, C, 16] = TP_simple(node_features[source_idx[e], C, 16], Y(edge_vectors[e])).
+/* messages[E, C, 16] = TP_simple(node_features[source_idx[e], C, 16], Y(edge_vectors[e])),
+ * node_features [N_nodes, C, 16].
  * normalize as in batteries_spherical_harmonics (0 = reference behaviour).
  * node_features and messages must be 16-byte aligned.
  * Replaces batteries::fused_sh_tp_simple, src/message_passing/fused_sh_tp.cu:125-146. */
 int batteries_fused_sh_tp_simple(const float* edge_vectors, const float* node_features,
-                                 const int64_t* source_idx, float* messages, int64_t N_edges,
-                                 int C, int normalize, hipStream_t stream);
+                                 const int64_t* source_idx, float* messages, int64_t N_nodes,
+                                 int64_t N_edges, int C, int normalize, hipStream_t stream);
 
-/* Fused SH + TP + scatter-add into destinations, one pass, no atomics,
+/* Fused SH + TP + scatter-add into destinations (node_features [N_src, C, 16],
+ * node_output [N_dst, C, 16]), one pass, no atomics,
  * deterministic:
  *   node_output[d, C, 16] = sum_{k in [row_ptr[d], row_ptr[d+1])}
  *        TP_simple(node_features[source_idx[e_k]], Y(edge_vectors[e_k])),
@@ -124,8 +126,36 @@ int batteries_fused_sh_tp_simple(const float* edge_vectors, const float* node_fe
  * batteries::fused_message_passing_simple below. */
 int batteries_sh_tp_scatter_csr(const float* edge_vectors, const float* node_features,
                                 const int64_t* source_idx, const int64_t* perm,
-                                const int64_t* row_ptr, float* node_output, int64_t N_dst,
-                                int64_t N_edges, int C, int normalize, hipStream_t stream);
+                                const int64_t* row_ptr, float* node_output, int64_t N_src,
+                                int64_t N_dst, int64_t N_edges, int C, int normalize,
+                                hipStream_t stream);
+
+/* Spatial processing schedule for the fused scatter (no reference counterpart:
+ * the reference processes destinations in index order).  Built once per graph:
+ *   batteries_spatial_order      order[N] = atoms sorted by the Morton code of
+ *                                their cell in a 32^3 grid over the box (host box[3])
+ *   batteries_mp_schedule_shape  n_blocks (multiple of 8) x rows_per_block for C
+ *   batteries_mp_schedule        row_ptr_s[n_blocks*rows_per_block + 1],
+ *                                row_dst[n_blocks*rows_per_block] (-1 = padding),
+ *                                edge_perm[E] (scheduled slot -> original edge; col_perm,
+ *                                if given, is applied as in fused_message_passing_simple)
+ * and consumed by batteries_sh_tp_scatter_scheduled, whose result equals
+ * batteries_sh_tp_scatter_csr on the same graph. */
+size_t batteries_spatial_order_workspace_bytes(int64_t N);
+int batteries_spatial_order(const float* positions, const float* box, int64_t N, void* workspace,
+                            size_t workspace_bytes, int64_t* order, hipStream_t stream);
+int batteries_mp_schedule_shape(int64_t N_dst, int C, int* n_blocks, int* rows_per_block);
+size_t batteries_mp_schedule_workspace_bytes(int n_blocks, int rows_per_block);
+int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_perm, const int64_t* order,
+                          int64_t N_dst, int64_t N_edges, int C, int n_blocks, int rows_per_block,
+                          int64_t* row_ptr_s, int64_t* row_dst, int64_t* edge_perm,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+int batteries_sh_tp_scatter_scheduled(const float* edge_vectors, const float* node_features,
+                                      const int64_t* source_idx, const int64_t* row_ptr_s,
+                                      const int64_t* edge_perm, const int64_t* row_dst,
+                                      int n_blocks, int rows_per_block, float* node_output,
+                                      int64_t N_src, int64_t N_edges, int C, int normalize,
+                                      hipStream_t stream);
 
 /* node_output[N_atoms, C, 16]; CSR slot k is edge col_idx[k], whose source is
  * edge_index[0, col_idx[k]] and vector edge_vectors[col_idx[k]].

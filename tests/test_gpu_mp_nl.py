@@ -211,3 +211,52 @@ def test_config4_scatter_full_size(bm, dev):
     assert normwise_err(out.cpu(), want) <= 1e-5
     # deterministic: bitwise identical on a second run
     assert torch.equal(out, bm.sh_tp_scatter(v, x, src, off, None, True))
+
+
+def test_spatial_order_is_a_morton_permutation(bm, dev):
+    pos, cell = periodic_box(5000, 3)
+    order = bm.spatial_order(pos.to(dev), cell).cpu().numpy()
+    assert np.array_equal(np.sort(order), np.arange(5000))
+    L = float(cell[0, 0])
+    q = np.clip((pos.numpy() / L * 32).astype(int), 0, 31)
+
+    def spread(v):
+        r = np.zeros_like(v)
+        for b in range(5):
+            r |= ((v >> b) & 1) << (3 * b)
+        return r
+
+    key = spread(q[:, 0]) | (spread(q[:, 1]) << 1) | (spread(q[:, 2]) << 2)
+    k = key[order]
+    assert (np.diff(k) >= 0).all()
+    same = np.diff(k) == 0
+    assert (np.diff(order)[same] > 0).all()     # ascending atom index inside a cell
+
+
+@pytest.mark.parametrize("n,c", [(5000, 64), (1500, 16), (700, 128), (40, 5)])
+def test_scheduled_scatter_equals_index_order(bm, dev, n, c):
+    import batmobile
+    pos, cell = periodic_box(n, 11 + n)
+    g = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+    x = torch.randn(n, c, 16, generator=gen(12)).to(dev)
+    a = g.sh_tp_scatter(x)
+    b = g.sh_tp_scatter_index_order(x)
+    # each destination is summed by one wave in CSR order in both: bitwise identical
+    assert torch.equal(a, b)
+    assert int(g.row_dst.ge(0).sum()) == n
+    want = omp.sh_tp_scatter(g.vec.cpu().double().numpy(), x.cpu().double().numpy(), g.src.cpu().numpy(),
+                             g.dst.cpu().numpy(), n, normalize=True)
+    assert normwise_err(a.cpu(), want) <= 1e-5
+
+
+def test_schedule_with_col_perm_matches_fused_message_passing_simple(bm, dev):
+    n, e, c = 900, 20000, 32
+    vec, x, src, dst = _random_graph(n, e, c, 51)
+    ei = torch.stack([src, dst]).to(dev)
+    rp, ci = bm.edge_index_to_csr(ei, n)
+    order = torch.randperm(n, generator=gen(52)).to(dev)
+    rps, ep, rdst, nb, rpb = bm.mp_schedule(rp, order, c, ci)
+    out = bm.sh_tp_scatter_scheduled(vec.to(dev), x.to(dev), ei[0].contiguous(), rps, ep, rdst, nb, rpb, n,
+                                     False)
+    ref = bm.fused_message_passing_simple(x.to(dev), vec.to(dev), ei, rp, ci)
+    assert torch.equal(out, ref)
