@@ -313,10 +313,11 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 // rows_per_block (<= kScatterRows, scheduled) rows of this workgroup.
 //
 // Same operator/MFMA scheme as above, arranged so that the compiler can keep
-// kRing gathers in flight: on gfx9 loads and stores share one counter and may
-// complete out of order, so a store between a gather and its use -- or a gather
-// issued under a data-dependent condition -- makes the compiler drain every
-// outstanding gather before the next MFMA.  Hence the edge loop has neither:
+// kRing gathers in flight.  On gfx9 loads and stores share one counter, and
+// with a store pending the compiler treats the counter as out of order and
+// drains every outstanding gather before the next use; a gather issued under a
+// data-dependent condition has the same effect.  Hence the edge loop has
+// neither:
 //   - every batch is kSBatch edges fully unrolled, and every edge issues the
 //     gather for the edge kRing = kSBatch positions ahead (past the block's last
 //     edge it gathers row 0 of the same tensor, a valid address whose value is
@@ -324,13 +325,14 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 //     block's last row has been staged);
 //   - a finished row is staged in LDS (the workgroup owns at most kScatterRows
 //     rows) and all rows are written to HBM once, after the last batch.
-// Row boundaries are per-batch 64-bit masks built with ballots in phase 1:
-// `starts` selects a zero C operand for the first MFMA of a row (the
-// accumulator is never written outside MFMAs), `ends` triggers the staging.
+// The per-edge control is one scalar bit test: `ends` (a 64-bit mask per batch,
+// built with scalar arithmetic from the row ends) marks the edges that close a
+// row; there the accumulator is staged and reset to zero.
 // ---------------------------------------------------------------------------
 constexpr int kSBatch = 32;       // edges per batch (operators in LDS)
 constexpr int kRing = kSBatch;    // gathers in flight per lane
 constexpr int kScatterRows = 10;  // rows per workgroup (all staged in LDS)
+constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
 template <bool NORM, bool BUF, bool PERM>
 __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
@@ -353,7 +355,6 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const int g = lane >> 4;
     const int i16 = lane & 15;
     const int c = blockIdx.y * kChanGroup + w * 16 + i16;
-    const bool tile_live = blockIdx.y * kChanGroup + w * 16 < C;
     const uint32_t row_bytes = (uint32_t)C * 64u;
     const int voff = (c < C ? c : C - 1) * 64 + g * 16;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -367,6 +368,16 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     }
     __syncthreads();
     const int64_t e0 = sRow[0], e1 = sRow[nrows];
+
+    // Last edge of each non-empty row, relative to e0 (-1: empty or absent row).
+    // Wave-uniform, kept in scalar registers.
+    int row_last[kScatterRows];
+    static_for<kScatterRows>([&](auto rr) {
+        constexpr int r = decltype(rr)::value;
+        int v = -1;
+        if (r < nrows && sRow[r + 1] > sRow[r]) v = (int)(sRow[r + 1] - 1 - e0);
+        row_last[r] = __builtin_amdgcn_readfirstlane(v);
+    });
 
     // Edge records move through a three-stage pipeline so that no wait is on a
     // load younger than the gathers in flight: the edge id of batch b+3 (one
@@ -392,6 +403,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
 
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
     v4f acc = zero4;
+    int slot = 0;  // staged rows so far (the non-empty rows, in order)
 
     EdgeRec cur = record(edge_id(e0));
     EdgeRec nxt = record(edge_id(e0 + kSBatch));
@@ -399,9 +411,9 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     // Every wave runs the edge loop, also one whose 16 channels are all past C
     // (its lanes read channel C-1 and never store): a branch around the loop
     // would make the loop-carried records look like the youngest loads on one
-    // path, and the compiler would drain every gather at the loop latch.
-    // (The guard encloses the ring fill and the loop together for the same
-    // reason: the loop header is reached only after the ring fill.)
+    // path, and the compiler would drain every gather at the loop latch.  (The
+    // guard encloses the ring fill and the loop together for the same reason:
+    // the loop header is reached only after the ring fill.)
     float4 ring[kRing];
     if (e0 < e1) {
     static_for<kRing>([&](auto uu) {
@@ -412,23 +424,14 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         const int nb = (int)min<int64_t>(kSBatch, e1 - kb);
         __syncthreads();
         phase1_build<NORM>(cur, nb, sM);
-        // row of each edge of the batch (for staging) and the batch's row boundaries
-        int my_row = 0;
-        bool is_start = false, is_end = false;
-        if (lane < nb) {
-            const int64_t k = kb + lane;
-            int lo = 0, hi = nrows;  // last row with sRow[row] <= k
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (sRow[mid] <= k) lo = mid;
-                else hi = mid - 1;
-            }
-            my_row = lo;
-            is_start = sRow[lo] == k;
-            is_end = sRow[lo + 1] == k + 1;
-        }
-        const uint64_t starts = __ballot(is_start);
-        const uint64_t ends = __ballot(is_end);
+        // edges of this batch that close a row
+        const int rel = (int)(kb - e0);
+        uint64_t ends = 0;
+        static_for<kScatterRows>([&](auto rr) {
+            constexpr int r = decltype(rr)::value;
+            const int p = row_last[r] - rel;
+            if (row_last[r] >= 0 && p >= 0 && p < kSBatch) ends |= 1ull << p;
+        });
         __syncthreads();
         const EdgeRec nn = record(id2);
         id2 = edge_id(kb + 3 * kSBatch);
@@ -437,18 +440,22 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         __builtin_amdgcn_sched_barrier(0);
         {
             const float* mrow = sM + i16 * 16 + 4 * g;
-            float4 mr[2];
-            mr[0] = *reinterpret_cast<const float4*>(mrow);
+            float4 mr[kLdsAhead + 1];
+            static_for<kLdsAhead>([&](auto qq) {
+                constexpr int q = decltype(qq)::value;
+                mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
+            });
             static_for<kSBatch>([&](auto jj) {
                 constexpr int j = decltype(jj)::value;
-                if constexpr (j + 1 < kSBatch)
-                    mr[(j + 1) & 1] = *reinterpret_cast<const float4*>(mrow + (j + 1) * kMStride);
-                if ((starts >> j) & 1ull) acc = mfma4(mr[j & 1], ring[j], zero4);
-                else acc = mfma4(mr[j & 1], ring[j], acc);
+                if constexpr (j + kLdsAhead < kSBatch)
+                    mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
+                        *reinterpret_cast<const float4*>(mrow + (j + kLdsAhead) * kMStride);
+                acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
                 ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, j), row_bytes);
                 if ((ends >> j) & 1ull) {
-                    const int r = __builtin_amdgcn_readlane(my_row, j);
-                    sStage[w][r][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                    sStage[w][slot][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                    ++slot;
+                    acc = zero4;
                 }
             });
         }
@@ -456,15 +463,13 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         nxt = nn;
     }
     }
-    if (tile_live) {
-        for (int r = 0; r < nrows; ++r) {
-            const int64_t orow = sDst[r];
-            if (c < C && orow >= 0) {
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (sRow[r + 1] > sRow[r]) v = sStage[w][r][lane];
-                *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
-            }
-        }
+    int s = 0;
+    for (int r = 0; r < nrows; ++r) {
+        const int64_t orow = sDst[r];
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sRow[r + 1] > sRow[r]) v = sStage[w][s++][lane];
+        if (c < C && orow >= 0)
+            *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
     }
 }
 
