@@ -110,6 +110,25 @@ def cpu_baseline(torch, w, gpu_out):
     }
 
 
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes recorded in profiles/hbm_traffic.txt (scaled by the copy calibration)."""
+    path = os.path.join(REPO, "profiles", "hbm_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("#") or "|" not in line:
+                    continue
+                k, wl, fk, wk, fs, ws = [t.strip() for t in line.split("|")]
+                if k == kernel and wl == workload:
+                    b = float(fk) * 1024 * float(fs) + float(wk) * 1024 * float(ws)
+                    return b, (f"profiles/hbm_traffic.txt: rocprofv3 FETCH_SIZE {fk} KiB x {fs} + "
+                               f"WRITE_SIZE {wk} KiB x {ws}")
+    except OSError:
+        pass
+    return None, "no rocprofv3 traffic record for this kernel"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +185,8 @@ def main():
     achieved_gbs = bytes_alg / (kernel_ms * 1e-3) / 1e9
     achieved_tf = flops_alg / (kernel_ms * 1e-3) / 1e12
 
+    traffic, traffic_note = measured_traffic("mp_scatter_kernel<true, true, true>", "configs[3]")
+
     extra = {}
     pos_d = w["pos"].to(dev)
     extra["neighbor_list_ms"] = round(time_call(torch, lambda: bm.neighbor_list(pos_d, w["cell"], CUTOFF, False)), 4)
@@ -190,13 +211,15 @@ def main():
             "workload": "configs[3] fused SH+TP+scatter, simple variant: N=5000 atoms, C=64, "
                         "cutoff 5.0 A (~30 nbr), edges sorted by destination, in-kernel normalisation",
             "N_atoms": N_ATOMS, "C": C, "E": E, "box_A": round(w["L"], 4), "seed": SEED,
-            "kernel": "mp_simple_mfma_kernel<SCATTER, NORM> (batmobile.Graph.sh_tp_scatter: spatial schedule)",
+            "kernel": "mp_scatter_kernel<NORM=true, BUF=true, PERM=true> "
+                      "(batmobile.Graph.sh_tp_scatter: spatial schedule)",
             "reference_published_rtx3090_ms": 5.935,
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": None,
+            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
             "algorithmic_bytes_per_launch": bytes_alg, "kernel_ms": kernel_ms,
+            "traffic_source": traffic_note,
         },
         "roofline_mfma": {
             "bound": "mfma", "achieved": achieved_tf, "peak": MFMA_FP32_PEAK_TFLOPS,
