@@ -33,6 +33,36 @@ __device__ __forceinline__ void static_for(F&& f) {
 __host__ __device__ constexpr int sh_dim(int l) { return (l + 1) * (l + 1); }
 
 // ---------------------------------------------------------------------------
+// v_mfma_f32_16x16x4f32: D (16x16) += A (16x4) * B (4x16), fp32 in and out.
+// Lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and holds
+// D[4 (l / 16) + r][l % 16] in element r of the accumulator.
+// mfma4 runs four of them, k-step s taking component s of both float4s.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ v4f mfma1(float a, float b, v4f acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
+// Raw buffer loads: 32-bit lane offset (VGPR) + uniform offset (SGPR) from a
+// base address, reads past num_records bytes return 0.
+constexpr int kBufferDword3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, (int)bytes,
+                                             kBufferDword3);
+}
+__device__ __forceinline__ float buffer_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ v4f mfma4(const float4 a, const float4 b, v4f acc) {
+    acc = mfma1(a.x, b.x, acc);
+    acc = mfma1(a.y, b.y, acc);
+    acc = mfma1(a.z, b.z, acc);
+    acc = mfma1(a.w, b.w, acc);
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
 // Real spherical harmonics (e3nn component normalisation, y polar axis) of a
 // (not necessarily unit) vector, as the recurrence
 //   Y_{l+1}[M] = sum c * Y_l[m] * r_j .

@@ -89,18 +89,9 @@ __device__ __forceinline__ void phase1_build(EdgeRec r, int nb, float* sM) {
     }
 }
 
-__device__ __forceinline__ v4f mfma4(const float4 m, const float4 xv, v4f acc) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(m.x, xv.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(m.y, xv.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(m.z, xv.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(m.w, xv.w, acc, 0, 0, 0);
-    return acc;
-}
-
 // Gather of one lane's float4 of source row `src` at byte offset `voff` inside
 // the row.  BUF: raw buffer load with the row offset in a scalar register (X
 // below 4 GiB); otherwise a 64-bit global load.
-constexpr int kBufferDword3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3
 
 template <bool BUF>
 __device__ __forceinline__ float4 gather(const float* __restrict__ X, __amdgpu_buffer_rsrc_t rsrc,

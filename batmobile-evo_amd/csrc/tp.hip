@@ -87,80 +87,595 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// weighted product
-//   out[n,co,o] = sum_q W[path(q), ci, co] * T[n,ci,q] * [out(q) == o]
-//   T[n,ci,q]   = sum_{(a,b) in q} c * x[n,ci,a] * y[n,b]     (156 slots)
+// Weighted product on MFMA.
+//
+//   T[n,ci,q]   = sum_{(a,b) in slot q} c * x[n,ci,a] * y[n,b]      156 slots q = (path, m_out)
+//   out[n,co,o] = sum_{q: out(q) = o} sum_ci W[p(q),ci,co] T[n,ci,q]
+//   h[n,ci,q]   = sum_co W[p(q),ci,co] g[n,co,out(q)]
+//   gx[n,ci,a]  = sum_{q,b} c * y[n,b] * h[n,ci,q]
+//   gy[n,b]     = sum_{ci,q,a} c * x[n,ci,a] * h[n,ci,q]
+//   gW[p,ci,co] = sum_n sum_{q in p} T[n,ci,q] * g[n,co,out(q)]
+//
+// The three channel contractions (out, h, gW) are GEMMs per slot and run on
+// v_mfma_f32_16x16x4f32 over 16-row tiles; the CG contractions (T, gx, gy) run
+// on the VALU with compile-time coefficients.  Each kernel splits the slots
+// into groups taken by different workgroups (blockIdx.z), so that a group's
+// outputs are disjoint from the others':
+//   forward:  output components o in [4G, 4G + 4)      (4 groups)
+//   backward: paths with l1 in {0,1}, {2}, {3}          (3 groups; disjoint gx columns)
+// K-dimension trick: a float4 read by lane group g = lane / 16 supplies k-steps
+// s = 0..3, and A and B agree on which channel (or row) each (g, s) stands for.
 // ---------------------------------------------------------------------------
-constexpr int kWRows = 4;     // rows per workgroup
-constexpr int kWChunk = 16;   // input channels per LDS chunk
+constexpr int kTile = 16;  // rows per MFMA tile
 
-__global__ __launch_bounds__(kTpBlock) void tp_weighted_forward_kernel(
-    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
-    float* __restrict__ out, int64_t n, int cin, int cout) {
-    __shared__ float sT[kWRows * kWChunk * kNumSlots];
-    __shared__ float sy[kWRows * 16];
-    const int64_t row0 = (int64_t)blockIdx.x * kWRows;
-    const int rows = (int)min<int64_t>(kWRows, n - row0);
-    const int tid = threadIdx.x;
-    for (int i = tid; i < rows * 16; i += kTpBlock) sy[i] = y[row0 * 16 + i];
-    // each thread owns (r, co) pairs r = pair / cout, co = pair % cout
-    const int npairs = rows * cout;
-    const int my_pairs = (npairs + kTpBlock - 1) / kTpBlock;  // usually 1
-    for (int pp = 0; pp < my_pairs; ++pp) {
-        const int pair = tid + pp * kTpBlock;
-        const bool active = pair < npairs;
-        const int r = active ? pair / cout : 0;
-        const int co = active ? pair - r * cout : 0;
-        float acc[16];
+constexpr int kFwdGroups = 4;
+constexpr bool fwd_in_group(int q, int G) { return kSlotOut[q] / 4 == G; }
+constexpr int fwd_group_size(int G) {
+    int c = 0;
+    for (int q = 0; q < kNumSlots; ++q) c += fwd_in_group(q, G) ? 1 : 0;
+    return c;
+}
+constexpr int fwd_local(int q, int G) {
+    int c = 0;
+    for (int i = 0; i < q; ++i) c += fwd_in_group(i, G) ? 1 : 0;
+    return c;
+}
+constexpr bool fwd_path_in_group(int p, int G) {
+    for (int m = 0; m < 2 * kPathL[p][2] + 1; ++m)
+        if (fwd_in_group(kPathSlot[p] + m, G)) return true;
+    return false;
+}
+constexpr int fwd_group_paths(int G) {
+    int c = 0;
+    for (int p = 0; p < kNumPaths; ++p) c += fwd_path_in_group(p, G) ? 1 : 0;
+    return c;
+}
+constexpr int fwd_path_local(int p, int G) {
+    int c = 0;
+    for (int i = 0; i < p; ++i) c += fwd_path_in_group(i, G) ? 1 : 0;
+    return c;
+}
+constexpr int fwd_path_at(int k, int G) {  // the k-th path of group G
+    for (int p = 0; p < kNumPaths; ++p)
+        if (fwd_path_in_group(p, G) && fwd_path_local(p, G) == k) return p;
+    return -1;
+}
+constexpr int fwd_max_group() {
+    int m = 0;
+    for (int G = 0; G < kFwdGroups; ++G) m = fwd_group_size(G) > m ? fwd_group_size(G) : m;
+    return m;
+}
+constexpr int kFwdMaxSlots = fwd_max_group();
+
+constexpr int kBwdGroups = 3;
+constexpr int kBwdL1First[kBwdGroups] = {0, 2, 3};
+constexpr int kBwdL1Last[kBwdGroups] = {1, 2, 3};
+constexpr bool bwd_path_in_group(int p, int G) {
+    return kPathL[p][0] >= kBwdL1First[G] && kPathL[p][0] <= kBwdL1Last[G];
+}
+constexpr int bwd_a0(int G) { return kBwdL1First[G] * kBwdL1First[G]; }
+constexpr int bwd_na(int G) { return (kBwdL1Last[G] + 1) * (kBwdL1Last[G] + 1) - bwd_a0(G); }
+constexpr int bwd_group_size(int G) {
+    int c = 0;
+    for (int p = 0; p < kNumPaths; ++p) c += bwd_path_in_group(p, G) ? 2 * kPathL[p][2] + 1 : 0;
+    return c;
+}
+constexpr int bwd_group_paths(int G) {
+    int c = 0;
+    for (int p = 0; p < kNumPaths; ++p) c += bwd_path_in_group(p, G) ? 1 : 0;
+    return c;
+}
+// position of path p among the paths of group G, and of slot q among its slots
+constexpr int bwd_path_local(int p, int G) {
+    int c = 0;
+    for (int i = 0; i < p; ++i) c += bwd_path_in_group(i, G) ? 1 : 0;
+    return c;
+}
+constexpr int bwd_path_at(int k, int G) {  // the k-th path of group G
+    for (int p = 0; p < kNumPaths; ++p)
+        if (bwd_path_in_group(p, G) && bwd_path_local(p, G) == k) return p;
+    return -1;
+}
+constexpr int bwd_slot_local(int q, int G) {
+    int c = 0;
+    for (int i = 0; i < q; ++i) c += bwd_path_in_group(kSlotPath[i], G) ? 1 : 0;
+    return c;
+}
+constexpr int bwd_max_group() {
+    int m = 0;
+    for (int G = 0; G < kBwdGroups; ++G) m = bwd_group_size(G) > m ? bwd_group_size(G) : m;
+    return m;
+}
+constexpr int kBwdMaxSlots = bwd_max_group();
+
+// Out-of-range operands.  Every load reads a clamped, valid address and is
+// issued unconditionally (a branch around a load costs a full wait right after
+// it).  Where an out-of-range value could reach a stored result it is zeroed
+// with mask0, an exact byte select (v_perm_b32) that the compiler does not turn
+// back into a branch; elsewhere the tail is harmless by construction (it meets
+// a zero operand, or lands in a discarded output row or column).
+__device__ __forceinline__ float mask0(float v, bool ok) {
+    return __uint_as_float(
+        __builtin_amdgcn_perm(__float_as_uint(v), 0u, ok ? 0x07060504u : 0x0c0c0c0cu));
+}
+
+// 16 floats at p + off (off a multiple of 4 floats, a valid address)
+__device__ __forceinline__ void load16(const float* __restrict__ p, int64_t off, float* v) {
+    const float4* q = reinterpret_cast<const float4*>(p + off);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
-        for (int c0 = 0; c0 < cin; c0 += kWChunk) {
-            const int cw = min(kWChunk, cin - c0);
-            __syncthreads();
-            // phase 1: per-path products for (r, ci) of this chunk
-            for (int it = tid; it < rows * cw; it += kTpBlock) {
-                const int rr = it / cw, ci = it - rr * cw;
-                const float* xr = x + ((row0 + rr) * cin + c0 + ci) * 16;
-                float a[16], b[16], t[kNumSlots];
+    for (int k = 0; k < 4; ++k) {
+        const float4 t = q[k];
+        v[4 * k + 0] = t.x;
+        v[4 * k + 1] = t.y;
+        v[4 * k + 2] = t.z;
+        v[4 * k + 3] = t.w;
+    }
+}
+// the same, zeroed when !ok
+__device__ __forceinline__ void load16_mask(const float* __restrict__ p, int64_t off, bool ok,
+                                            float* v) {
+    load16(p, off, v);
 #pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    a[k] = xr[k];
-                    b[k] = sy[rr * 16 + k];
+    for (int k = 0; k < 16; ++k) v[k] = mask0(v[k], ok);
+}
+
+// ---- forward ---------------------------------------------------------------
+// Workgroup: 16 rows x 64 output channels x one output group G; wave w owns
+// output channels co0 .. co0+15.  Per chunk of 16 input channels: thread
+// (row, ci) builds the group's T values into LDS, then each wave runs
+//   D[co][row] += W[p][ci][co] (A, global/L2) x T[row][ci][q] (B, LDS)
+// for every slot q of the group, one accumulator per output component.
+// LDS layout sT[slot][g][row][s] with ci = 4g + s: the B read of lane
+// (row = lane % 16, g) is one float4, and a wave's T writes are contiguous.
+template <int G>
+__device__ __forceinline__ void fwd_group(const float* __restrict__ x, const float* __restrict__ w,
+                                          float* __restrict__ out, int64_t n, int cin, int cout,
+                                          float* sT, const float* sY) {
+    constexpr int NS = fwd_group_size(G);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g4 = lane >> 4, i16 = lane & 15;
+    const int64_t row0 = (int64_t)blockIdx.x * kTile;
+    const int co0 = (blockIdx.y * 4 + wv) * 16;
+    const bool live = co0 < cout;
+    const int trow = tid & 15, tcl = tid >> 4;
+    const bool trow_ok = row0 + trow < n;
+    float yb[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) yb[k] = sY[trow * 16 + k];
+    v4f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    constexpr int NP = fwd_group_paths(G);
+    const int co = co0 + i16;
+    const int wpath_bytes = cin * cout * 4;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
+    for (int c0 = 0; c0 < cin; c0 += 16) {
+        // A operands W[p][c0 + 4 g4 + s][co] of the group's paths through a
+        // register ring of kWRing paths: the first ones are issued before the T
+        // computation (their latency hides behind it), and each path's MFMAs
+        // issue the load of the path kWRing ahead.
+        // (ci >= cin meets T = 0; co >= cout lands in a discarded output row).
+        // Buffer loads: lane offset in a VGPR, path offset p * cin * cout in an SGPR.
+        int wo[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) wo[s] = (min(c0 + 4 * g4 + s, cin - 1) * cout + min(co, cout - 1)) * 4;
+        auto load_w = [&](int p) {
+            const int so = p * wpath_bytes;
+            return make_float4(buffer_ld(wr, wo[0], so), buffer_ld(wr, wo[1], so),
+                               buffer_ld(wr, wo[2], so), buffer_ld(wr, wo[3], so));
+        };
+        constexpr int kWRing = 4;
+        float4 wring[kWRing];
+        static_for<(NP < kWRing ? NP : kWRing)>([&](auto kk) {
+            constexpr int k = decltype(kk)::value;
+            constexpr int pk = fwd_path_at(k, G);
+            wring[k] = load_w(pk);
+        });
+        float t[NS];
+        {
+            const int ci = c0 + tcl;
+            // y through an empty asm each chunk: the products c * y[b] are formed
+            // here instead of being hoisted out of the chunk loop (and kept live)
+            float yk[16];
+#pragma unroll
+            for (int b = 0; b < 16; ++b) yk[b] = yb[b];
+            asm volatile("" : "+v"(yk[0]), "+v"(yk[1]), "+v"(yk[2]), "+v"(yk[3]), "+v"(yk[4]),
+                              "+v"(yk[5]), "+v"(yk[6]), "+v"(yk[7]), "+v"(yk[8]), "+v"(yk[9]),
+                              "+v"(yk[10]), "+v"(yk[11]), "+v"(yk[12]), "+v"(yk[13]),
+                              "+v"(yk[14]), "+v"(yk[15]));
+            float xa[16];
+            // T must be 0 for ci >= cin (it meets nonzero W); rows >= n are discarded
+            load16_mask(x, ((min<int64_t>(row0 + trow, n - 1)) * cin + min(ci, cin - 1)) * 16,
+                        ci < cin, xa);
+#pragma unroll
+            for (int q = 0; q < NS; ++q) t[q] = 0.0f;
+            static_for<kNumEntries>([&](auto kk) {
+                constexpr CGEntry e = kCG[decltype(kk)::value];
+                if constexpr (fwd_in_group(e.q, G)) {
+                    constexpr int sl = fwd_local(e.q, G);
+                    t[sl] = fmaf(e.c * yk[e.b], xa[e.a], t[sl]);
                 }
-                tp_per_path(a, b, t);
-                float* dstT = sT + (rr * kWChunk + ci) * kNumSlots;
+            });
+        }
+        __syncthreads();  // the previous chunk's B reads are done
 #pragma unroll
-                for (int q = 0; q < kNumSlots; ++q) dstT[q] = t[q];
-            }
-            __syncthreads();
-            if (active) {
-                for (int ci = 0; ci < cw; ++ci) {
-                    const float* Tq = sT + (r * kWChunk + ci) * kNumSlots;
-                    const float* wc = w + (int64_t)(c0 + ci) * cout + co;
-                    static_for<kNumPaths>([&](auto pp2) {
-                        constexpr int p = decltype(pp2)::value;
-                        const float wp = wc[(int64_t)p * cin * cout];
-                        constexpr int s0 = kPathSlot[p];
-                        constexpr int lo = kPathL[p][2];
-                        static_for<2 * lo + 1>([&](auto mm) {
-                            constexpr int m = decltype(mm)::value;
-                            acc[lo * lo + m] = fmaf(wp, Tq[s0 + m], acc[lo * lo + m]);
-                        });
+        for (int q = 0; q < NS; ++q) sT[q * 256 + (tcl >> 2) * 64 + trow * 4 + (tcl & 3)] = t[q];
+        __syncthreads();
+        if (live) {
+            static_for<kNumPaths>([&](auto pp) {
+                constexpr int p = decltype(pp)::value;
+                if constexpr (fwd_path_in_group(p, G)) {
+                    constexpr int k = fwd_path_local(p, G);
+                    const float4 a4 = wring[k % kWRing];
+                    if constexpr (k + kWRing < NP) {
+                        constexpr int pn = fwd_path_at(k + kWRing, G);
+                        wring[k % kWRing] = load_w(pn);
+                    }
+                    constexpr int lo = kPathL[p][2];
+                    static_for<2 * lo + 1>([&](auto mm) {
+                        constexpr int q = kPathSlot[p] + decltype(mm)::value;
+                        if constexpr (fwd_in_group(q, G)) {
+                            constexpr int sl = fwd_local(q, G);
+                            constexpr int oj = kSlotOut[q] & 3;
+                            const float4 b4 = *reinterpret_cast<const float4*>(
+                                sT + sl * 256 + g4 * 64 + i16 * 4);
+                            acc[oj] = mfma4(a4, b4, acc[oj]);
+                        }
                     });
                 }
-            }
+            });
         }
-        if (active) {
-            float* o = out + ((row0 + r) * cout + co) * 16;
+    }
+    // D[4 g4 + r][i16]: output channel co0 + 4 g4 + r of row row0 + i16
+    const int64_t row = row0 + i16;
+    if (live && row < n) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) o[k] = acc[k];
+        for (int r = 0; r < 4; ++r) {
+            const int co = co0 + 4 * g4 + r;
+            if (co < cout)
+                *reinterpret_cast<float4*>(out + (row * cout + co) * 16 + 4 * G) =
+                    make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
         }
     }
 }
 
-// grad_x and grad_y.  h[n,ci,q] = sum_co W[path(q),ci,co] g[n,co,out(q)],
-// gx = CG^T(h, y), gy = sum_ci CG^T(h, x).  One thread per (row, ci); the
-// per-ci gy partials are reduced in a fixed order.
+__global__ __launch_bounds__(kTpBlock) void tp_weighted_fwd_mfma_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
+    float* __restrict__ out, int64_t n, int cin, int cout) {
+    __shared__ __attribute__((aligned(16))) float sT[kFwdMaxSlots * 256];
+    __shared__ float sY[kTile * 16];
+    const int64_t row0 = (int64_t)blockIdx.x * kTile;
+    {
+        const int r = threadIdx.x >> 4, k = threadIdx.x & 15;
+        sY[threadIdx.x] = row0 + r < n ? y[(row0 + r) * 16 + k] : 0.0f;
+    }
+    __syncthreads();
+    switch (blockIdx.z) {
+        case 0: fwd_group<0>(x, w, out, n, cin, cout, sT, sY); break;
+        case 1: fwd_group<1>(x, w, out, n, cin, cout, sT, sY); break;
+        case 2: fwd_group<2>(x, w, out, n, cin, cout, sT, sY); break;
+        default: fwd_group<3>(x, w, out, n, cin, cout, sT, sY); break;
+    }
+}
+
+// ---- backward: grad_x and per-group grad_y ----------------------------------
+// Workgroup: 16 rows x one l1 group G; wave w takes input-channel tiles
+// w, w + nw, ...  The grad_output tile of the 16 rows is staged in LDS as
+// sG[o][co/4][row][co%4] (plane stride PS): lane (row, g) reads
+// g[row][cb + 4g .. +3][o] as one float4.  Per path p of the group:
+//   D[ci][row] = h_p[row][ci][m_out] = sum_co W[p][ci][co] (A) g[row][co][o] (B)
+// lands in lane (row = lane % 16, ci = 4 g + r), which then applies the CG
+// entries of p to its own 4 channels: gx columns of the group and a grad_y
+// partial.  The partials are summed over lanes and waves in a fixed order.
+template <int G, int KCO>
+__device__ __forceinline__ void bwd_xy_group(const float* __restrict__ x,
+                                             const float* __restrict__ y,
+                                             const float* __restrict__ w, float* __restrict__ gx,
+                                             float* __restrict__ gy_part, int64_t n, int cin,
+                                             int cout, float* sG) {
+    constexpr int PS = KCO * 16 + 4;
+    constexpr int A0 = bwd_a0(G), NA = bwd_na(G);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nw = blockDim.x >> 6;
+    const int g4 = lane >> 4, i16 = lane & 15;
+    const int64_t row0 = (int64_t)blockIdx.x * kTile;
+    const int64_t row = row0 + i16;
+    const bool row_ok = row < n;
+    const int64_t row_c = row_ok ? row : n - 1;  // clamped row for unconditional loads
+    const int wpath_bytes = cin * cout * 4;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
+    float yb[16];
+    load16(y, row_c * 16, yb);  // rows >= n only reach discarded outputs
+    float gyp[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gyp[k] = 0.0f;
+
+    for (int ct = wv; ct * 16 < cin; ct += nw) {
+        const int ci0 = ct * 16;
+        float xa[4][NA], gxa[4][NA];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int ci = ci0 + 4 * g4 + r;
+            const float* xr = x + (row_c * cin + min(ci, cin - 1)) * 16 + A0;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+                xa[r][a] = mask0(xr[a], ci < cin);  // meets h rows of channels >= cin
+                gxa[r][a] = 0.0f;
+            }
+        }
+        // A operands W[p][ciA][cb + 4 g4 + s] of one path, all KCO/16 channel
+        // chunks (clamped addresses: channels >= cin give h rows that meet
+        // x = 0 or are discarded, co >= cout meets the zero-padded g tile).
+        // The next path's operands are loaded while this path's MFMAs and CG
+        // contraction run.
+        // Buffer loads: lane offset in a VGPR, path offset p * cin * cout in an SGPR.
+        const int ciA = ci0 + i16;
+        const int wrow = min(ciA, cin - 1) * cout;
+        constexpr int NCB = KCO / 16;
+        auto load_w = [&](int p, float4* dst) {
+            const int so = p * wpath_bytes;
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                float a[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    a[s] = buffer_ld(wr, (wrow + min(cb * 16 + 4 * g4 + s, cout - 1)) * 4, so);
+                dst[cb] = make_float4(a[0], a[1], a[2], a[3]);
+            }
+        };
+        // One path per iteration of a loop that is not unrolled: each path is a
+        // basic block of its own, so instruction selection cannot hoist every
+        // path's MFMAs ahead of the CG contractions (which would keep all of
+        // the group's h accumulators live at once).
+        constexpr int NPG = bwd_group_paths(G);
+        float4 wcur[NCB], wnxt[NCB];
+        constexpr int p0 = bwd_path_at(0, G);
+        load_w(p0, wcur);
+#pragma clang loop unroll(disable)
+        for (int k = 0; k < NPG; ++k) {
+            // y through an empty asm each iteration: the products c * y[b] are then
+            // formed per path instead of being hoisted out of the loops (some 200
+            // loop-invariant values that would not fit in registers)
+            float yk[16];
+#pragma unroll
+            for (int b = 0; b < 16; ++b) yk[b] = yb[b];
+            asm volatile("" : "+v"(yk[0]), "+v"(yk[1]), "+v"(yk[2]), "+v"(yk[3]), "+v"(yk[4]),
+                              "+v"(yk[5]), "+v"(yk[6]), "+v"(yk[7]), "+v"(yk[8]), "+v"(yk[9]),
+                              "+v"(yk[10]), "+v"(yk[11]), "+v"(yk[12]), "+v"(yk[13]),
+                              "+v"(yk[14]), "+v"(yk[15]));
+            static_for<NPG>([&](auto kk) {
+                constexpr int kc = decltype(kk)::value;
+                if (k == kc) {
+                    constexpr int p = bwd_path_at(kc, G);
+                    if constexpr (kc + 1 < NPG) {
+                        constexpr int pn = bwd_path_at(kc + 1, G);
+                        load_w(pn, wnxt);
+                    }
+                    constexpr int lo = kPathL[p][2];
+                    constexpr int NM = 2 * lo + 1;
+                    v4f h[NM];
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) h[m] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int cb = 0; cb < NCB; ++cb) {
+                        if (cb * 16 < cout) {  // uniform
+                            static_for<NM>([&](auto mm) {
+                                constexpr int m = decltype(mm)::value;
+                                const float4 b4 = *reinterpret_cast<const float4*>(
+                                    sG + (lo * lo + m) * PS + (cb * 4 + g4) * 64 + i16 * 4);
+                                h[m] = mfma4(wcur[cb], b4, h[m]);
+                            });
+                        }
+                        __builtin_amdgcn_sched_barrier(0);  // bound the B reads in flight
+                    }
+                    static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                        constexpr CGEntry e = kCG[kPathEntry[p] + decltype(ee)::value];
+                        constexpr int m = e.o - lo * lo;
+                        constexpr int ai = e.a - A0;
+                        const float cy = e.c * yk[e.b];
+                        float sacc = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            gxa[r][ai] = fmaf(cy, h[m][r], gxa[r][ai]);
+                            sacc = fmaf(xa[r][ai], h[m][r], sacc);
+                        }
+                        gyp[e.b] = fmaf(e.c, sacc, gyp[e.b]);
+                    });
+                    if constexpr (kc + 1 < NPG) {
+#pragma unroll
+                        for (int cb = 0; cb < NCB; ++cb) wcur[cb] = wnxt[cb];
+                    }
+                }
+            });
+        }
+        if (gx && row_ok) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ci = ci0 + 4 * g4 + r;
+                if (ci < cin)
+#pragma unroll
+                    for (int a = 0; a < NA; ++a) gx[(row * cin + ci) * 16 + A0 + a] = gxa[r][a];
+            }
+        }
+    }
+    if (!gy_part) return;  // uniform over the workgroup
+    __syncthreads();       // sG is reused for the reduction
+    float* sRed = sG;      // [wave][g][row][16]
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sRed[((wv * 4 + g4) * 16 + i16) * 16 + k] = gyp[k];
+    __syncthreads();
+    for (int i = tid; i < kTile * 16; i += blockDim.x) {
+        const int rr = i >> 4, k = i & 15;
+        float sum = 0.0f;
+        for (int v = 0; v < nw; ++v)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) sum += sRed[((v * 4 + gg) * 16 + rr) * 16 + k];
+        if (row0 + rr < n) gy_part[((int64_t)G * n + row0 + rr) * 16 + k] = sum;
+    }
+}
+
+template <int KCO>
+__global__ __launch_bounds__(kTpBlock) void tp_weighted_bwd_xy_mfma_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
+    const float* __restrict__ g, float* __restrict__ gx, float* __restrict__ gy_part, int64_t n,
+    int cin, int cout) {
+    constexpr int PS = KCO * 16 + 4;
+    __shared__ __attribute__((aligned(16))) float sG[kTile * PS];
+    const int64_t row0 = (int64_t)blockIdx.x * kTile;
+    const int cout16 = (cout + 15) & ~15;  // MFMA chunks read channels below cout16
+    // stage g[row0 .. row0+15][co][o] (zeros past n and past cout)
+    for (int i = threadIdx.x; i < kTile * cout16 * 4; i += blockDim.x) {
+        const int rr = i / (cout16 * 4), rem = i - rr * cout16 * 4;
+        const int co = rem >> 2, j = rem & 3;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row0 + rr < n && co < cout)
+            v = *reinterpret_cast<const float4*>(g + ((row0 + rr) * cout + co) * 16 + 4 * j);
+        float* d = sG + (co >> 2) * 64 + rr * 4 + (co & 3);
+        d[(4 * j + 0) * PS] = v.x;
+        d[(4 * j + 1) * PS] = v.y;
+        d[(4 * j + 2) * PS] = v.z;
+        d[(4 * j + 3) * PS] = v.w;
+    }
+    __syncthreads();
+    switch (blockIdx.z) {
+        case 0: bwd_xy_group<0, KCO>(x, y, w, gx, gy_part, n, cin, cout, sG); break;
+        case 1: bwd_xy_group<1, KCO>(x, y, w, gx, gy_part, n, cin, cout, sG); break;
+        default: bwd_xy_group<2, KCO>(x, y, w, gx, gy_part, n, cin, cout, sG); break;
+    }
+}
+
+// gy[i] = part[0][i] + part[1][i] + part[2][i] (fixed order)
+__global__ __launch_bounds__(kTpBlock) void sum_groups_kernel(const float* __restrict__ part,
+                                                              float* __restrict__ out,
+                                                              int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * kTpBlock + threadIdx.x;
+    if (i >= count) return;
+    float s = part[i];
+    for (int G = 1; G < kBwdGroups; ++G) s += part[(int64_t)G * count + i];
+    out[i] = s;
+}
+
+// ---- backward: grad_W partials over row segments ----------------------------
+// Workgroup: one row segment x 16 input channels x one l1 group x 64 output
+// channels (wave w: co0 .. co0+15).  Per 16-row chunk: thread t builds T for
+// (row 4 (t % 4) + t / 64, ci (t / 4) % 16) into sT[slot][g][ci][r] (row = 4 r + g),
+// lane (co, g) holds g[row 4 r + g][co][0..15] in registers, and
+//   D[ci][co] += T[row][ci][q] (A, LDS float4 over r) x g[row][co][out(q)] (B)
+// with k = (m_out, r) for every path of the group; one accumulator per path.
+template <int G>
+__device__ __forceinline__ void bwd_w_group(const float* __restrict__ x, const float* __restrict__ y,
+                                            const float* __restrict__ g, float* __restrict__ part,
+                                            int64_t n, int cin, int cout, int64_t rows_per_seg,
+                                            float* sT, float* sY) {
+    constexpr int NS = bwd_group_size(G);
+    constexpr int NP = bwd_group_paths(G);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g4 = lane >> 4, i16 = lane & 15;
+    const int64_t seg = blockIdx.x;
+    const int ci0 = blockIdx.y * 16;
+    const int co0 = ((blockIdx.z / kBwdGroups) * 4 + wv) * 16;
+    const bool live = co0 < cout;
+    const int64_t r0 = seg * rows_per_seg;
+    const int64_t r1 = min<int64_t>(n, r0 + rows_per_seg);
+    // T thread mapping
+    const int t_r = tid & 3, t_ci = ci0 + ((tid >> 2) & 15), t_g = tid >> 6;
+    const int t_row = 4 * t_r + t_g;
+    v4f acc[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t rc = r0; rc < r1; rc += kTile) {
+        __syncthreads();  // the previous chunk's reads of sT and sY are done
+        {
+            const int rr = tid >> 4, k = tid & 15;
+            sY[tid] = y[min<int64_t>(rc + rr, n - 1) * 16 + k];
+        }
+        // B operands of this chunk, issued before the T computation hides their latency
+        float gv[4][16];
+        {
+            const int co = co0 + i16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // rows past the segment must not count; co >= cout is a discarded column
+                const int64_t rw = rc + 4 * r + g4;
+                load16_mask(g, (min<int64_t>(rw, n - 1) * cout + min(co, cout - 1)) * 16, rw < r1,
+                            gv[r]);
+            }
+        }
+        __syncthreads();
+        {
+            float xa[16], yb[16], t[NS];
+            // T rows past the segment meet g = 0; channels >= cin are discarded rows
+            load16(x, (min<int64_t>(rc + t_row, n - 1) * cin + min(t_ci, cin - 1)) * 16, xa);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) yb[k] = sY[t_row * 16 + k];
+#pragma unroll
+            for (int q = 0; q < NS; ++q) t[q] = 0.0f;
+            static_for<kNumEntries>([&](auto kk) {
+                constexpr CGEntry e = kCG[decltype(kk)::value];
+                if constexpr (bwd_path_in_group(e.p, G)) {
+                    constexpr int sl = bwd_slot_local(e.q, G);
+                    t[sl] = fmaf(e.c * yb[e.b], xa[e.a], t[sl]);
+                }
+            });
+#pragma unroll
+            for (int q = 0; q < NS; ++q) sT[q * 256 + tid] = t[q];
+        }
+        __syncthreads();
+        if (live) {
+            static_for<kNumPaths>([&](auto pp) {
+                constexpr int p = decltype(pp)::value;
+                if constexpr (bwd_path_in_group(p, G)) {
+                    constexpr int lo = kPathL[p][2];
+                    constexpr int pl = bwd_path_local(p, G);
+                    static_for<2 * lo + 1>([&](auto mm) {
+                        constexpr int m = decltype(mm)::value;
+                        constexpr int sl = bwd_slot_local(kPathSlot[p] + m, G);
+                        const float4 a4 =
+                            *reinterpret_cast<const float4*>(sT + sl * 256 + g4 * 64 + i16 * 4);
+                        const float4 b4 = make_float4(gv[0][lo * lo + m], gv[1][lo * lo + m],
+                                                      gv[2][lo * lo + m], gv[3][lo * lo + m]);
+                        acc[pl] = mfma4(a4, b4, acc[pl]);
+                    });
+                }
+            });
+        }
+    }
+    // D[4 g4 + r][i16]: input channel ci0 + 4 g4 + r, output channel co0 + i16
+    if (live) {
+        const int co = co0 + i16;
+        static_for<kNumPaths>([&](auto pp) {
+            constexpr int p = decltype(pp)::value;
+            if constexpr (bwd_path_in_group(p, G)) {
+                constexpr int pl = bwd_path_local(p, G);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ci = ci0 + 4 * g4 + r;
+                    if (ci < cin && co < cout)
+                        part[((seg * kNumPaths + p) * cin + ci) * cout + co] = acc[pl][r];
+                }
+            }
+        });
+    }
+}
+
+__global__ __launch_bounds__(kTpBlock) void tp_weighted_bwd_w_mfma_kernel(
+    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
+    float* __restrict__ part, int64_t n, int cin, int cout, int64_t rows_per_seg) {
+    __shared__ __attribute__((aligned(16))) float sT[kBwdMaxSlots * 256];
+    __shared__ float sY[kTile * 16];
+    switch (blockIdx.z % kBwdGroups) {
+        case 0: bwd_w_group<0>(x, y, g, part, n, cin, cout, rows_per_seg, sT, sY); break;
+        case 1: bwd_w_group<1>(x, y, g, part, n, cin, cout, rows_per_seg, sT, sY); break;
+        default: bwd_w_group<2>(x, y, g, part, n, cin, cout, rows_per_seg, sT, sY); break;
+    }
+}
+
+// grad_x and grad_y for C_out above the LDS tile of the MFMA kernel (128):
+// h[n,ci,q] = sum_co W[path(q),ci,co] g[n,co,out(q)], gx = CG^T(h, y),
+// gy = sum_ci CG^T(h, x).  One thread per (row, ci); per-ci gy partials are
+// reduced in a fixed order.
 constexpr int kBRows = 2;
 __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
@@ -227,77 +742,6 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
     }
 }
 
-// grad_W partials over a segment of rows:
-//   part[seg, p, ci, co] = sum_{n in seg} sum_{q in p} T[n,ci,q] * g[n,co,out(q)]
-// Block = (ci chunk of 4, segment); thread = (ci_local, co).
-constexpr int kGwCi = 4;
-__global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_w_partial_kernel(
-    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
-    float* __restrict__ part, int64_t n, int cin, int cout, int64_t rows_per_seg) {
-    __shared__ float sT[kGwCi * kNumSlots];
-    __shared__ float sx[kGwCi * 16];
-    __shared__ float sy[16];
-    const int ci0 = blockIdx.x * kGwCi;
-    const int seg = blockIdx.y;
-    const int64_t r0 = (int64_t)seg * rows_per_seg;
-    const int64_t r1 = min<int64_t>(n, r0 + rows_per_seg);
-    const int tid = threadIdx.x;
-    const int cw = min(kGwCi, cin - ci0);
-    // thread -> (ci_local, co) pairs, looping when 4*cout > 256
-    const int npairs = cw * cout;
-    constexpr int kMaxPairs = 4;  // supports cout <= 256
-    float acc[kMaxPairs][kNumPaths];
-#pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j)
-#pragma unroll
-        for (int p = 0; p < kNumPaths; ++p) acc[j][p] = 0.0f;
-    for (int64_t row = r0; row < r1; ++row) {
-        __syncthreads();
-        for (int i = tid; i < cw * 16; i += kTpBlock) sx[i] = x[(row * cin + ci0) * 16 + i];
-        if (tid < 16) sy[tid] = y[row * 16 + tid];
-        __syncthreads();
-        if (tid < cw) {
-            float a[16], b[16], t[kNumSlots];
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                a[k] = sx[tid * 16 + k];
-                b[k] = sy[k];
-            }
-            tp_per_path(a, b, t);
-#pragma unroll
-            for (int q = 0; q < kNumSlots; ++q) sT[tid * kNumSlots + q] = t[q];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < kMaxPairs; ++j) {
-            const int pair = tid + j * kTpBlock;
-            if (pair < npairs) {
-                const int cl = pair / cout, co = pair - cl * cout;
-                const float* gr = g + (row * cout + co) * 16;
-                float gv[16];
-#pragma unroll
-                for (int k = 0; k < 16; ++k) gv[k] = gr[k];
-                const float* Tq = sT + cl * kNumSlots;
-                static_for<kNumSlots>([&](auto qq) {
-                    constexpr int q = decltype(qq)::value;
-                    acc[j][kSlotPath[q]] = fmaf(Tq[q], gv[kSlotOut[q]], acc[j][kSlotPath[q]]);
-                });
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) {
-        const int pair = tid + j * kTpBlock;
-        if (pair < npairs) {
-            const int cl = pair / cout, co = pair - cl * cout;
-            float* dst = part + (int64_t)seg * kNumPaths * cin * cout;
-#pragma unroll
-            for (int p = 0; p < kNumPaths; ++p)
-                dst[((int64_t)p * cin + ci0 + cl) * cout + co] = acc[j][p];
-        }
-    }
-}
-
 // gW[i] = sum_s part[s, i] in ascending s (deterministic).
 __global__ __launch_bounds__(kTpBlock) void reduce_segments_kernel(const float* __restrict__ part,
                                                                    float* __restrict__ out,
@@ -314,11 +758,14 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t count) {
     if (i < count) p[i] = 0.0f;
 }
 
-static int64_t gw_rows_per_seg(int64_t n, int cin) {
-    const int64_t cchunks = ceil_div(cin, kGwCi);
-    const int64_t segs = std::max<int64_t>(1, 1024 / cchunks);
-    const int64_t rps = ceil_div(n, segs);
-    return std::max<int64_t>(rps, 32);
+// Row segments of the grad_W reduction: a fixed function of N (not of the
+// device), so results are the same on every GPU.
+constexpr int64_t kGwMaxSegments = 96;
+static int64_t gw_segments(int64_t n) {
+    return std::max<int64_t>(1, std::min<int64_t>(kGwMaxSegments, ceil_div(n, kTile)));
+}
+static int64_t gw_rows_per_seg(int64_t n) {
+    return ceil_div(ceil_div(n, kTile), gw_segments(n)) * kTile;
 }
 
 }  // namespace bmhip
@@ -358,24 +805,31 @@ extern "C" int batteries_tensor_product_l3(const float* input1, const float* inp
                                            int C_in, int C_out, hipStream_t stream) {
     if (N < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
-    tp_weighted_forward_kernel<<<(unsigned)ceil_div(N, kWRows), kTpBlock, 0, stream>>>(
-        input1, input2, weights, output, N, C_in, C_out);
+    if (ceil_div(N, kTile) > INT32_MAX || ceil_div(C_out, 64) > 65535) return BM_ERR_ARG;
+    if ((int64_t)kNumPaths * C_in * C_out * 4 > INT32_MAX) return BM_ERR_ARG;  // W via 32-bit offsets
+    if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(output)) & 15)
+        return BM_ERR_ARG;
+    dim3 grid((unsigned)ceil_div(N, kTile), (unsigned)ceil_div(C_out, 64), kFwdGroups);
+    tp_weighted_fwd_mfma_kernel<<<grid, kTpBlock, 0, stream>>>(input1, input2, weights, output, N,
+                                                               C_in, C_out);
     return (int)hipGetLastError();
 }
 
+// Workspace of the weighted backward: grad_y partials of the three path groups
+// [3][N][16], then grad_W partials of the row segments [S][34][C_in][C_out].
 extern "C" size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in,
                                                                     int C_out) {
     if (N <= 0 || C_in <= 0 || C_out <= 0) return 0;
-    const int64_t rps = gw_rows_per_seg(N, C_in);
-    const int64_t segs = ceil_div(N, rps);
-    return (size_t)(segs * kNumPaths * (int64_t)C_in * C_out) * sizeof(float);
+    const size_t gy = (size_t)kBwdGroups * (size_t)N * 16;
+    const size_t gw = (size_t)gw_segments(N) * kNumPaths * (size_t)C_in * (size_t)C_out;
+    return (gy + gw) * sizeof(float);
 }
 
 extern "C" int batteries_tensor_product_backward_l3(
     const float* input1, const float* input2, const float* weights, const float* grad_output,
     float* grad_input1, float* grad_input2, float* grad_weights, int64_t N, int C_in, int C_out,
     void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (N < 0 || C_in <= 0 || C_out <= 0 || C_out > 256) return BM_ERR_ARG;
+    if (N < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
     if (N == 0) {
         if (grad_weights) {
             const int64_t count = (int64_t)kNumPaths * C_in * C_out;
@@ -385,29 +839,57 @@ extern "C" int batteries_tensor_product_backward_l3(
         }
         return BM_OK;
     }
+    if (ceil_div(N, kTile) > INT32_MAX) return BM_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(grad_output)) & 15)
+        return BM_ERR_ARG;
+    const size_t need = batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out);
+    if ((grad_input2 || grad_weights) && (!workspace || workspace_bytes < need))
+        return BM_ERR_WORKSPACE;
+    float* gy_part = static_cast<float*>(workspace);
+    float* gw_part = gy_part ? gy_part + (size_t)kBwdGroups * N * 16 : nullptr;
     if (grad_input1 || grad_input2) {
-        const size_t smem =
-            sizeof(float) * ((size_t)kBRows * C_out * 16 + (size_t)kBRows * C_in * 16 + kBRows * 16);
-        if (smem > 64 * 1024) return BM_ERR_ARG;
-        tp_weighted_backward_xy_kernel<<<(unsigned)ceil_div(N, kBRows), kTpBlock, smem, stream>>>(
-            input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return (int)e;
+        float* gyp = grad_input2 ? gy_part : nullptr;
+        if (C_out <= 128 && (int64_t)kNumPaths * C_in * C_out * 4 <= INT32_MAX) {
+            const int nw = (int)std::min<int64_t>(4, ceil_div(C_in, 16));
+            dim3 grid((unsigned)ceil_div(N, kTile), 1, kBwdGroups);
+            if (C_out <= 64)
+                tp_weighted_bwd_xy_mfma_kernel<64><<<grid, 64 * nw, 0, stream>>>(
+                    input1, input2, weights, grad_output, grad_input1, gyp, N, C_in, C_out);
+            else
+                tp_weighted_bwd_xy_mfma_kernel<128><<<grid, 64 * nw, 0, stream>>>(
+                    input1, input2, weights, grad_output, grad_input1, gyp, N, C_in, C_out);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return (int)e;
+            if (grad_input2) {
+                const int64_t count = N * 16;
+                sum_groups_kernel<<<(unsigned)ceil_div(count, kTpBlock), kTpBlock, 0, stream>>>(
+                    gy_part, grad_input2, count);
+                e = hipGetLastError();
+                if (e != hipSuccess) return (int)e;
+            }
+        } else {
+            const size_t smem = sizeof(float) *
+                                ((size_t)kBRows * C_out * 16 + (size_t)kBRows * C_in * 16 + kBRows * 16);
+            if (smem > 64 * 1024) return BM_ERR_ARG;
+            tp_weighted_backward_xy_kernel<<<(unsigned)ceil_div(N, kBRows), kTpBlock, smem, stream>>>(
+                input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return (int)e;
+        }
     }
     if (grad_weights) {
-        const size_t need = batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out);
-        if (!workspace || workspace_bytes < need) return BM_ERR_WORKSPACE;
-        const int64_t rps = gw_rows_per_seg(N, C_in);
-        const int64_t segs = ceil_div(N, rps);
-        float* part = static_cast<float*>(workspace);
-        dim3 grid((unsigned)ceil_div(C_in, kGwCi), (unsigned)segs);
-        tp_weighted_backward_w_partial_kernel<<<grid, kTpBlock, 0, stream>>>(
-            input1, input2, grad_output, part, N, C_in, C_out, rps);
+        const int64_t segs = gw_segments(N);
+        const int64_t rps = gw_rows_per_seg(N);
+        if (ceil_div(C_in, 16) > 65535 || ceil_div(C_out, 64) * kBwdGroups > 65535) return BM_ERR_ARG;
+        dim3 grid((unsigned)segs, (unsigned)ceil_div(C_in, 16),
+                  (unsigned)(ceil_div(C_out, 64) * kBwdGroups));
+        tp_weighted_bwd_w_mfma_kernel<<<grid, kTpBlock, 0, stream>>>(input1, input2, grad_output,
+                                                                     gw_part, N, C_in, C_out, rps);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return (int)e;
         const int64_t count = (int64_t)kNumPaths * C_in * C_out;
         reduce_segments_kernel<<<(unsigned)ceil_div(count, kTpBlock), kTpBlock, 0, stream>>>(
-            part, grad_weights, count, (int)segs);
+            gw_part, grad_weights, count, (int)segs);
         e = hipGetLastError();
         if (e != hipSuccess) return (int)e;
     }

@@ -110,6 +110,64 @@ def cpu_baseline(torch, w, gpu_out):
     }
 
 
+def event_ms(torch, fn, reps):
+    """Mean device time per call of fn() over `reps` calls, HIP events on the current stream."""
+    fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def other_configs(torch, bm, dev):
+    """configs[0..2] of the survey, timed on this GPU (parity cases; reported beside the
+    headline).  Inputs as the survey states (seeds 0, 1, 2); algorithmic work per unit:
+    SH 76 B/edge, TP simple 192 B/row, weighted TP fwd E(312 Ci Co + 1222 Ci) flop,
+    weighted TP bwd E(624 Ci Co + 3666 Ci) flop."""
+    res = {}
+    g = torch.Generator().manual_seed(0)
+    E1 = 20000
+    v = torch.randn(E1, 3, generator=g)
+    v = (v / v.norm(dim=1, keepdim=True)).to(dev)
+    x1 = torch.randn(E1, 16, generator=g).to(dev)
+    y1 = bm.spherical_harmonics(v, 3)
+    t = event_ms(torch, lambda: bm.spherical_harmonics(v, 3), 200)
+    res["cfg0_sh_l3_ms"] = round(t, 5)
+    res["cfg0_sh_l3_GBs"] = round(E1 * 76 / (t * 1e-3) / 1e9, 1)
+    t = event_ms(torch, lambda: bm.tensor_product_simple(x1, y1), 200)
+    res["cfg0_tp_simple_ms"] = round(t, 5)
+    res["cfg0_tp_simple_GBs"] = round(E1 * 192 / (t * 1e-3) / 1e9, 1)
+
+    def weighted_inputs(seed, n, ci, co):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(n, ci, 16, generator=g)
+        vv = torch.randn(n, 3, generator=g)
+        y = bm.spherical_harmonics((vv / vv.norm(dim=1, keepdim=True)).to(dev), 3)
+        w = torch.randn(34, ci, co, generator=g) / math.sqrt(ci)
+        return x.to(dev), y, w.to(dev), g
+
+    x2, y2, w2, _ = weighted_inputs(1, 1000, 32, 64)
+    t = event_ms(torch, lambda: bm.tensor_product(x2, y2, w2), 50)
+    f = 1000 * (312 * 32 * 64 + 1222 * 32)
+    res["cfg1_tp_weighted_fwd_ms"] = round(t, 5)
+    res["cfg1_tp_weighted_fwd_TFLOPs"] = round(f / (t * 1e-3) / 1e12, 2)
+    res["cfg1_tp_weighted_fwd_mfma_frac"] = round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+
+    x3, y3, w3, g3 = weighted_inputs(2, 20000, 32, 64)
+    go = torch.randn(20000, 64, 16, generator=g3).to(dev)
+    t = event_ms(torch, lambda: bm.tensor_product_backward(x3, y3, w3, go, True, True, True), 10)
+    f = 20000 * (624 * 32 * 64 + 3666 * 32)
+    res["cfg2_tp_weighted_bwd_ms"] = round(t, 5)
+    res["cfg2_tp_weighted_bwd_TFLOPs"] = round(f / (t * 1e-3) / 1e12, 2)
+    res["cfg2_tp_weighted_bwd_mfma_frac"] = round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+    return res
+
+
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     passes recorded in profiles/hbm_traffic.txt (scaled by the copy calibration)."""
@@ -193,6 +251,7 @@ def main():
     extra["graph_build_ms"] = round(time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS)), 4)
     extra["index_order_kernel_ms"] = round(time_call(torch, lambda: graph.sh_tp_scatter_index_order(w["x"]), 20), 4)
     extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
+    extra.update(other_configs(torch, bm, dev))
 
     res = {
         "metric": METRIC,

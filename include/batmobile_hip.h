@@ -85,13 +85,14 @@ int batteries_tensor_product_simple_backward_l3(const float* input1, const float
 int batteries_tensor_product_l3(const float* input1, const float* input2, const float* weights,
                                 float* output, int64_t N, int C_in, int C_out, hipStream_t stream);
 
-/* Workspace for batteries_tensor_product_backward_l3 with grad_weights != NULL. */
+/* Workspace for batteries_tensor_product_backward_l3 when grad_input2 or grad_weights
+ * is requested (grad_input1 alone needs none). */
 size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in, int C_out);
 
 /* Exact adjoint of batteries_tensor_product_l3.  Any of grad_input1 [N,C_in,16],
  * grad_input2 [N,16], grad_weights [34,C_in,C_out] may be NULL (not computed).
  * grad_weights is a deterministic reduction over rows; N = 0 gives zeros.
- * C_out <= 256.  Replaces batteries::tensor_product_backward_l3,
+ * input1 and grad_output 16-byte aligned.  Replaces batteries::tensor_product_backward_l3,
  * src/tensor_product/tensor_product_backward.cu:948-1005 (bound at
  * python/bindings.cpp:325-393). */
 int batteries_tensor_product_backward_l3(const float* input1, const float* input2,
