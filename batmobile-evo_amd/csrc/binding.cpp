@@ -265,7 +265,7 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> tensor_product_backward(
     const c10::DeviceGuard guard(input1.device());
     torch::Tensor ws;
     size_t wsb = 0;
-    if (needs_input2_grad || needs_weights_grad) {  // grad_y partials and grad_W partials
+    if (needs_weights_grad) {  // grad_W partials of the row segments
         wsb = batteries_tensor_product_backward_workspace_bytes(N, (int)C_in, (int)C_out);
         ws = torch::empty({(int64_t)((wsb + 3) / 4)}, opt);
     }

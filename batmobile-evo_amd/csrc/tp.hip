@@ -359,173 +359,152 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_fwd_mfma_kernel(
     }
 }
 
-// ---- backward: grad_x and per-group grad_y ----------------------------------
-// Workgroup: 16 rows x one l1 group G; wave w takes input-channel tiles
-// w, w + nw, ...  The grad_output tile of the 16 rows is staged in LDS as
-// sG[o][co/4][row][co%4] (plane stride PS): lane (row, g) reads
-// g[row][cb + 4g .. +3][o] as one float4.  Per path p of the group:
+// ---- backward: grad_x and grad_y ---------------------------------------------
+// Workgroup: 16 rows; its waves take (l1 group G, input-channel tile) units
+// u = wave, wave + nwave, ... with G = u % 3, tile = u / 3.  The grad_output
+// tile of the 16 rows is staged once in LDS as sG[o][co/4][row][co%4] (plane
+// stride PS): lane (row, g) reads g[row][cb + 4g .. +3][o] as one float4.
+// Per path p of the group:
 //   D[ci][row] = h_p[row][ci][m_out] = sum_co W[p][ci][co] (A) g[row][co][o] (B)
 // lands in lane (row = lane % 16, ci = 4 g + r), which then applies the CG
-// entries of p to its own 4 channels: gx columns of the group and a grad_y
-// partial.  The partials are summed over lanes and waves in a fixed order.
+// entries of p to its own 4 channels: the group's gx columns, and a grad_y
+// partial in gyp.  The partials are summed over lanes and waves in a fixed order.
 template <int G, int KCO>
-__device__ __forceinline__ void bwd_xy_group(const float* __restrict__ x,
-                                             const float* __restrict__ y,
-                                             const float* __restrict__ w, float* __restrict__ gx,
-                                             float* __restrict__ gy_part, int64_t n, int cin,
-                                             int cout, float* sG) {
+__device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const float* yb,
+                                            const __amdgpu_buffer_rsrc_t wr, float* __restrict__ gx,
+                                            int64_t n, int cin, int cout, int ct, const float* sG,
+                                            float* gyp) {
     constexpr int PS = KCO * 16 + 4;
     constexpr int A0 = bwd_a0(G), NA = bwd_na(G);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int g4 = lane >> 4, i16 = lane & 15;
-    const int64_t row0 = (int64_t)blockIdx.x * kTile;
-    const int64_t row = row0 + i16;
+    const int64_t row = (int64_t)blockIdx.x * kTile + i16;
     const bool row_ok = row < n;
     const int64_t row_c = row_ok ? row : n - 1;  // clamped row for unconditional loads
     const int wpath_bytes = cin * cout * 4;
-    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
-    float yb[16];
-    load16(y, row_c * 16, yb);  // rows >= n only reach discarded outputs
-    float gyp[16];
+    const int ci0 = ct * 16;
+    float xa[4][NA], gxa[4][NA];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) gyp[k] = 0.0f;
-
-    for (int ct = wv; ct * 16 < cin; ct += nw) {
-        const int ci0 = ct * 16;
-        float xa[4][NA], gxa[4][NA];
+    for (int r = 0; r < 4; ++r) {
+        const int ci = ci0 + 4 * g4 + r;
+        const float* xr = x + (row_c * cin + min(ci, cin - 1)) * 16 + A0;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            xa[r][a] = mask0(xr[a], ci < cin);  // meets h rows of channels >= cin
+            gxa[r][a] = 0.0f;
+        }
+    }
+    // A operands W[p][ciA][cb + 4 g4 + s] of one path, all KCO/16 channel chunks,
+    // through buffer loads (lane offset in a VGPR, path offset p * cin * cout in
+    // an SGPR).  Clamped addresses: channels >= cin give h rows that meet x = 0 or
+    // are discarded, co >= cout meets the zero-padded g tile.  The next path's
+    // operands are loaded while this path's MFMAs and CG contraction run.
+    const int ciA = ci0 + i16;
+    const int wrow = min(ciA, cin - 1) * cout;
+    constexpr int NCB = KCO / 16;
+    auto load_w = [&](int p, float4* dst) {
+        const int so = p * wpath_bytes;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            float a[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                a[s] = buffer_ld(wr, (wrow + min(cb * 16 + 4 * g4 + s, cout - 1)) * 4, so);
+            dst[cb] = make_float4(a[0], a[1], a[2], a[3]);
+        }
+    };
+    // One path per iteration of a loop that is not unrolled: each path is a basic
+    // block of its own, so instruction selection cannot hoist every path's MFMAs
+    // ahead of the CG contractions (which would keep all of the group's h
+    // accumulators live at once).
+    constexpr int NPG = bwd_group_paths(G);
+    constexpr bool PF = KCO <= 64;  // next-path prefetch (registers allow it up to 64 channels)
+    float4 wcur[NCB], wnxt[NCB];
+    constexpr int p0 = bwd_path_at(0, G);
+    load_w(p0, wcur);
+#pragma clang loop unroll(disable)
+    for (int k = 0; k < NPG; ++k) {
+        // y through an empty asm each iteration: the products c * y[b] are then
+        // formed per path instead of being hoisted out of the loop (some 200
+        // loop-invariant values that would not fit in registers)
+        float yk[16];
+#pragma unroll
+        for (int b = 0; b < 16; ++b) yk[b] = yb[b];
+        asm volatile("" : "+v"(yk[0]), "+v"(yk[1]), "+v"(yk[2]), "+v"(yk[3]), "+v"(yk[4]),
+                          "+v"(yk[5]), "+v"(yk[6]), "+v"(yk[7]), "+v"(yk[8]), "+v"(yk[9]),
+                          "+v"(yk[10]), "+v"(yk[11]), "+v"(yk[12]), "+v"(yk[13]),
+                          "+v"(yk[14]), "+v"(yk[15]));
+        static_for<NPG>([&](auto kk) {
+            constexpr int kc = decltype(kk)::value;
+            if (k == kc) {
+                constexpr int p = bwd_path_at(kc, G);
+                if constexpr (!PF && kc > 0) load_w(p, wcur);
+                if constexpr (PF && kc + 1 < NPG) {
+                    constexpr int pn = bwd_path_at(kc + 1, G);
+                    load_w(pn, wnxt);
+                }
+                constexpr int lo = kPathL[p][2];
+                constexpr int NM = 2 * lo + 1;
+                v4f h[NM];
+#pragma unroll
+                for (int m = 0; m < NM; ++m) h[m] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+                    if (cb * 16 < cout) {  // uniform
+                        static_for<NM>([&](auto mm) {
+                            constexpr int m = decltype(mm)::value;
+                            const float4 b4 = *reinterpret_cast<const float4*>(
+                                sG + (lo * lo + m) * PS + (cb * 4 + g4) * 64 + i16 * 4);
+                            h[m] = mfma4(wcur[cb], b4, h[m]);
+                        });
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // bound the B reads in flight
+                }
+                static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                    constexpr CGEntry e = kCG[kPathEntry[p] + decltype(ee)::value];
+                    constexpr int m = e.o - lo * lo;
+                    constexpr int ai = e.a - A0;
+                    const float cy = e.c * yk[e.b];
+                    float sacc = 0.0f;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        gxa[r][ai] = fmaf(cy, h[m][r], gxa[r][ai]);
+                        sacc = fmaf(xa[r][ai], h[m][r], sacc);
+                    }
+                    gyp[e.b] = fmaf(e.c, sacc, gyp[e.b]);
+                });
+                if constexpr (PF && kc + 1 < NPG) {
+#pragma unroll
+                    for (int cb = 0; cb < NCB; ++cb) wcur[cb] = wnxt[cb];
+                }
+            }
+        });
+    }
+    if (gx && row_ok) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int ci = ci0 + 4 * g4 + r;
-            const float* xr = x + (row_c * cin + min(ci, cin - 1)) * 16 + A0;
+            if (ci < cin)
 #pragma unroll
-            for (int a = 0; a < NA; ++a) {
-                xa[r][a] = mask0(xr[a], ci < cin);  // meets h rows of channels >= cin
-                gxa[r][a] = 0.0f;
-            }
+                for (int a = 0; a < NA; ++a) gx[(row * cin + ci) * 16 + A0 + a] = gxa[r][a];
         }
-        // A operands W[p][ciA][cb + 4 g4 + s] of one path, all KCO/16 channel
-        // chunks (clamped addresses: channels >= cin give h rows that meet
-        // x = 0 or are discarded, co >= cout meets the zero-padded g tile).
-        // The next path's operands are loaded while this path's MFMAs and CG
-        // contraction run.
-        // Buffer loads: lane offset in a VGPR, path offset p * cin * cout in an SGPR.
-        const int ciA = ci0 + i16;
-        const int wrow = min(ciA, cin - 1) * cout;
-        constexpr int NCB = KCO / 16;
-        auto load_w = [&](int p, float4* dst) {
-            const int so = p * wpath_bytes;
-#pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) {
-                float a[4];
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    a[s] = buffer_ld(wr, (wrow + min(cb * 16 + 4 * g4 + s, cout - 1)) * 4, so);
-                dst[cb] = make_float4(a[0], a[1], a[2], a[3]);
-            }
-        };
-        // One path per iteration of a loop that is not unrolled: each path is a
-        // basic block of its own, so instruction selection cannot hoist every
-        // path's MFMAs ahead of the CG contractions (which would keep all of
-        // the group's h accumulators live at once).
-        constexpr int NPG = bwd_group_paths(G);
-        float4 wcur[NCB], wnxt[NCB];
-        constexpr int p0 = bwd_path_at(0, G);
-        load_w(p0, wcur);
-#pragma clang loop unroll(disable)
-        for (int k = 0; k < NPG; ++k) {
-            // y through an empty asm each iteration: the products c * y[b] are then
-            // formed per path instead of being hoisted out of the loops (some 200
-            // loop-invariant values that would not fit in registers)
-            float yk[16];
-#pragma unroll
-            for (int b = 0; b < 16; ++b) yk[b] = yb[b];
-            asm volatile("" : "+v"(yk[0]), "+v"(yk[1]), "+v"(yk[2]), "+v"(yk[3]), "+v"(yk[4]),
-                              "+v"(yk[5]), "+v"(yk[6]), "+v"(yk[7]), "+v"(yk[8]), "+v"(yk[9]),
-                              "+v"(yk[10]), "+v"(yk[11]), "+v"(yk[12]), "+v"(yk[13]),
-                              "+v"(yk[14]), "+v"(yk[15]));
-            static_for<NPG>([&](auto kk) {
-                constexpr int kc = decltype(kk)::value;
-                if (k == kc) {
-                    constexpr int p = bwd_path_at(kc, G);
-                    if constexpr (kc + 1 < NPG) {
-                        constexpr int pn = bwd_path_at(kc + 1, G);
-                        load_w(pn, wnxt);
-                    }
-                    constexpr int lo = kPathL[p][2];
-                    constexpr int NM = 2 * lo + 1;
-                    v4f h[NM];
-#pragma unroll
-                    for (int m = 0; m < NM; ++m) h[m] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int cb = 0; cb < NCB; ++cb) {
-                        if (cb * 16 < cout) {  // uniform
-                            static_for<NM>([&](auto mm) {
-                                constexpr int m = decltype(mm)::value;
-                                const float4 b4 = *reinterpret_cast<const float4*>(
-                                    sG + (lo * lo + m) * PS + (cb * 4 + g4) * 64 + i16 * 4);
-                                h[m] = mfma4(wcur[cb], b4, h[m]);
-                            });
-                        }
-                        __builtin_amdgcn_sched_barrier(0);  // bound the B reads in flight
-                    }
-                    static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
-                        constexpr CGEntry e = kCG[kPathEntry[p] + decltype(ee)::value];
-                        constexpr int m = e.o - lo * lo;
-                        constexpr int ai = e.a - A0;
-                        const float cy = e.c * yk[e.b];
-                        float sacc = 0.0f;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            gxa[r][ai] = fmaf(cy, h[m][r], gxa[r][ai]);
-                            sacc = fmaf(xa[r][ai], h[m][r], sacc);
-                        }
-                        gyp[e.b] = fmaf(e.c, sacc, gyp[e.b]);
-                    });
-                    if constexpr (kc + 1 < NPG) {
-#pragma unroll
-                        for (int cb = 0; cb < NCB; ++cb) wcur[cb] = wnxt[cb];
-                    }
-                }
-            });
-        }
-        if (gx && row_ok) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int ci = ci0 + 4 * g4 + r;
-                if (ci < cin)
-#pragma unroll
-                    for (int a = 0; a < NA; ++a) gx[(row * cin + ci) * 16 + A0 + a] = gxa[r][a];
-            }
-        }
-    }
-    if (!gy_part) return;  // uniform over the workgroup
-    __syncthreads();       // sG is reused for the reduction
-    float* sRed = sG;      // [wave][g][row][16]
-#pragma unroll
-    for (int k = 0; k < 16; ++k) sRed[((wv * 4 + g4) * 16 + i16) * 16 + k] = gyp[k];
-    __syncthreads();
-    for (int i = tid; i < kTile * 16; i += blockDim.x) {
-        const int rr = i >> 4, k = i & 15;
-        float sum = 0.0f;
-        for (int v = 0; v < nw; ++v)
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) sum += sRed[((v * 4 + gg) * 16 + rr) * 16 + k];
-        if (row0 + rr < n) gy_part[((int64_t)G * n + row0 + rr) * 16 + k] = sum;
     }
 }
 
 template <int KCO>
-__global__ __launch_bounds__(kTpBlock) void tp_weighted_bwd_xy_mfma_kernel(
+__global__ __launch_bounds__(512) void tp_weighted_bwd_xy_mfma_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
-    const float* __restrict__ g, float* __restrict__ gx, float* __restrict__ gy_part, int64_t n,
+    const float* __restrict__ g, float* __restrict__ gx, float* __restrict__ gy, int64_t n,
     int cin, int cout) {
     constexpr int PS = KCO * 16 + 4;
     __shared__ __attribute__((aligned(16))) float sG[kTile * PS];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nwave = blockDim.x >> 6;
+    const int g4 = lane >> 4, i16 = lane & 15;
     const int64_t row0 = (int64_t)blockIdx.x * kTile;
     const int cout16 = (cout + 15) & ~15;  // MFMA chunks read channels below cout16
     // stage g[row0 .. row0+15][co][o] (zeros past n and past cout)
-    for (int i = threadIdx.x; i < kTile * cout16 * 4; i += blockDim.x) {
+    for (int i = tid; i < kTile * cout16 * 4; i += blockDim.x) {
         const int rr = i / (cout16 * 4), rem = i - rr * cout16 * 4;
         const int co = rem >> 2, j = rem & 3;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -538,22 +517,37 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_bwd_xy_mfma_kernel(
         d[(4 * j + 3) * PS] = v.w;
     }
     __syncthreads();
-    switch (blockIdx.z) {
-        case 0: bwd_xy_group<0, KCO>(x, y, w, gx, gy_part, n, cin, cout, sG); break;
-        case 1: bwd_xy_group<1, KCO>(x, y, w, gx, gy_part, n, cin, cout, sG); break;
-        default: bwd_xy_group<2, KCO>(x, y, w, gx, gy_part, n, cin, cout, sG); break;
+    const int64_t row_c = min<int64_t>(row0 + i16, n - 1);
+    float yb[16];
+    load16(y, row_c * 16, yb);  // rows >= n only reach discarded outputs
+    float gyp[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gyp[k] = 0.0f;
+    const int wpath_bytes = cin * cout * 4;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
+    const int units = kBwdGroups * ((cin + 15) / 16);
+    for (int u = wv; u < units; u += nwave) {
+        const int ct = u / kBwdGroups;
+        switch (u % kBwdGroups) {
+            case 0: bwd_xy_unit<0, KCO>(x, yb, wr, gx, n, cin, cout, ct, sG, gyp); break;
+            case 1: bwd_xy_unit<1, KCO>(x, yb, wr, gx, n, cin, cout, ct, sG, gyp); break;
+            default: bwd_xy_unit<2, KCO>(x, yb, wr, gx, n, cin, cout, ct, sG, gyp); break;
+        }
     }
-}
-
-// gy[i] = part[0][i] + part[1][i] + part[2][i] (fixed order)
-__global__ __launch_bounds__(kTpBlock) void sum_groups_kernel(const float* __restrict__ part,
-                                                              float* __restrict__ out,
-                                                              int64_t count) {
-    const int64_t i = (int64_t)blockIdx.x * kTpBlock + threadIdx.x;
-    if (i >= count) return;
-    float s = part[i];
-    for (int G = 1; G < kBwdGroups; ++G) s += part[(int64_t)G * count + i];
-    out[i] = s;
+    if (!gy) return;   // uniform over the workgroup
+    __syncthreads();   // sG is reused for the reduction
+    float* sRed = sG;  // [wave][g][row][16]
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sRed[((wv * 4 + g4) * 16 + i16) * 16 + k] = gyp[k];
+    __syncthreads();
+    for (int i = tid; i < kTile * 16; i += blockDim.x) {
+        const int rr = i >> 4, k = i & 15;
+        float sum = 0.0f;
+        for (int v = 0; v < nwave; ++v)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) sum += sRed[((v * 4 + gg) * 16 + rr) * 16 + k];
+        if (row0 + rr < n) gy[(row0 + rr) * 16 + k] = sum;
+    }
 }
 
 // ---- backward: grad_W partials over row segments ----------------------------
@@ -817,12 +811,12 @@ extern "C" int batteries_tensor_product_l3(const float* input1, const float* inp
 
 // Workspace of the weighted backward: grad_y partials of the three path groups
 // [3][N][16], then grad_W partials of the row segments [S][34][C_in][C_out].
+// Workspace of the weighted backward: grad_W partials of the row segments
+// [S][34][C_in][C_out] (grad_input1 / grad_input2 alone need none).
 extern "C" size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in,
                                                                     int C_out) {
     if (N <= 0 || C_in <= 0 || C_out <= 0) return 0;
-    const size_t gy = (size_t)kBwdGroups * (size_t)N * 16;
-    const size_t gw = (size_t)gw_segments(N) * kNumPaths * (size_t)C_in * (size_t)C_out;
-    return (gy + gw) * sizeof(float);
+    return (size_t)gw_segments(N) * kNumPaths * (size_t)C_in * (size_t)C_out * sizeof(float);
 }
 
 extern "C" int batteries_tensor_product_backward_l3(
@@ -843,30 +837,22 @@ extern "C" int batteries_tensor_product_backward_l3(
     if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(grad_output)) & 15)
         return BM_ERR_ARG;
     const size_t need = batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out);
-    if ((grad_input2 || grad_weights) && (!workspace || workspace_bytes < need))
-        return BM_ERR_WORKSPACE;
-    float* gy_part = static_cast<float*>(workspace);
-    float* gw_part = gy_part ? gy_part + (size_t)kBwdGroups * N * 16 : nullptr;
+    if (grad_weights && (!workspace || workspace_bytes < need)) return BM_ERR_WORKSPACE;
+    float* gw_part = static_cast<float*>(workspace);
     if (grad_input1 || grad_input2) {
-        float* gyp = grad_input2 ? gy_part : nullptr;
         if (C_out <= 128 && (int64_t)kNumPaths * C_in * C_out * 4 <= INT32_MAX) {
-            const int nw = (int)std::min<int64_t>(4, ceil_div(C_in, 16));
-            dim3 grid((unsigned)ceil_div(N, kTile), 1, kBwdGroups);
+            // one wave per (path group, 16-channel tile), at most 8 per workgroup
+            const int units = kBwdGroups * (int)ceil_div(C_in, 16);
+            const int nwave = std::min(units, 8);
+            const unsigned grid = (unsigned)ceil_div(N, kTile);
             if (C_out <= 64)
-                tp_weighted_bwd_xy_mfma_kernel<64><<<grid, 64 * nw, 0, stream>>>(
-                    input1, input2, weights, grad_output, grad_input1, gyp, N, C_in, C_out);
+                tp_weighted_bwd_xy_mfma_kernel<64><<<grid, 64 * nwave, 0, stream>>>(
+                    input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
             else
-                tp_weighted_bwd_xy_mfma_kernel<128><<<grid, 64 * nw, 0, stream>>>(
-                    input1, input2, weights, grad_output, grad_input1, gyp, N, C_in, C_out);
+                tp_weighted_bwd_xy_mfma_kernel<128><<<grid, 64 * nwave, 0, stream>>>(
+                    input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return (int)e;
-            if (grad_input2) {
-                const int64_t count = N * 16;
-                sum_groups_kernel<<<(unsigned)ceil_div(count, kTpBlock), kTpBlock, 0, stream>>>(
-                    gy_part, grad_input2, count);
-                e = hipGetLastError();
-                if (e != hipSuccess) return (int)e;
-            }
         } else {
             const size_t smem = sizeof(float) *
                                 ((size_t)kBRows * C_out * 16 + (size_t)kBRows * C_in * 16 + kBRows * 16);

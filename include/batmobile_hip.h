@@ -85,8 +85,7 @@ int batteries_tensor_product_simple_backward_l3(const float* input1, const float
 int batteries_tensor_product_l3(const float* input1, const float* input2, const float* weights,
                                 float* output, int64_t N, int C_in, int C_out, hipStream_t stream);
 
-/* Workspace for batteries_tensor_product_backward_l3 when grad_input2 or grad_weights
- * is requested (grad_input1 alone needs none). */
+/* Workspace for batteries_tensor_product_backward_l3 with grad_weights != NULL. */
 size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in, int C_out);
 
 /* Exact adjoint of batteries_tensor_product_l3.  Any of grad_input1 [N,C_in,16],

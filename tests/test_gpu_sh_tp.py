@@ -107,7 +107,8 @@ def test_tp_simple_backward(bm, dev):
     assert normwise_err(gy.cpu(), wy) <= 1e-5
 
 
-@pytest.mark.parametrize("n,cin,cout", [(1000, 32, 64), (37, 3, 5), (64, 16, 16), (5, 64, 128)])
+@pytest.mark.parametrize("n,cin,cout", [(1000, 32, 64), (37, 3, 5), (64, 16, 16), (5, 64, 128),
+                                         (17, 40, 200)])
 def test_tp_weighted_forward(bm, dev, n, cin, cout):
     # (1000, 32, 64) is configs[1]: x ~ N(0,1), Y of normalised Gaussian vectors, W ~ N(0, 1/C_in)
     x = torch.randn(n, cin, 16, generator=gen(1))
@@ -129,7 +130,14 @@ def _tp_backward_oracle_chunked(x, y, w, g, chunk=2000):
     return np.concatenate(gx), np.concatenate(gy), gw
 
 
-@pytest.mark.parametrize("n,cin,cout", [(20000, 32, 64), (300, 5, 7), (1, 16, 16)])
+@pytest.mark.parametrize("n,cin,cout", [
+    (20000, 32, 64),   # configs[2]
+    (300, 5, 7),
+    (1, 16, 16),
+    (40, 20, 100),     # C_out in (64, 128]: the 128-channel grad_output tile
+    (20, 8, 160),      # C_out > 128: the per-(row, channel) grad_x / grad_y kernel
+    (33, 80, 24),      # 15 (group, channel-tile) units on 8 waves: waves loop over units
+])
 def test_tp_weighted_backward(bm, dev, n, cin, cout):
     # (20000, 32, 64) is configs[2]: upstream grad ~ N(0,1)
     x = torch.randn(n, cin, 16, generator=gen(21))
