@@ -123,68 +123,162 @@ __global__ void nl_sort_bins_kernel(const int64_t* __restrict__ bin_start, int* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Stencil passes (count, then write): one wave per home cell.  The atoms of the
+// 27 cells around it (reference order: dz, dy, dx from -1 to 1, atoms of a cell
+// in ascending index) are staged in LDS as (x, y, z, j); then for each home
+// atom i the lanes test 64 candidates at a time and a ballot gives every kept
+// pair its slot, so row i lists its neighbors in stencil order.  Candidate
+// lists longer than the LDS buffer are processed in chunks.
+// ---------------------------------------------------------------------------
+constexpr int kNlCap = 2048;  // candidates staged per chunk (32 KB)
+
 template <bool WRITE>
-__global__ void nl_stencil_kernel(const float* __restrict__ pos, BinCfg c, float rc2,
-                                  int self_loops, const int64_t* __restrict__ bin_start,
-                                  const int* __restrict__ order, int64_t* __restrict__ counts,
-                                  const int64_t* __restrict__ offsets, int* __restrict__ esrc,
-                                  int* __restrict__ edst, float* __restrict__ evec, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float pi[3] = {pos[i * 3], pos[i * 3 + 1], pos[i * 3 + 2]};
-    int b[3];
-    bin_coords(pi[0], pi[1], pi[2], c, b);
-    int64_t w = WRITE ? offsets[i] : 0;
-    int64_t cnt = 0;
-    for (int dz = -1; dz <= 1; ++dz)
-        for (int dy = -1; dy <= 1; ++dy)
-            for (int dx = -1; dx <= 1; ++dx) {
-                const int k = wrap_bin(b[0] + dx, c.nb[0]) + wrap_bin(b[1] + dy, c.nb[1]) * c.nb[0] +
-                              wrap_bin(b[2] + dz, c.nb[2]) * c.nb[0] * c.nb[1];
-                for (int64_t s = bin_start[k]; s < bin_start[k + 1]; ++s) {
-                    const int j = order[s];
-                    if (!self_loops && j == (int)i) continue;
-                    const float pj[3] = {pos[(int64_t)j * 3], pos[(int64_t)j * 3 + 1],
-                                         pos[(int64_t)j * 3 + 2]};
-                    float d[3];
-                    if (min_image(pi, pj, c, d) <= rc2) {
-                        if constexpr (WRITE) {
-                            esrc[w] = (int)i;
-                            edst[w] = j;
-                            evec[w * 3 + 0] = d[0];
-                            evec[w * 3 + 1] = d[1];
-                            evec[w * 3 + 2] = d[2];
-                            ++w;
-                        } else {
-                            ++cnt;
-                        }
+__global__ __launch_bounds__(64) void nl_cell_kernel(const float* __restrict__ pos, BinCfg c,
+                                                     float rc2, int self_loops,
+                                                     const int64_t* __restrict__ bin_start,
+                                                     const int* __restrict__ order,
+                                                     int64_t* __restrict__ counts,
+                                                     const int64_t* __restrict__ offsets,
+                                                     int* __restrict__ esrc, int* __restrict__ edst,
+                                                     float* __restrict__ evec) {
+    __shared__ float4 sCand[kNlCap];
+    __shared__ int sStart[27], sPre[28];
+    const int lane = threadIdx.x;
+    const int k = blockIdx.x;
+    const int bx = k % c.nb[0], by = (k / c.nb[0]) % c.nb[1], bz = k / (c.nb[0] * c.nb[1]);
+    int cnt_l = 0;
+    if (lane < 27) {
+        const int dz = lane / 9 - 1, dy = (lane / 3) % 3 - 1, dx = lane % 3 - 1;
+        const int kk = wrap_bin(bx + dx, c.nb[0]) + wrap_bin(by + dy, c.nb[1]) * c.nb[0] +
+                       wrap_bin(bz + dz, c.nb[2]) * c.nb[0] * c.nb[1];
+        const int64_t s0 = bin_start[kk];
+        sStart[lane] = (int)s0;
+        cnt_l = (int)(bin_start[kk + 1] - s0);
+    }
+    // exclusive prefix of the 27 counts (wave-level, lanes 0..26)
+    int incl = cnt_l;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+    }
+    if (lane < 27) sPre[lane] = incl - cnt_l;
+    if (lane == 26) sPre[27] = incl;
+    __syncthreads();
+    const int T = sPre[27];
+    const int home0 = sStart[13], H = sPre[14] - sPre[13];
+    if (H == 0) return;  // uniform: no home atoms
+
+    // stage candidates [base, base + n) of the concatenated 27-cell list
+    auto stage = [&](int base, int n) {
+        for (int t = lane; t < n; t += 64) {
+            const int idx = base + t;
+            int cell = 0;
+#pragma unroll
+            for (int q = 1; q < 27; ++q) cell += sPre[q] <= idx ? 1 : 0;
+            const int j = order[sStart[cell] + (idx - sPre[cell])];
+            sCand[t] = make_float4(pos[(int64_t)j * 3], pos[(int64_t)j * 3 + 1],
+                                   pos[(int64_t)j * 3 + 2], __int_as_float(j));
+        }
+    };
+    const bool one_chunk = T <= kNlCap;
+    if (one_chunk) {
+        stage(0, T);
+        __syncthreads();
+    }
+    for (int hh = 0; hh < H; ++hh) {
+        const int i = __builtin_amdgcn_readfirstlane(order[home0 + hh]);
+        const float pi[3] = {pos[(int64_t)i * 3], pos[(int64_t)i * 3 + 1], pos[(int64_t)i * 3 + 2]};
+        int64_t w = WRITE ? offsets[i] : 0;
+        for (int base = 0; base < T; base += kNlCap) {
+            const int n = min(kNlCap, T - base);
+            if (!one_chunk) {
+                __syncthreads();
+                stage(base, n);
+                __syncthreads();
+            }
+            for (int c0 = 0; c0 < n; c0 += 64) {
+                const int t = c0 + lane;
+                bool keep = false;
+                float d[3] = {0.f, 0.f, 0.f};
+                int j = 0;
+                if (t < n) {
+                    const float4 cj = sCand[t];
+                    j = __float_as_int(cj.w);
+                    const float pj[3] = {cj.x, cj.y, cj.z};
+                    keep = (self_loops || j != i) && min_image(pi, pj, c, d) <= rc2;
+                }
+                const uint64_t m = __ballot(keep);
+                if constexpr (WRITE) {
+                    if (keep) {
+                        const int64_t at = w + __popcll(m & ((1ull << lane) - 1ull));
+                        esrc[at] = i;
+                        edst[at] = j;
+                        evec[at * 3 + 0] = d[0];
+                        evec[at * 3 + 1] = d[1];
+                        evec[at * 3 + 2] = d[2];
                     }
                 }
+                w += __popcll(m);
             }
-    if constexpr (!WRITE) counts[i] = cnt;
+        }
+        if constexpr (!WRITE) {
+            if (lane == 0) counts[i] = w;
+        }
+    }
 }
 
-// sort each atom's neighbors by j (insertion sort; ~30 entries)
-__global__ void nl_sort_rows_kernel(const int64_t* __restrict__ offsets, int* __restrict__ edst,
-                                    float* __restrict__ evec, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const int64_t s = offsets[i], e = offsets[i + 1];
+// Sort each atom's neighbors by j: one wave per row.  Rows of at most 64
+// entries: lane l holds entry l and writes it at its rank (number of smaller j,
+// ties by position); longer rows (dense systems): insertion sort by one lane.
+__global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __restrict__ offsets,
+                                                           int* __restrict__ edst,
+                                                           float* __restrict__ evec, int64_t n) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;  // uniform per wave
+    const int64_t s = offsets[row], e = offsets[row + 1];
+    const int len = (int)(e - s);
+    if (len <= 1) return;
+    if (len <= 64) {
+        int j = 0;
+        float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+        if (lane < len) {
+            j = edst[s + lane];
+            v0 = evec[(s + lane) * 3];
+            v1 = evec[(s + lane) * 3 + 1];
+            v2 = evec[(s + lane) * 3 + 2];
+        }
+        int rank = 0;
+        for (int m = 0; m < len; ++m) {
+            const int jm = __builtin_amdgcn_readlane(j, m);
+            rank += (jm < j || (jm == j && m < lane)) ? 1 : 0;
+        }
+        if (lane < len) {
+            edst[s + rank] = j;
+            evec[(s + rank) * 3] = v0;
+            evec[(s + rank) * 3 + 1] = v1;
+            evec[(s + rank) * 3 + 2] = v2;
+        }
+        return;
+    }
+    if (lane != 0) return;
     for (int64_t a = s + 1; a < e; ++a) {
         const int v = edst[a];
         const float v0 = evec[a * 3], v1 = evec[a * 3 + 1], v2 = evec[a * 3 + 2];
-        int64_t j = a - 1;
-        while (j >= s && edst[j] > v) {
-            edst[j + 1] = edst[j];
-            evec[(j + 1) * 3] = evec[j * 3];
-            evec[(j + 1) * 3 + 1] = evec[j * 3 + 1];
-            evec[(j + 1) * 3 + 2] = evec[j * 3 + 2];
-            --j;
+        int64_t q = a - 1;
+        while (q >= s && edst[q] > v) {
+            edst[q + 1] = edst[q];
+            evec[(q + 1) * 3] = evec[q * 3];
+            evec[(q + 1) * 3 + 1] = evec[q * 3 + 1];
+            evec[(q + 1) * 3 + 2] = evec[q * 3 + 2];
+            --q;
         }
-        edst[j + 1] = v;
-        evec[(j + 1) * 3] = v0;
-        evec[(j + 1) * 3 + 1] = v1;
-        evec[(j + 1) * 3 + 2] = v2;
+        edst[q + 1] = v;
+        evec[(q + 1) * 3] = v0;
+        evec[(q + 1) * 3 + 1] = v1;
+        evec[(q + 1) * 3 + 2] = v2;
     }
 }
 
@@ -303,9 +397,9 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
                                                                     order, N);
         nl_sort_bins_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_start, order,
                                                                               c.total);
-        nl_stencil_kernel<false><<<(unsigned)ceil_div(N, B), B, 0, stream>>>(
+        nl_cell_kernel<false><<<(unsigned)c.total, 64, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
-            nullptr, nullptr, N);
+            nullptr, nullptr);
     }
     rc = scan_i64(counts, offsets, N, stream);
     if (rc != BM_OK) return rc;
@@ -332,11 +426,11 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
     const int64_t* offsets = reinterpret_cast<const int64_t*>(ws + L.offsets);
     const int B = 256;
     if (N > 0) {
-        nl_stencil_kernel<true><<<(unsigned)ceil_div(N, B), B, 0, stream>>>(
+        nl_cell_kernel<true><<<(unsigned)c.total, 64, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, edge_src,
-            edge_dst, edge_vectors, N);
-        nl_sort_rows_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(offsets, edge_dst,
-                                                                        edge_vectors, N);
+            edge_dst, edge_vectors);
+        nl_sort_rows_kernel<<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(offsets, edge_dst,
+                                                                         edge_vectors, N);
     }
     if (row_offsets) {
         hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),

@@ -150,6 +150,21 @@ def test_neighbor_list_bit_exact(bm, dev, n):
         np.testing.assert_array_equal(vec, bv)
 
 
+def test_neighbor_list_dense_long_rows_and_chunked_cells(bm, dev):
+    """3000 atoms in a 12 A box with r_c = 4 A: 3 bins per axis, so every cell's
+    27-cell candidate list is the whole system (> 2048 staged per chunk), and
+    rows hold ~300 neighbours (> 64: the single-lane row sort)."""
+    pos = torch.rand(3000, 3, generator=gen(7)) * 12.0
+    cell = torch.diag(torch.tensor([12.0, 12.0, 12.0]))
+    ei, vec, off = _nl_gpu(bm, dev, pos, cell, 4.0)
+    assert np.diff(off).max() > 64
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 4.0)
+    np.testing.assert_array_equal(ei, np.stack([s, d]))
+    np.testing.assert_array_equal(vec, v)
+    bs, bd, bv = onl.brute_force(pos.numpy(), cell.numpy(), 4.0)
+    np.testing.assert_array_equal(ei, np.stack([bs, bd]))
+
+
 def test_neighbor_list_small_box_self_loops_and_lattice(bm, dev):
     pos, cell = periodic_box(40, 8)           # box ~ 8.8 A: 3 bins of < r_c
     ei, vec, _ = _nl_gpu(bm, dev, pos, cell, 5.0, True)
