@@ -24,7 +24,7 @@ PYDIR = os.path.join(HERE, "python")
 LIB = os.path.join(LIBDIR, "libbatmobile_hip.so")
 EXT = os.path.join(PYDIR, "_batmobile" + sysconfig.get_config_var("EXT_SUFFIX"))
 
-HIP_SOURCES = ["sh.hip", "tp.hip", "mp.hip", "nl.hip"]
+HIP_SOURCES = ["sh.hip", "tp.hip", "mp.hip", "nl.hip", "mace.hip"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"

@@ -597,6 +597,129 @@ torch::Tensor selftest_mfma_16x16x4(const torch::Tensor& A, const torch::Tensor&
     return D;
 }
 
+// ---------------------------------------------------------------------------
+// MACE-style interaction layer with per-edge radial weights (no single
+// reference function: benchmarks/benchmark_e2e_mace.py:281-434 composes the
+// same steps with shared weights)
+// ---------------------------------------------------------------------------
+torch::Tensor gemm_f32(const torch::Tensor& A, const torch::Tensor& B, bool trans_b) {
+    TORCH_CHECK(A.dim() == 2 && B.dim() == 2, "A and B must be 2D");
+    TORCH_CHECK(A.dtype() == torch::kFloat32 && B.dtype() == torch::kFloat32, "float32 only");
+    const int64_t M = A.size(0), K = A.size(1);
+    const int64_t N = trans_b ? B.size(0) : B.size(1);
+    TORCH_CHECK((trans_b ? B.size(1) : B.size(0)) == K, "inner dimensions differ");
+    TORCH_CHECK(N <= INT32_MAX && K <= INT32_MAX, "N and K must fit int32");
+    torch::Tensor C = torch::empty({M, N}, f32_like(A));
+    if (M == 0 || N == 0) return C;
+    const c10::DeviceGuard guard(A.device());
+    check_status(batteries_gemm_f32(cptr<float>(A, "A"), cptr<float>(B, "B"), mptr<float>(C, "C"),
+                                    M, (int)N, (int)K, trans_b ? 1 : 0, current_stream(A)),
+                 "gemm_f32");
+    return C;
+}
+
+torch::Tensor mace_reverse_edges(const torch::Tensor& row_ptr, const torch::Tensor& src) {
+    TORCH_CHECK(row_ptr.dtype() == torch::kInt64 && src.dtype() == torch::kInt64, "int64 indices");
+    const int64_t N = row_ptr.numel() - 1, E = src.numel();
+    TORCH_CHECK(N >= 0, "row_ptr must have N + 1 entries");
+    torch::Tensor rev = torch::empty({E}, row_ptr.options());
+    torch::Tensor missing = torch::empty({1}, row_ptr.options().dtype(torch::kInt32));
+    const c10::DeviceGuard guard(row_ptr.device());
+    check_status(batteries_mace_reverse_edges(cptr<int64_t>(row_ptr, "row_ptr"),
+                                              cptr<int64_t>(src, "src"), mptr<int64_t>(rev, "rev"),
+                                              mptr<int>(missing, "missing"), N, E,
+                                              current_stream(row_ptr)),
+                 "mace_reverse_edges");
+    TORCH_CHECK(missing.item<int>() == 0, "mace_reverse_edges: the edge list is not symmetric");
+    return rev;
+}
+
+struct MaceArgs {
+    float box[3];
+    int64_t N, E, C;
+};
+
+MaceArgs mace_check(const torch::Tensor& positions, const torch::Tensor& cell,
+                    const torch::Tensor& x, const torch::Tensor& w1, const torch::Tensor& b1,
+                    const torch::Tensor& w2, const torch::Tensor& src, const torch::Tensor& dst,
+                    const torch::Tensor& row_ptr) {
+    MaceArgs a;
+    TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
+    TORCH_CHECK(x.dim() == 3 && x.size(2) == 16, "node_features must be [N, C, 16]");
+    a.N = positions.size(0);
+    a.C = x.size(1);
+    a.E = src.numel();
+    TORCH_CHECK(x.size(0) == a.N, "node_features and positions disagree on N");
+    TORCH_CHECK(a.C >= 1 && a.C <= 256, "C must be in [1, 256]");
+    TORCH_CHECK(w1.numel() == 8 * 64 && b1.numel() == 64, "W1 [8, 64], b1 [64]");
+    TORCH_CHECK(w2.dim() == 2 && w2.size(0) == 64 && w2.size(1) == 34 * a.C, "W2 must be [64, 34 C]");
+    TORCH_CHECK(dst.numel() == a.E && row_ptr.numel() == a.N + 1, "edge arrays disagree");
+    for (const auto* t : {&positions, &x, &w1, &b1, &w2})
+        TORCH_CHECK(t->dtype() == torch::kFloat32, "float32 tensors expected");
+    for (const auto* t : {&src, &dst, &row_ptr})
+        TORCH_CHECK(t->dtype() == torch::kInt64, "int64 indices expected");
+    TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
+    torch::Tensor cell_cpu = cell.detach().to(torch::kCPU, torch::kFloat32).contiguous();
+    const float* h = cell_cpu.data_ptr<float>();
+    a.box[0] = h[0];
+    a.box[1] = h[4];
+    a.box[2] = h[8];
+    return a;
+}
+
+torch::Tensor mace_forward(const torch::Tensor& positions, const torch::Tensor& cell,
+                           const torch::Tensor& node_features, const torch::Tensor& w1,
+                           const torch::Tensor& b1, const torch::Tensor& w2,
+                           const torch::Tensor& src, const torch::Tensor& dst,
+                           const torch::Tensor& row_ptr, double cutoff) {
+    const MaceArgs a = mace_check(positions, cell, node_features, w1, b1, w2, src, dst, row_ptr);
+    torch::Tensor x = aligned16(node_features);
+    torch::Tensor out = torch::empty({a.N, a.C, 16}, f32_like(x));
+    if (a.N == 0) return out;
+    const c10::DeviceGuard guard(x.device());
+    const size_t wsb = batteries_mace_workspace_bytes(a.E, (int)a.C, 0);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 3) / 4)}, f32_like(x));
+    check_status(batteries_mace_forward(cptr<float>(positions, "positions"), a.box,
+                                        cptr<float>(x, "node_features"), cptr<float>(w1, "W1"),
+                                        cptr<float>(b1, "b1"), cptr<float>(w2, "W2"),
+                                        cptr<int64_t>(src, "src"), cptr<int64_t>(dst, "dst"),
+                                        cptr<int64_t>(row_ptr, "row_ptr"), mptr<float>(out, "out"),
+                                        a.N, a.E, (int)a.C, (float)cutoff, ws.data_ptr(), wsb,
+                                        current_stream(x)),
+                 "mace_forward");
+    return out;
+}
+
+torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor& cell,
+                            const torch::Tensor& node_features, const torch::Tensor& w1,
+                            const torch::Tensor& b1, const torch::Tensor& w2,
+                            const torch::Tensor& src, const torch::Tensor& dst,
+                            const torch::Tensor& row_ptr, const torch::Tensor& rev,
+                            const torch::Tensor& grad_out, double cutoff) {
+    const MaceArgs a = mace_check(positions, cell, node_features, w1, b1, w2, src, dst, row_ptr);
+    TORCH_CHECK(rev.numel() == a.E && rev.dtype() == torch::kInt64, "rev must be int64 [E]");
+    TORCH_CHECK(grad_out.dim() == 3 && grad_out.size(0) == a.N && grad_out.size(1) == a.C &&
+                    grad_out.size(2) == 16 && grad_out.dtype() == torch::kFloat32,
+                "grad_out must be float32 [N, C, 16]");
+    torch::Tensor x = aligned16(node_features);
+    torch::Tensor g = aligned16(grad_out.contiguous());
+    torch::Tensor gpos = torch::empty({a.N, 3}, f32_like(x));
+    if (a.N == 0) return gpos;
+    const c10::DeviceGuard guard(x.device());
+    const size_t wsb = batteries_mace_workspace_bytes(a.E, (int)a.C, 1);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 3) / 4)}, f32_like(x));
+    check_status(batteries_mace_backward(cptr<float>(positions, "positions"), a.box,
+                                         cptr<float>(x, "node_features"), cptr<float>(w1, "W1"),
+                                         cptr<float>(b1, "b1"), cptr<float>(w2, "W2"),
+                                         cptr<int64_t>(src, "src"), cptr<int64_t>(dst, "dst"),
+                                         cptr<int64_t>(row_ptr, "row_ptr"),
+                                         cptr<int64_t>(rev, "rev"), cptr<float>(g, "grad_out"),
+                                         mptr<float>(gpos, "grad_pos"), a.N, a.E, (int)a.C,
+                                         (float)cutoff, ws.data_ptr(), wsb, current_stream(x)),
+                 "mace_backward");
+    return gpos;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_batmobile, m) {
@@ -660,6 +783,18 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("edge_perm"), py::arg("row_dst"), py::arg("n_blocks"),
           py::arg("rows_per_block"), py::arg("N_dst"), py::arg("normalize") = false,
           "sh_tp_scatter processed in the order of an mp_schedule (same result)");
+    m.def("gemm_f32", &gemm_f32, py::arg("A"), py::arg("B"), py::arg("trans_b") = false,
+          "C = A @ B (or A @ B.T) on MFMA, fp32 (extension)");
+    m.def("mace_reverse_edges", &mace_reverse_edges, py::arg("row_ptr"), py::arg("src"),
+          "index of every edge's reverse in a symmetric destination-grouped edge list (extension)");
+    m.def("mace_forward", &mace_forward, py::arg("positions"), py::arg("cell"),
+          py::arg("node_features"), py::arg("W1"), py::arg("b1"), py::arg("W2"), py::arg("src"),
+          py::arg("dst"), py::arg("row_ptr"), py::arg("cutoff"),
+          "MACE-style layer with per-edge radial weights, forward (extension)");
+    m.def("mace_backward", &mace_backward, py::arg("positions"), py::arg("cell"),
+          py::arg("node_features"), py::arg("W1"), py::arg("b1"), py::arg("W2"), py::arg("src"),
+          py::arg("dst"), py::arg("row_ptr"), py::arg("rev"), py::arg("grad_out"),
+          py::arg("cutoff"), "gradient of the MACE-style layer w.r.t. positions (extension)");
     m.def("selftest_mfma_16x16x4", &selftest_mfma_16x16x4, py::arg("A"), py::arg("B"),
           "D = A @ B through one v_mfma_f32_16x16x4f32 (lane-layout self test)");
 }

@@ -1,0 +1,615 @@
+// MACE-style interaction layer with per-edge radial weights (the baseline's
+// configs[4]): Bessel radial basis -> MLP [8 -> 64 -> 34 C] -> channel-wise
+// weighted CG product of X[src] with Y(v) -> scatter-add into destinations,
+// and its gradient with respect to the positions.
+//
+// Pattern of reference benchmarks/benchmark_e2e_mace.py:281-434 (SH -> TP ->
+// scatter, forces by backward through the edge vectors :412-420); the
+// reference's own block shares one W[34, C, C] over edges, the per-edge radial
+// weights are this configuration's.  Layer definition (fp32 here):
+//   v_e = min_image(pos[dst_e] - pos[src_e]), r = |v|, u = v / r
+//   B_k = sqrt(2/rc) sin(k pi r/rc) / r * f(r/rc),  f(d) = 1 - 28 d^6 + 48 d^7 - 21 d^8
+//   h = silu(B W1 + b1), R[e, c, p] = (h W2)[c * 34 + p]
+//   out[d, c, o] = sum_{e -> d} sum_p R[e,c,p] sum_{(a,b) in p -> o} CG x[src_e,c,a] Y_e[b]
+//
+// Work per edge: the MLP's second layer is a GEMM [edges x 64] x [64 x 34C]
+// (557 kflop per edge at C = 128) and runs on MFMA over edge chunks; the CG
+// work (1378 flop per edge and channel) runs on the VALU, thread per
+// (destination row, channel), so every output row is written by one thread in
+// a fixed edge order (deterministic, no atomics).  Forces are gathered per
+// atom from per-edge gradients through the reverse-edge map of the symmetric
+// edge list.
+#include "common.h"
+#include "batmobile_hip.h"
+
+namespace bmhip {
+
+constexpr int kNBasis = 8;
+constexpr int kHidden = 64;
+constexpr int64_t kMaceChunk = 65536;  // edges per chunk (R and its gradient live per chunk)
+
+#pragma clang fp contract(off)
+// v = pos[dst] - pos[src] with the minimum image of an orthorhombic box, in the
+// neighbor list's operation order (so v equals its vectors negated, exactly)
+__device__ __forceinline__ void edge_vector(const float* __restrict__ pos, int64_t s, int64_t d,
+                                            const float* box, const float* inv, float* v) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const float t = pos[d * 3 + k] - pos[s * 3 + k];
+        const float q = t * inv[k];
+        const float rr = rintf(q);
+        const float m = rr * box[k];
+        v[k] = t - m;
+    }
+}
+#pragma clang fp contract(on)
+
+struct MaceBox {
+    float box[3];
+    float inv[3];
+};
+
+// Bessel basis with envelope, and its derivative with respect to r.
+__device__ __forceinline__ void radial_basis(float r, float rc, float* B, float* dB) {
+    const float d = r / rc;
+    float f = 0.f, df = 0.f;
+    if (d < 1.0f) {
+        const float d5 = d * d * d * d * d, d6 = d5 * d;
+        f = 1.0f - 28.0f * d6 + 48.0f * d6 * d - 21.0f * d6 * d * d;
+        const float om = 1.0f - d;
+        df = -168.0f * d5 * om * om / rc;  // f'(d) / rc
+    }
+    const float norm = sqrtf(2.0f / rc);
+    const float ir = 1.0f / r;
+#pragma unroll
+    for (int k = 0; k < kNBasis; ++k) {
+        const float w = (float)(k + 1) * 3.14159265358979323846f / rc;
+        float sn, cs;
+        sincosf(w * r, &sn, &cs);
+        const float g = norm * sn * ir;                       // bare Bessel
+        const float dg = norm * (w * cs * ir - sn * ir * ir);  // its derivative
+        B[k] = g * f;
+        if (dB) dB[k] = dg * f + g * df;
+    }
+}
+
+__device__ __forceinline__ float sigmoidf(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// An empty asm that takes and returns 16 values: everything computed from them
+// afterwards depends on this point and cannot be hoisted above it.
+__device__ __forceinline__ void launder16(float* v) {
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                      "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
+                      "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]));
+}
+
+// ---------------------------------------------------------------------------
+// edge vectors from positions (grid over edges)
+// ---------------------------------------------------------------------------
+__global__ void mace_edge_vectors_kernel(const float* __restrict__ pos, MaceBox bx,
+                                         const int64_t* __restrict__ src,
+                                         const int64_t* __restrict__ dst, float* __restrict__ vec,
+                                         int64_t n_edges) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_edges) return;
+    float v[3];
+    edge_vector(pos, src[e], dst[e], bx.box, bx.inv, v);
+    vec[e * 3 + 0] = v[0];
+    vec[e * 3 + 1] = v[1];
+    vec[e * 3 + 2] = v[2];
+}
+
+// ---------------------------------------------------------------------------
+// h[e, :] = silu(B(r_e) W1 + b1), edges [e0, e1) of the chunk (row e - e0 of h)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mace_radial_kernel(const float* __restrict__ vec,
+                                                          const float* __restrict__ w1,
+                                                          const float* __restrict__ b1,
+                                                          float* __restrict__ h, int64_t e0,
+                                                          int64_t e1, float rc) {
+    __shared__ float sW[kNBasis * kHidden + kHidden];
+    for (int i = threadIdx.x; i < kNBasis * kHidden + kHidden; i += blockDim.x)
+        sW[i] = i < kNBasis * kHidden ? w1[i] : b1[i - kNBasis * kHidden];
+    __syncthreads();
+    const int64_t e = e0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= e1) return;
+    float vx = vec[e * 3], vy = vec[e * 3 + 1], vz = vec[e * 3 + 2];
+    const float r = normalize3(vx, vy, vz);
+    float B[kNBasis];
+    radial_basis(r, rc, B, nullptr);
+    float4* out = reinterpret_cast<float4*>(h + (e - e0) * kHidden);
+#pragma unroll
+    for (int j4 = 0; j4 < kHidden / 4; ++j4) {
+        float z[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int j = j4 * 4 + t;
+            float acc = sW[kNBasis * kHidden + j];
+#pragma unroll
+            for (int k = 0; k < kNBasis; ++k) acc = fmaf(B[k], sW[k * kHidden + j], acc);
+            z[t] = acc * sigmoidf(acc);
+        }
+        out[j4] = make_float4(z[0], z[1], z[2], z[3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 GEMM on MFMA: C[M, N] = A[M, K] B, with B = [K, N] (row-major) or, when
+// TB, given as B^T [N, K] (row-major).  Tile 64 x 64, K step 16, four waves:
+// wave w computes rows 16 w .. 16 w + 15 of the tile, four 16x16 MFMA tiles.
+// ---------------------------------------------------------------------------
+template <bool TB>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A,
+                                                       const float* __restrict__ B,
+                                                       float* __restrict__ C, int M, int N, int K) {
+    __shared__ float sA[64][17];   // [m][k]
+    __shared__ float sB[16][65];   // [k][n]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g4 = lane >> 4, i16 = lane & 15;
+    const int64_t m0 = (int64_t)blockIdx.y * 64;
+    const int n0 = blockIdx.x * 64;
+    v4f acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int i = tid + it * 256;
+            {   // A: 64 rows x 16 k, k fastest (row-major A)
+                const int m = i >> 4, k = i & 15;
+                const int64_t gm = m0 + m;
+                sA[m][k] = (gm < M && k0 + k < K) ? A[gm * K + k0 + k] : 0.0f;
+            }
+            if constexpr (TB) {  // B^T [N, K]: k fastest
+                const int n = i >> 4, k = i & 15;
+                sB[k][n] = (n0 + n < N && k0 + k < K) ? B[(int64_t)(n0 + n) * K + k0 + k] : 0.0f;
+            } else {             // B [K, N]: n fastest
+                const int k = i >> 6, n = i & 63;
+                sB[k][n] = (n0 + n < N && k0 + k < K) ? B[(int64_t)(k0 + k) * N + n0 + n] : 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const float a = sA[16 * wv + i16][4 * ks + g4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = mfma1(a, sB[4 * ks + g4][16 * t + i16], acc[t]);
+        }
+    }
+    // D[4 g4 + r][i16] of tile t: row m0 + 16 wv + 4 g4 + r, column n0 + 16 t + i16
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int n = n0 + 16 * t + i16;
+        if (n >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + 16 * wv + 4 * g4 + r;
+            if (m < M) C[m * N + n] = acc[t][r];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward product + scatter for the edges [e0, e1) of a chunk: thread (row d,
+// channel c) adds sum_{e in row d, e0 <= e < e1} m[e, c, :] to out[d, c, :].
+// Per path: the path's CG entries give T_p[m_out] from x[src, c, a] and Y[b],
+// weighted by R[e, c, p] (row e - e0 of the chunk's R).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
+    const float* __restrict__ vec, const float* __restrict__ x, const int64_t* __restrict__ src,
+    const int64_t* __restrict__ row_ptr, const float* __restrict__ R, int64_t e0, int64_t e1,
+    float* __restrict__ out, int C) {
+    const int64_t d = blockIdx.x;
+    const int c = blockIdx.y * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    const int64_t s = max(row_ptr[d], e0), e = min(row_ptr[d + 1], e1);
+    if (s >= e) return;
+    float m[16];
+#pragma unroll
+    for (int o = 0; o < 16; ++o) m[o] = 0.0f;
+    for (int64_t k = s; k < e; ++k) {
+        float ux = vec[k * 3], uy = vec[k * 3 + 1], uz = vec[k * 3 + 2];
+        normalize3(ux, uy, uz);
+        float Y[16];
+        sh_forward<3>(ux, uy, uz, Y);
+        float xs[16];
+        const float4* xp = reinterpret_cast<const float4*>(x + (src[k] * C + c) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = xp[q];
+            xs[4 * q] = t.x;
+            xs[4 * q + 1] = t.y;
+            xs[4 * q + 2] = t.z;
+            xs[4 * q + 3] = t.w;
+        }
+        const float* Rr = R + ((k - e0) * C + c) * kNumPaths;
+        static_for<kNumPaths>([&](auto pp) {
+            constexpr int p = decltype(pp)::value;
+            constexpr int lo = kPathL[p][2];
+            float tq[2 * lo + 1];
+#pragma unroll
+            for (int q = 0; q < 2 * lo + 1; ++q) tq[q] = 0.0f;
+            static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
+                tq[en.o - lo * lo] = fmaf(en.c * Y[en.b], xs[en.a], tq[en.o - lo * lo]);
+            });
+            const float rp = Rr[p];
+#pragma unroll
+            for (int q = 0; q < 2 * lo + 1; ++q) m[lo * lo + q] = fmaf(rp, tq[q], m[lo * lo + q]);
+        });
+    }
+    float4* op = reinterpret_cast<float4*>(out + (d * C + c) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 t = op[q];
+        t.x += m[4 * q];
+        t.y += m[4 * q + 1];
+        t.z += m[4 * q + 2];
+        t.w += m[4 * q + 3];
+        op[q] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, per edge of the chunk (thread (row d, channel c); the workgroup
+// walks row d's edges together):
+//   gR[e, c, p] = sum_{m_out} g[d, c, o] T_p[e, c, m_out]
+//   gY[e, b]    = sum_c sum_{entries of p} CG R[e,c,p] x[src,c,a] g[d,c,o]
+// gY is summed over the channels (threads) in a fixed order: lanes by a
+// butterfly, waves through LDS.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mace_tp_backward_kernel(
+    const float* __restrict__ vec, const float* __restrict__ x, const int64_t* __restrict__ src,
+    const int64_t* __restrict__ row_ptr, const float* __restrict__ R,
+    const float* __restrict__ gout, int64_t e0, int64_t e1, float* __restrict__ gR,
+    float* __restrict__ gY, int C) {
+    __shared__ float sRed[16][17];
+    const int64_t d = blockIdx.x;
+    const int c = threadIdx.x;
+    const bool live = c < C;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int64_t s = max(row_ptr[d], e0), e = min(row_ptr[d + 1], e1);
+    if (s >= e) return;  // uniform over the workgroup
+    const int cc = live ? c : C - 1;
+    float g[16];
+    {
+        const float4* gp = reinterpret_cast<const float4*>(gout + (d * C + cc) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = gp[q];
+            g[4 * q] = live ? t.x : 0.f;
+            g[4 * q + 1] = live ? t.y : 0.f;
+            g[4 * q + 2] = live ? t.z : 0.f;
+            g[4 * q + 3] = live ? t.w : 0.f;
+        }
+    }
+    for (int64_t k = s; k < e; ++k) {
+        float ux = vec[k * 3], uy = vec[k * 3 + 1], uz = vec[k * 3 + 2];
+        normalize3(ux, uy, uz);
+        float Y[16];
+        sh_forward<3>(ux, uy, uz, Y);
+        float xs[16];
+        const float4* xp = reinterpret_cast<const float4*>(x + (src[k] * C + cc) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = xp[q];
+            xs[4 * q] = t.x;
+            xs[4 * q + 1] = t.y;
+            xs[4 * q + 2] = t.z;
+            xs[4 * q + 3] = t.w;
+        }
+        const float* Rr = R + ((k - e0) * C + cc) * kNumPaths;
+        float* gRr = gR + ((k - e0) * C + cc) * kNumPaths;
+        float gy[16];
+#pragma unroll
+        for (int b = 0; b < 16; ++b) gy[b] = 0.0f;
+        // one path per iteration of a loop that is not unrolled: each path is a
+        // basic block of its own, so the 34 paths are not interleaved (which
+        // would keep several hundred temporaries live)
+#pragma clang loop unroll(disable)
+        for (int pk = 0; pk < kNumPaths; ++pk) {
+            // x, Y and g through empty asms each iteration: the products of the
+            // CG entries are formed per path instead of being hoisted out of the
+            // path loop (hundreds of loop-invariant values)
+            float xk[16], yk[16], gk[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                xk[q] = xs[q];
+                yk[q] = Y[q];
+                gk[q] = g[q];
+            }
+            launder16(xk);
+            launder16(yk);
+            launder16(gk);
+            static_for<kNumPaths>([&](auto pp) {
+                constexpr int p = decltype(pp)::value;
+                if (pk == p) {
+                    const float rp = Rr[p];
+                    float gr = 0.0f;
+                    static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                        constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
+                        const float xg = xk[en.a] * gk[en.o];
+                        gr = fmaf(en.c * yk[en.b], xg, gr);
+                        gy[en.b] = fmaf(en.c * rp, xg, gy[en.b]);
+                    });
+                    if (live) gRr[p] = gr;
+                }
+            });
+        }
+        // sum gy over the channels: butterfly within each wave, then waves in order
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            float v = live ? gy[b] : 0.0f;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+            gy[b] = v;
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int b = 0; b < 16; ++b) sRed[wv][b] = gy[b];
+        }
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            float t = 0.0f;
+            for (int w = 0; w < nw; ++w) t += sRed[w][threadIdx.x];
+            gY[(k - e0) * 16 + threadIdx.x] = t;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward through the radial MLP, the normalisation and SH, per edge:
+//   g_v = g_r u + (g_u - u (u . g_u)) / r
+// with g_r = sum_k (sum_j W1[k, j] g_h[j] silu'(z_j)) dB_k/dr and
+// g_u = SH backward of gY at u.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mace_radial_backward_kernel(
+    const float* __restrict__ vec, const float* __restrict__ w1, const float* __restrict__ b1,
+    const float* __restrict__ gh, const float* __restrict__ gY, int64_t e0, int64_t e1, float rc,
+    float* __restrict__ gv) {
+    __shared__ float sW[kNBasis * kHidden + kHidden];
+    for (int i = threadIdx.x; i < kNBasis * kHidden + kHidden; i += blockDim.x)
+        sW[i] = i < kNBasis * kHidden ? w1[i] : b1[i - kNBasis * kHidden];
+    __syncthreads();
+    const int64_t e = e0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= e1) return;
+    float ux = vec[e * 3], uy = vec[e * 3 + 1], uz = vec[e * 3 + 2];
+    const float r = normalize3(ux, uy, uz);
+    float B[kNBasis], dB[kNBasis];
+    radial_basis(r, rc, B, dB);
+    float gB[kNBasis];
+#pragma unroll
+    for (int k = 0; k < kNBasis; ++k) gB[k] = 0.0f;
+    const float* ghr = gh + (e - e0) * kHidden;
+    for (int j = 0; j < kHidden; ++j) {
+        float z = sW[kNBasis * kHidden + j];
+#pragma unroll
+        for (int k = 0; k < kNBasis; ++k) z = fmaf(B[k], sW[k * kHidden + j], z);
+        const float sg = sigmoidf(z);
+        const float gz = ghr[j] * sg * (1.0f + z * (1.0f - sg));
+#pragma unroll
+        for (int k = 0; k < kNBasis; ++k) gB[k] = fmaf(sW[k * kHidden + j], gz, gB[k]);
+    }
+    float gr = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNBasis; ++k) gr = fmaf(gB[k], dB[k], gr);
+    float Y[16], gyv[16];
+    sh_forward<3>(ux, uy, uz, Y);
+#pragma unroll
+    for (int b = 0; b < 16; ++b) gyv[b] = gY[(e - e0) * 16 + b];
+    float gux, guy, guz;
+    sh_backward<3>(ux, uy, uz, Y, gyv, gux, guy, guz);
+    const float dot = ux * gux + uy * guy + uz * guz;
+    const float ir = 1.0f / r;
+    gv[e * 3 + 0] = gr * ux + (gux - ux * dot) * ir;
+    gv[e * 3 + 1] = gr * uy + (guy - uy * dot) * ir;
+    gv[e * 3 + 2] = gr * uz + (guz - uz * dot) * ir;
+}
+
+// ---------------------------------------------------------------------------
+// grad_pos[a] = sum_{e in row a} (g_v[e] - g_v[rev[e]]): v_e = pos[dst] -
+// pos[src], and rev[e] is the edge with the roles of a and src_e swapped.
+// ---------------------------------------------------------------------------
+__global__ void mace_forces_kernel(const float* __restrict__ gv, const int64_t* __restrict__ row_ptr,
+                                   const int64_t* __restrict__ rev, float* __restrict__ gpos,
+                                   int64_t n) {
+    const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    float f0 = 0.f, f1 = 0.f, f2 = 0.f;
+    for (int64_t e = row_ptr[a]; e < row_ptr[a + 1]; ++e) {
+        const int64_t t = rev[e];
+        if (t < 0) continue;  // edge list not symmetric (reported by the reverse-edge build)
+        f0 += gv[e * 3 + 0] - gv[t * 3 + 0];
+        f1 += gv[e * 3 + 1] - gv[t * 3 + 1];
+        f2 += gv[e * 3 + 2] - gv[t * 3 + 2];
+    }
+    gpos[a * 3 + 0] = f0;
+    gpos[a * 3 + 1] = f1;
+    gpos[a * 3 + 2] = f2;
+}
+
+// rev[e] for e = (src j -> dst i): the edge (src i -> dst j), found by binary
+// search in row j (sources ascending); -1 if the edge list is not symmetric.
+__global__ void mace_reverse_edges_kernel(const int64_t* __restrict__ row_ptr,
+                                          const int64_t* __restrict__ src,
+                                          int64_t* __restrict__ rev, int* __restrict__ missing,
+                                          int64_t n, int64_t n_edges) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_edges) return;
+    // destination of e: the row containing e
+    int64_t lo = 0, hi = n;  // last row with row_ptr[row] <= e
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (row_ptr[mid] <= e) lo = mid;
+        else hi = mid;
+    }
+    const int64_t i = lo, j = src[e];
+    int64_t a = row_ptr[j], b = row_ptr[j + 1];  // first position with src >= i
+    while (a < b) {
+        const int64_t mid = (a + b) >> 1;
+        if (src[mid] < i) a = mid + 1;
+        else b = mid;
+    }
+    const bool ok = a < row_ptr[j + 1] && src[a] == i;
+    rev[e] = ok ? a : -1;
+    if (!ok) atomicAdd(missing, 1);
+}
+
+__global__ void mace_fill_zero_kernel(float* __restrict__ p, int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = 0.0f;
+}
+
+__global__ void mace_zero_int_kernel(int* __restrict__ p) { *p = 0; }
+
+struct MaceWs {
+    float *vec, *h, *R, *gR, *gh, *gY, *gv;
+    size_t bytes;
+};
+
+static size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
+
+static MaceWs mace_ws(void* base, int64_t E, int C, bool backward) {
+    const int64_t eb = std::min<int64_t>(std::max<int64_t>(E, 1), kMaceChunk);
+    char* p = static_cast<char*>(base);
+    size_t o = 0;
+    MaceWs w{};
+    auto take = [&](size_t bytes) {
+        float* r = p ? reinterpret_cast<float*>(p + o) : nullptr;
+        o = a256(o + bytes);
+        return r;
+    };
+    w.vec = take(sizeof(float) * 3 * (size_t)E);
+    w.h = take(sizeof(float) * (size_t)eb * kHidden);
+    w.R = take(sizeof(float) * (size_t)eb * C * kNumPaths);
+    if (backward) {
+        w.gR = take(sizeof(float) * (size_t)eb * C * kNumPaths);
+        w.gh = take(sizeof(float) * (size_t)eb * kHidden);
+        w.gY = take(sizeof(float) * (size_t)eb * 16);
+        w.gv = take(sizeof(float) * 3 * (size_t)E);
+    }
+    w.bytes = o;
+    return w;
+}
+
+static int gemm_launch(const float* A, const float* B, float* Cm, int64_t M, int N, int K, bool tb,
+                       hipStream_t s) {
+    if (M <= 0 || N <= 0 || K <= 0) return BM_OK;
+    dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
+    if (grid.y > 65535) return BM_ERR_ARG;
+    if (tb) gemm_f32_kernel<true><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+    else gemm_f32_kernel<false><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+    return (int)hipGetLastError();
+}
+
+}  // namespace bmhip
+
+using namespace bmhip;
+
+extern "C" int batteries_gemm_f32(const float* A, const float* B, float* C, int64_t M, int N, int K,
+                                  int trans_b, hipStream_t stream) {
+    if (M < 0 || N < 0 || K < 0 || M > INT32_MAX) return BM_ERR_ARG;
+    return gemm_launch(A, B, C, M, N, K, trans_b != 0, stream);
+}
+
+extern "C" size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward) {
+    if (N_edges < 0 || C <= 0) return 0;
+    return mace_ws(nullptr, N_edges, C, backward != 0).bytes;
+}
+
+extern "C" int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src,
+                                            int64_t* rev, int* d_missing, int64_t N,
+                                            int64_t N_edges, hipStream_t stream) {
+    if (N < 0 || N_edges < 0 || !d_missing) return BM_ERR_ARG;
+    mace_zero_int_kernel<<<1, 1, 0, stream>>>(d_missing);
+    if (N_edges == 0) return (int)hipGetLastError();
+    mace_reverse_edges_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
+        row_ptr, src, rev, d_missing, N, N_edges);
+    return (int)hipGetLastError();
+}
+
+static bool mace_args_ok(const float* box, int64_t N, int64_t E, int C, float cutoff) {
+    if (!box || N < 0 || E < 0 || C <= 0 || C > 256 || !(cutoff > 0.0f)) return false;
+    for (int k = 0; k < 3; ++k)
+        if (!(box[k] > 0.0f)) return false;
+    return (int64_t)kMaceChunk * C * kNumPaths < INT32_MAX;
+}
+
+static MaceBox mace_box(const float* box) {
+    MaceBox b;
+    for (int k = 0; k < 3; ++k) {
+        b.box[k] = box[k];
+        b.inv[k] = 1.0f / box[k];
+    }
+    return b;
+}
+
+extern "C" int batteries_mace_forward(const float* positions, const float* box,
+                                      const float* node_features, const float* w1,
+                                      const float* b1, const float* w2, const int64_t* src,
+                                      const int64_t* dst, const int64_t* row_ptr, float* out,
+                                      int64_t N, int64_t N_edges, int C, float cutoff,
+                                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!mace_args_ok(box, N, N_edges, C, cutoff)) return BM_ERR_ARG;
+    if (N == 0) return BM_OK;
+    const MaceWs w = mace_ws(workspace, N_edges, C, false);
+    if (!workspace || workspace_bytes < w.bytes) return BM_ERR_WORKSPACE;
+    const int64_t count = N * (int64_t)C * 16;
+    mace_fill_zero_kernel<<<(unsigned)ceil_div(count, 256), 256, 0, stream>>>(out, count);
+    if (N_edges == 0) return (int)hipGetLastError();
+    const MaceBox bx = mace_box(box);
+    mace_edge_vectors_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
+        positions, bx, src, dst, w.vec, N_edges);
+    const int nthr = C >= 256 ? 256 : (int)ceil_div(C, 64) * 64;
+    for (int64_t e0 = 0; e0 < N_edges; e0 += kMaceChunk) {
+        const int64_t e1 = std::min(N_edges, e0 + kMaceChunk), eb = e1 - e0;
+        mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
+                                                                             e1, cutoff);
+        int rc = gemm_launch(w.h, w2, w.R, eb, C * kNumPaths, kHidden, false, stream);
+        if (rc != BM_OK) return rc;
+        dim3 grid((unsigned)N, (unsigned)ceil_div(C, nthr));
+        mace_tp_scatter_kernel<<<grid, nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, w.R,
+                                                          e0, e1, out, C);
+    }
+    return (int)hipGetLastError();
+}
+
+extern "C" int batteries_mace_backward(const float* positions, const float* box,
+                                       const float* node_features, const float* w1,
+                                       const float* b1, const float* w2, const int64_t* src,
+                                       const int64_t* dst, const int64_t* row_ptr,
+                                       const int64_t* rev, const float* grad_out, float* grad_pos,
+                                       int64_t N, int64_t N_edges, int C, float cutoff,
+                                       void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+    if (!mace_args_ok(box, N, N_edges, C, cutoff)) return BM_ERR_ARG;
+    if (N == 0) return BM_OK;
+    const MaceWs w = mace_ws(workspace, N_edges, C, true);
+    if (!workspace || workspace_bytes < w.bytes) return BM_ERR_WORKSPACE;
+    if (N_edges == 0) {
+        mace_fill_zero_kernel<<<(unsigned)ceil_div(N * 3, 256), 256, 0, stream>>>(grad_pos, N * 3);
+        return (int)hipGetLastError();
+    }
+    const MaceBox bx = mace_box(box);
+    mace_edge_vectors_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
+        positions, bx, src, dst, w.vec, N_edges);
+    const int nthr = (int)ceil_div(C, 64) * 64;
+    for (int64_t e0 = 0; e0 < N_edges; e0 += kMaceChunk) {
+        const int64_t e1 = std::min(N_edges, e0 + kMaceChunk), eb = e1 - e0;
+        mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
+                                                                             e1, cutoff);
+        int rc = gemm_launch(w.h, w2, w.R, eb, C * kNumPaths, kHidden, false, stream);
+        if (rc != BM_OK) return rc;
+        mace_tp_backward_kernel<<<(unsigned)N, nthr, 0, stream>>>(
+            w.vec, node_features, src, row_ptr, w.R, grad_out, e0, e1, w.gR, w.gY, C);
+        rc = gemm_launch(w.gR, w2, w.gh, eb, kHidden, C * kNumPaths, true, stream);
+        if (rc != BM_OK) return rc;
+        mace_radial_backward_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(
+            w.vec, w1, b1, w.gh, w.gY, e0, e1, cutoff, w.gv);
+    }
+    mace_forces_kernel<<<(unsigned)ceil_div(N, 256), 256, 0, stream>>>(w.gv, row_ptr, rev, grad_pos,
+                                                                        N);
+    return (int)hipGetLastError();
+}

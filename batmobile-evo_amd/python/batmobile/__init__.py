@@ -53,8 +53,13 @@ from _batteries import (  # noqa: E402
     spatial_order,
     mp_schedule,
     sh_tp_scatter_scheduled,
+    gemm_f32,
+    mace_reverse_edges,
+    mace_forward,
+    mace_backward,
 )
 from .graph import Graph  # noqa: E402
+from .mace import MACEInteraction, MaceLayerFunction  # noqa: E402
 
 # Autograd-compatible wrappers (reference __init__.py:35-44)
 from .autograd import (  # noqa: E402
@@ -99,4 +104,10 @@ __all__ = [
     "mp_schedule",
     "sh_tp_scatter_scheduled",
     "Graph",
+    "gemm_f32",
+    "mace_reverse_edges",
+    "mace_forward",
+    "mace_backward",
+    "MACEInteraction",
+    "MaceLayerFunction",
 ]

@@ -21,6 +21,9 @@ import _batmobile
 class Graph:
     def __init__(self, positions, cell, cutoff, channels, self_loops=False):
         ei, vec, off = _batmobile.neighbor_list(positions, cell, float(cutoff), bool(self_loops))
+        self.cell = cell
+        self.cutoff = float(cutoff)
+        self._rev = None
         self.n_atoms = positions.shape[0]
         self.src = ei[1].contiguous()
         self.dst = ei[0].contiguous()
@@ -34,6 +37,12 @@ class Graph:
     @property
     def num_edges(self):
         return int(self.src.numel())
+
+    def reverse_edges(self):
+        """rev[e]: index of the edge with source and destination swapped (built once)."""
+        if self._rev is None:
+            self._rev = _batmobile.mace_reverse_edges(self.row_ptr, self.src)
+        return self._rev
 
     def sh_tp_scatter(self, node_features, normalize=True):
         """out[d] = sum_{e -> d} TP_simple(X[src_e], Y_lm(v_e)); one kernel, spatial schedule."""

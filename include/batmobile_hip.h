@@ -239,6 +239,41 @@ void neighbor_list_free(NeighborListResult* result);
 size_t neighbor_list_estimate_memory(int64_t N, float density, float cutoff);
 
 /* ---------------------------------------------------------------------------
+ * MACE-style interaction layer with per-edge radial weights (no single
+ * reference counterpart: the reference composes SH -> TP -> scatter with one
+ * shared W[34,C,C] in benchmarks/benchmark_e2e_mace.py:281-355 and takes forces
+ * by backward through the edge vectors, :412-420; the per-edge radial weights
+ * are the baseline's configs[4]).
+ *   v_e = min_image(pos[dst] - pos[src]); B_k(r) = sqrt(2/rc) sin(k pi r/rc)/r f(r/rc),
+ *   f(d) = 1 - 28 d^6 + 48 d^7 - 21 d^8; h = silu(B W1 + b1) with W1 [8,64], b1 [64];
+ *   R[e,c,p] = (h W2)[c*34 + p] with W2 [64, 34 C];
+ *   out[d,c,o] = sum_{e->d} sum_p R[e,c,p] sum_{(a,b) in p->o} CG x[src,c,a] Y(v_e/|v_e|)[b].
+ * Edges grouped by destination (row_ptr [N+1]) with sources ascending per row,
+ * symmetric (every (j->i) has (i->j)), as batmobile.Graph builds them.  box is a
+ * host float[3] (orthorhombic cell diagonal).  C <= 256.
+ * ------------------------------------------------------------------------- */
+/* C[M,N] = A[M,K] B on MFMA (fp32); B is [K,N] row-major, or [N,K] row-major when trans_b. */
+int batteries_gemm_f32(const float* A, const float* B, float* C, int64_t M, int N, int K,
+                       int trans_b, hipStream_t stream);
+size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward);
+/* rev[e] = index of the edge with source and destination swapped (-1 if absent);
+ * *d_missing (device int) counts the absent ones. */
+int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src, int64_t* rev,
+                                 int* d_missing, int64_t N, int64_t N_edges, hipStream_t stream);
+int batteries_mace_forward(const float* positions, const float* box, const float* node_features,
+                           const float* w1, const float* b1, const float* w2, const int64_t* src,
+                           const int64_t* dst, const int64_t* row_ptr, float* out, int64_t N,
+                           int64_t N_edges, int C, float cutoff, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+/* grad_pos[N,3] = d <out, grad_out> / d positions (rev from batteries_mace_reverse_edges). */
+int batteries_mace_backward(const float* positions, const float* box, const float* node_features,
+                            const float* w1, const float* b1, const float* w2, const int64_t* src,
+                            const int64_t* dst, const int64_t* row_ptr, const int64_t* rev,
+                            const float* grad_out, float* grad_pos, int64_t N, int64_t N_edges,
+                            int C, float cutoff, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Self test (no reference counterpart): D[16,16] = A[16,4] B[4,16] through one
  * v_mfma_f32_16x16x4f32 with the lane layout the kernels above assume.
  * ------------------------------------------------------------------------- */

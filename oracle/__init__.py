@@ -21,4 +21,8 @@ follows.  How each function is pinned:
   mp_*     composition identities (fused == SH->TP->index_add), per-edge loop.
   nl       brute force over all pairs (same fp32 op order), symmetry,
            hand-made lattice known answers.
+  mace     (the per-edge-weight layer of configs[4], defined here: no reference
+           API has per-edge weights) envelope values and vanishing derivatives,
+           Bessel orthonormality, unit weights reducing to TP_simple, finite
+           differences and translation invariance of the position gradient.
 """

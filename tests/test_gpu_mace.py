@@ -1,0 +1,89 @@
+"""MACE-style layer with per-edge radial weights on the GPU vs the
+float64 composition of oracle/mace.py; the fp32 MFMA GEMM vs float64."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mace as om
+
+from helpers import gen, normwise_err, periodic_box
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("m,n,k,tb", [(100, 70, 64, False), (65, 64, 300, True), (1, 1, 1, False),
+                                      (130, 4352, 64, False)])
+def test_gemm_f32(bm, dev, m, n, k, tb):
+    a = torch.randn(m, k, generator=gen(1))
+    b = torch.randn(n, k, generator=gen(2)) if tb else torch.randn(k, n, generator=gen(2))
+    c = bm.gemm_f32(a.to(dev), b.to(dev), tb).cpu()
+    ref = a.double() @ (b.double().T if tb else b.double())
+    assert normwise_err(c, ref.numpy()) <= 1e-6
+
+
+def _layer_inputs(dev, n, c, seed):
+    import batmobile
+    pos, cell = periodic_box(n, seed)
+    graph = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+    layer = batmobile.MACEInteraction(c, 5.0, device=dev, generator=gen(seed + 1))
+    x = torch.randn(n, c, 16, generator=gen(seed + 2))
+    go = torch.randn(n, c, 16, generator=gen(seed + 3))
+    return pos, cell, graph, layer, x, go
+
+
+def _oracle(pos, cell, graph, layer, x, go):
+    box = torch.diagonal(cell).numpy().astype(np.float64)
+    return om.layer_and_position_grad(pos.numpy(), box, x.numpy(), graph.src.cpu().numpy(),
+                                      graph.dst.cpu().numpy(), layer.W1.cpu().numpy(),
+                                      layer.b1.cpu().numpy(), layer.W2.cpu().numpy(), 5.0,
+                                      go.numpy())
+
+
+@pytest.mark.parametrize("n,c", [(80, 16), (300, 5)])
+def test_mace_layer_forward_and_forces(bm, dev, n, c):
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, n, c, 11)
+    p = pos.to(dev).requires_grad_(True)
+    out = layer(graph, p, x.to(dev))
+    out.backward(go.to(dev))
+    ref_out, ref_grad = _oracle(pos, cell, graph, layer, x, go)
+    assert normwise_err(out.detach().cpu(), ref_out) <= 1e-5
+    assert normwise_err(p.grad.cpu(), ref_grad) <= 1e-4
+    # translation invariance: the forces sum to zero
+    assert p.grad.sum(0).abs().max().item() <= 1e-5 * p.grad.abs().sum().item()
+
+
+def test_mace_layer_two_edge_chunks(bm, dev):
+    """~75k edges: two chunks of 65536 (rows split across chunks add up)."""
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, 2500, 2, 21)
+    assert graph.num_edges > 65536
+    p = pos.to(dev).requires_grad_(True)
+    out = layer(graph, p, x.to(dev))
+    out.backward(go.to(dev))
+    ref_out, ref_grad = _oracle(pos, cell, graph, layer, x, go)
+    assert normwise_err(out.detach().cpu(), ref_out) <= 1e-5
+    assert normwise_err(p.grad.cpu(), ref_grad) <= 1e-4
+
+
+def test_reverse_edges(bm, dev):
+    import batmobile
+    pos, cell = periodic_box(400, 31)
+    graph = batmobile.Graph(pos.to(dev), cell, 5.0, 8)
+    rev = graph.reverse_edges().cpu()
+    src, dst = graph.src.cpu(), graph.dst.cpu()
+    assert torch.equal(rev[rev], torch.arange(rev.numel()))
+    assert torch.equal(src[rev], dst) and torch.equal(dst[rev], src)
+    # a non-symmetric edge list is refused
+    with pytest.raises(RuntimeError, match="not symmetric"):
+        bm.mace_reverse_edges(graph.row_ptr, torch.zeros_like(graph.src))
+
+
+def test_mace_layer_is_deterministic(bm, dev):
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, 500, 8, 41)
+    outs, grads = [], []
+    for _ in range(2):
+        p = pos.to(dev).requires_grad_(True)
+        o = layer(graph, p, x.to(dev))
+        o.backward(go.to(dev))
+        outs.append(o.detach().cpu())
+        grads.append(p.grad.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
