@@ -9,7 +9,7 @@
 // weights are this configuration's.  Layer definition (fp32 here):
 //   v_e = min_image(pos[dst_e] - pos[src_e]), r = |v|, u = v / r
 //   B_k = sqrt(2/rc) sin(k pi r/rc) / r * f(r/rc),  f(d) = 1 - 28 d^6 + 48 d^7 - 21 d^8
-//   h = silu(B W1 + b1), R[e, c, p] = (h W2)[c * 34 + p]
+//   h = silu(B W1 + b1), R[e, c, p] = (h W2)[p * C + c]
 //   out[d, c, o] = sum_{e -> d} sum_p R[e,c,p] sum_{(a,b) in p -> o} CG x[src_e,c,a] Y_e[b]
 //
 // Work per edge: the MLP's second layer is a GEMM [edges x 64] x [64 x 34C]
@@ -75,13 +75,6 @@ __device__ __forceinline__ void radial_basis(float r, float rc, float* B, float*
 
 __device__ __forceinline__ float sigmoidf(float z) { return 1.0f / (1.0f + expf(-z)); }
 
-// An empty asm that takes and returns 16 values: everything computed from them
-// afterwards depends on this point and cannot be hoisted above it.
-__device__ __forceinline__ void launder16(float* v) {
-    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
-                      "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
-                      "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]));
-}
 
 // ---------------------------------------------------------------------------
 // edge vectors from positions (grid over edges)
@@ -223,7 +216,8 @@ __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
             xs[4 * q + 2] = t.z;
             xs[4 * q + 3] = t.w;
         }
-        const float* Rr = R + ((k - e0) * C + c) * kNumPaths;
+        // R[e, p, c]: lanes (channels) read consecutive addresses
+        const float* Rr = R + (k - e0) * C * kNumPaths + c;
         static_for<kNumPaths>([&](auto pp) {
             constexpr int p = decltype(pp)::value;
             constexpr int lo = kPathL[p][2];
@@ -234,7 +228,7 @@ __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
                 constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
                 tq[en.o - lo * lo] = fmaf(en.c * Y[en.b], xs[en.a], tq[en.o - lo * lo]);
             });
-            const float rp = Rr[p];
+            const float rp = Rr[p * C];
 #pragma unroll
             for (int q = 0; q < 2 * lo + 1; ++q) m[lo * lo + q] = fmaf(rp, tq[q], m[lo * lo + q]);
         });
@@ -299,44 +293,43 @@ __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
             xs[4 * q + 2] = t.z;
             xs[4 * q + 3] = t.w;
         }
-        const float* Rr = R + ((k - e0) * C + cc) * kNumPaths;
-        float* gRr = gR + ((k - e0) * C + cc) * kNumPaths;
+        // R and gR as [e, p, c]: lanes (channels) access consecutive addresses
+        const float* Rr = R + (k - e0) * C * kNumPaths + cc;
+        float* gRr = gR + (k - e0) * C * kNumPaths + cc;
         float gy[16];
 #pragma unroll
         for (int b = 0; b < 16; ++b) gy[b] = 0.0f;
-        // one path per iteration of a loop that is not unrolled: each path is a
-        // basic block of its own, so the 34 paths are not interleaved (which
-        // would keep several hundred temporaries live)
-#pragma clang loop unroll(disable)
-        for (int pk = 0; pk < kNumPaths; ++pk) {
-            // x, Y and g through empty asms each iteration: the products of the
-            // CG entries are formed per path instead of being hoisted out of the
-            // path loop (hundreds of loop-invariant values)
-            float xk[16], yk[16], gk[16];
+        // two passes over the paths, each fully unrolled (interleaving both in one
+        // pass keeps several hundred temporaries live):
+        // gR[p] = sum_m g[lo^2 + m] T_p[m] with T_p[m] = sum CG x[a] Y[b]
+        static_for<kNumPaths>([&](auto pp) {
+            constexpr int p = decltype(pp)::value;
+            constexpr int lo = kPathL[p][2];
+            float tq[2 * lo + 1];
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                xk[q] = xs[q];
-                yk[q] = Y[q];
-                gk[q] = g[q];
-            }
-            launder16(xk);
-            launder16(yk);
-            launder16(gk);
-            static_for<kNumPaths>([&](auto pp) {
-                constexpr int p = decltype(pp)::value;
-                if (pk == p) {
-                    const float rp = Rr[p];
-                    float gr = 0.0f;
-                    static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
-                        constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
-                        const float xg = xk[en.a] * gk[en.o];
-                        gr = fmaf(en.c * yk[en.b], xg, gr);
-                        gy[en.b] = fmaf(en.c * rp, xg, gy[en.b]);
-                    });
-                    if (live) gRr[p] = gr;
-                }
+            for (int q = 0; q < 2 * lo + 1; ++q) tq[q] = 0.0f;
+            static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
+                tq[en.o - lo * lo] = fmaf(en.c * Y[en.b], xs[en.a], tq[en.o - lo * lo]);
             });
-        }
+            float gr = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 2 * lo + 1; ++q) gr = fmaf(g[lo * lo + q], tq[q], gr);
+            if (live) gRr[p * C] = gr;
+        });
+        // gy[b] = sum over the entries of c x[a] R[p] g[o]
+        static_for<kNumPaths>([&](auto pp) {
+            constexpr int p = decltype(pp)::value;
+            constexpr int lo = kPathL[p][2];
+            const float rp = Rr[p * C];
+            float hq[2 * lo + 1];
+#pragma unroll
+            for (int q = 0; q < 2 * lo + 1; ++q) hq[q] = rp * g[lo * lo + q];
+            static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
+                gy[en.b] = fmaf(en.c * xs[en.a], hq[en.o - lo * lo], gy[en.b]);
+            });
+        });
         // sum gy over the channels: butterfly within each wave, then waves in order
 #pragma unroll
         for (int b = 0; b < 16; ++b) {

@@ -60,7 +60,7 @@ class MaceLayerFunction(torch.autograd.Function):
 class MACEInteraction(torch.nn.Module):
     """Interaction layer with per-edge radial weights (weights as buffers).
 
-    W1 [8, 64] ~ N(0, 1/8), b1 = 0, W2 [64, 34 C] ~ N(0, 1/64), column c * 34 + p
+    W1 [8, 64] ~ N(0, 1/8), b1 = 0, W2 [64, 34 C] ~ N(0, 1/64), column p * C + c
     weighting path p of channel c.
     """
 

@@ -168,6 +168,50 @@ def other_configs(torch, bm, dev):
     return res
 
 
+def mace_config4(torch, bm, dev, reps=3):
+    """MACE-style layer with per-edge radial weights at N = 50,000, C = 128
+    (uniform periodic box at ~30 neighbours within 5 A, seed 4): GPU neighbor list +
+    graph, forward, backward w.r.t. positions.  Flop model per edge: radial MLP
+    2 (8 64 + 64 34 C) and channel-wise CG product (1222 + 312) C forward; backward
+    recomputes the MLP and adds its transpose GEMM and twice the CG work."""
+    n, c = 50000, 128
+    g = torch.Generator().manual_seed(4)
+    L = (n / RHO) ** (1.0 / 3.0)
+    pos = (torch.rand(n, 3, generator=g) * L).to(dev)
+    cell = torch.diag(torch.tensor([L, L, L]))
+    x = torch.randn(n, c, 16, generator=g).to(dev)
+    go = torch.randn(n, c, 16, generator=g).to(dev)
+    layer = bm.MACEInteraction(c, CUTOFF, device=dev, generator=g)
+    graph = bm.Graph(pos, cell, CUTOFF, c)
+    graph.reverse_edges()
+    build = time_call(torch, lambda: (bm.Graph(pos, cell, CUTOFF, c).reverse_edges()), reps)
+    p = pos.clone().requires_grad_(True)
+    fwd, bwd = [], []
+    for _ in range(reps + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = layer(graph, p, x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        out.backward(go)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        fwd.append(t1 - t0)
+        bwd.append(t2 - t1)
+        p.grad = None
+    e = graph.num_edges
+    f_fwd = e * (2 * (8 * 64 + 64 * 34 * c) + (1222 + 312) * c)
+    f_bwd = e * (4 * (8 * 64 + 64 * 34 * c) + 2 * (1222 + 312) * c)
+    t_f, t_b = min(fwd[1:]), min(bwd[1:])
+    return {
+        "cfg4_mace_N": n, "cfg4_mace_C": c, "cfg4_mace_E": e,
+        "cfg4_mace_graph_build_ms": round(build, 3),
+        "cfg4_mace_fwd_ms": round(t_f * 1e3, 3), "cfg4_mace_bwd_ms": round(t_b * 1e3, 3),
+        "cfg4_mace_fwd_TFLOPs": round(f_fwd / t_f / 1e12, 2),
+        "cfg4_mace_bwd_TFLOPs": round(f_bwd / t_b / 1e12, 2),
+    }
+
+
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     passes recorded in profiles/hbm_traffic.txt (scaled by the copy calibration)."""
@@ -252,6 +296,7 @@ def main():
     extra["index_order_kernel_ms"] = round(time_call(torch, lambda: graph.sh_tp_scatter_index_order(w["x"]), 20), 4)
     extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
     extra.update(other_configs(torch, bm, dev))
+    extra.update(mace_config4(torch, bm, dev))
 
     res = {
         "metric": METRIC,

@@ -246,7 +246,7 @@ size_t neighbor_list_estimate_memory(int64_t N, float density, float cutoff);
  * are the baseline's configs[4]).
  *   v_e = min_image(pos[dst] - pos[src]); B_k(r) = sqrt(2/rc) sin(k pi r/rc)/r f(r/rc),
  *   f(d) = 1 - 28 d^6 + 48 d^7 - 21 d^8; h = silu(B W1 + b1) with W1 [8,64], b1 [64];
- *   R[e,c,p] = (h W2)[c*34 + p] with W2 [64, 34 C];
+ *   R[e,c,p] = (h W2)[p*C + c] with W2 [64, 34 C];
  *   out[d,c,o] = sum_{e->d} sum_p R[e,c,p] sum_{(a,b) in p->o} CG x[src,c,a] Y(v_e/|v_e|)[b].
  * Edges grouped by destination (row_ptr [N+1]) with sources ascending per row,
  * symmetric (every (j->i) has (i->j)), as batmobile.Graph builds them.  box is a

@@ -18,7 +18,7 @@ against this composition:
              Gasteiger, Gross, Guennemann, "Directional message passing for
              molecular graphs", ICLR 2020)
   h_e      = silu(B(r_e) W1 + b1)                           [E, 64]
-  R[e,c,p] = (h_e W2)[c * 34 + p]                           W2 [64, 34 C]
+  R[e,c,p] = (h_e W2)[p * C + c]                            W2 [64, 34 C]
   Y_e      = SH_3(u_e)                                      (spherical_harmonics.cu:33-97)
   m[e,c,o] = sum_p R[e,c,p] sum_{(a,b) in p -> o} CG x[src_e, c, a] Y_e[b]
   out[d]   = sum_{e: dst_e = d} m[e]
@@ -71,7 +71,7 @@ def layer(pos, box, x, src, dst, w1, b1, w2, rc):
     b = radial_basis(r, rc, xp=torch)
     h = torch.nn.functional.silu(b @ w1 + b1)
     c = x.shape[1]
-    R = (h @ w2).view(-1, c, NUM_PATHS)
+    R = (h @ w2).view(-1, NUM_PATHS, c).transpose(1, 2)          # [E, C, 34]
     y = sh.spherical_harmonics(u, 3, xp=torch)
     m = channelwise_tp(x[src], y, R)                                # [E, C, 16]
     return torch.zeros(pos.shape[0], c, 16, dtype=torch.float64).index_add_(0, dst, m)
