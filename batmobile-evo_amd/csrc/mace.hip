@@ -128,58 +128,108 @@ __global__ __launch_bounds__(256) void mace_radial_kernel(const float* __restric
 
 // ---------------------------------------------------------------------------
 // fp32 GEMM on MFMA: C[M, N] = A[M, K] B, with B = [K, N] (row-major) or, when
-// TB, given as B^T [N, K] (row-major).  Tile 64 x 64, K step 16, four waves:
-// wave w computes rows 16 w .. 16 w + 15 of the tile, four 16x16 MFMA tiles.
+// TB, given as B^T [N, K] (row-major).  Workgroup tile 128 x BN, K step 16,
+// four waves in 2 x 2, each 64 x BN/2 (4 x BN/32 MFMA tiles of 16 x 16).  Both
+// operands sit in LDS with k contiguous (sA[m][k], sB[n][k]), so one float4
+// read gives a lane its A (or B) values for four k-steps: k-step s of lane
+// group g = lane / 16 is k = 4 g + s, the same for A and B.
 // ---------------------------------------------------------------------------
-template <bool TB>
+template <bool TB, int BN>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A,
                                                        const float* __restrict__ B,
                                                        float* __restrict__ C, int M, int N, int K) {
-    __shared__ float sA[64][17];   // [m][k]
-    __shared__ float sB[16][65];   // [k][n]
+    constexpr int BM = 128, BK = 16, WN = BN / 2, NT = WN / 16;
+    constexpr int LD = BK + 4;  // row stride in floats (keeps float4 alignment)
+    __shared__ __attribute__((aligned(16))) float sA[BM * LD];
+    __shared__ __attribute__((aligned(16))) float sB[BN * LD];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv >> 1, wn = wv & 1;
     const int g4 = lane >> 4, i16 = lane & 15;
-    const int64_t m0 = (int64_t)blockIdx.y * 64;
-    const int n0 = blockIdx.x * 64;
-    v4f acc[4];
+    const int64_t m0 = (int64_t)blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const bool k4 = (K & 3) == 0, n4 = (N & 3) == 0;  // float4 global loads possible
+    v4f acc[4][NT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NT; ++ni) acc[mi][ni] = v4f{0.f, 0.f, 0.f, 0.f};
+    // one float4 of a row-major [rows, K] matrix (zeros past the edges)
+    auto ld_rowk = [&](const float* P, int64_t row, int64_t rows, int k) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row < rows) {
+            const float* q = P + row * K + k;
+            if (k4 && k + 3 < K) {
+                v = *reinterpret_cast<const float4*>(q);
+            } else {
+                v.x = k < K ? q[0] : 0.f;
+                v.y = k + 1 < K ? q[1] : 0.f;
+                v.z = k + 2 < K ? q[2] : 0.f;
+                v.w = k + 3 < K ? q[3] : 0.f;
+            }
+        }
+        return v;
+    };
+    for (int k0 = 0; k0 < K; k0 += BK) {
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int i = tid + it * 256;
-            {   // A: 64 rows x 16 k, k fastest (row-major A)
-                const int m = i >> 4, k = i & 15;
-                const int64_t gm = m0 + m;
-                sA[m][k] = (gm < M && k0 + k < K) ? A[gm * K + k0 + k] : 0.0f;
+        for (int it = 0; it < BM * BK / 4 / 256; ++it) {
+            const int idx = tid + it * 256, m = idx >> 2, kq = idx & 3;
+            *reinterpret_cast<float4*>(sA + m * LD + 4 * kq) = ld_rowk(A, m0 + m, M, k0 + 4 * kq);
+        }
+        if constexpr (TB) {
+#pragma unroll
+            for (int it = 0; it < BN * BK / 4 / 256; ++it) {
+                const int idx = tid + it * 256, n = idx >> 2, kq = idx & 3;
+                *reinterpret_cast<float4*>(sB + n * LD + 4 * kq) = ld_rowk(B, n0 + n, N, k0 + 4 * kq);
             }
-            if constexpr (TB) {  // B^T [N, K]: k fastest
-                const int n = i >> 4, k = i & 15;
-                sB[k][n] = (n0 + n < N && k0 + k < K) ? B[(int64_t)(n0 + n) * K + k0 + k] : 0.0f;
-            } else {             // B [K, N]: n fastest
-                const int k = i >> 6, n = i & 63;
-                sB[k][n] = (n0 + n < N && k0 + k < K) ? B[(int64_t)(k0 + k) * N + n0 + n] : 0.0f;
+        } else {
+#pragma unroll
+            for (int it = 0; it < BN * BK / 4 / 256; ++it) {
+                const int idx = tid + it * 256, k = idx / (BN / 4), nq = idx % (BN / 4);
+                const int kk = k0 + k, nn = n0 + 4 * nq;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (kk < K) {
+                    const float* q = B + (int64_t)kk * N + nn;
+                    if (n4 && nn + 3 < N) {
+                        v = *reinterpret_cast<const float4*>(q);
+                    } else {
+                        v.x = nn < N ? q[0] : 0.f;
+                        v.y = nn + 1 < N ? q[1] : 0.f;
+                        v.z = nn + 2 < N ? q[2] : 0.f;
+                        v.w = nn + 3 < N ? q[3] : 0.f;
+                    }
+                }
+                sB[(4 * nq + 0) * LD + k] = v.x;
+                sB[(4 * nq + 1) * LD + k] = v.y;
+                sB[(4 * nq + 2) * LD + k] = v.z;
+                sB[(4 * nq + 3) * LD + k] = v.w;
             }
         }
         __syncthreads();
+        float4 a[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const float a = sA[16 * wv + i16][4 * ks + g4];
+        for (int mi = 0; mi < 4; ++mi)
+            a[mi] = *reinterpret_cast<const float4*>(sA + (wm * 64 + mi * 16 + i16) * LD + 4 * g4);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[t] = mfma1(a, sB[4 * ks + g4][16 * t + i16], acc[t]);
+        for (int ni = 0; ni < NT; ++ni) {
+            const float4 b =
+                *reinterpret_cast<const float4*>(sB + (wn * WN + ni * 16 + i16) * LD + 4 * g4);
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) acc[mi][ni] = mfma4(a[mi], b, acc[mi][ni]);
         }
     }
-    // D[4 g4 + r][i16] of tile t: row m0 + 16 wv + 4 g4 + r, column n0 + 16 t + i16
+    // D[4 g4 + r][i16] of tile (mi, ni)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int n = n0 + 16 * t + i16;
+    for (int ni = 0; ni < NT; ++ni) {
+        const int n = n0 + wn * WN + ni * 16 + i16;
         if (n >= N) continue;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + 16 * wv + 4 * g4 + r;
-            if (m < M) C[m * N + n] = acc[t][r];
-        }
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + wm * 64 + mi * 16 + 4 * g4 + r;
+                if (m < M) C[m * N + n] = acc[mi][ni][r];
+            }
     }
 }
 
@@ -202,6 +252,14 @@ __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
 #pragma unroll
     for (int o = 0; o < 16; ++o) m[o] = 0.0f;
     for (int64_t k = s; k < e; ++k) {
+        // the edge's 34 weights R[e, p, c] first (lanes = channels read consecutive
+        // addresses), so their latency overlaps the SH and the x gather
+        float rr[kNumPaths];
+        {
+            const float* Rr = R + (k - e0) * C * kNumPaths + c;
+#pragma unroll
+            for (int p = 0; p < kNumPaths; ++p) rr[p] = Rr[p * C];
+        }
         float ux = vec[k * 3], uy = vec[k * 3 + 1], uz = vec[k * 3 + 2];
         normalize3(ux, uy, uz);
         float Y[16];
@@ -216,8 +274,6 @@ __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
             xs[4 * q + 2] = t.z;
             xs[4 * q + 3] = t.w;
         }
-        // R[e, p, c]: lanes (channels) read consecutive addresses
-        const float* Rr = R + (k - e0) * C * kNumPaths + c;
         static_for<kNumPaths>([&](auto pp) {
             constexpr int p = decltype(pp)::value;
             constexpr int lo = kPathL[p][2];
@@ -228,7 +284,7 @@ __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
                 constexpr CGEntry en = kCG[kPathEntry[p] + decltype(ee)::value];
                 tq[en.o - lo * lo] = fmaf(en.c * Y[en.b], xs[en.a], tq[en.o - lo * lo]);
             });
-            const float rp = Rr[p * C];
+            const float rp = rr[p];
 #pragma unroll
             for (int q = 0; q < 2 * lo + 1; ++q) m[lo * lo + q] = fmaf(rp, tq[q], m[lo * lo + q]);
         });
@@ -279,6 +335,13 @@ __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
         }
     }
     for (int64_t k = s; k < e; ++k) {
+        // the edge's 34 weights first: their latency overlaps the gR pass
+        float rr[kNumPaths];
+        {
+            const float* Rr = R + (k - e0) * C * kNumPaths + cc;
+#pragma unroll
+            for (int p = 0; p < kNumPaths; ++p) rr[p] = Rr[p * C];
+        }
         float ux = vec[k * 3], uy = vec[k * 3 + 1], uz = vec[k * 3 + 2];
         normalize3(ux, uy, uz);
         float Y[16];
@@ -293,8 +356,7 @@ __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
             xs[4 * q + 2] = t.z;
             xs[4 * q + 3] = t.w;
         }
-        // R and gR as [e, p, c]: lanes (channels) access consecutive addresses
-        const float* Rr = R + (k - e0) * C * kNumPaths + cc;
+        // gR as [e, p, c]: lanes (channels) write consecutive addresses
         float* gRr = gR + (k - e0) * C * kNumPaths + cc;
         float gy[16];
 #pragma unroll
@@ -321,7 +383,7 @@ __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
         static_for<kNumPaths>([&](auto pp) {
             constexpr int p = decltype(pp)::value;
             constexpr int lo = kPathL[p][2];
-            const float rp = Rr[p * C];
+            const float rp = rr[p];
             float hq[2 * lo + 1];
 #pragma unroll
             for (int q = 0; q < 2 * lo + 1; ++q) hq[q] = rp * g[lo * lo + q];
@@ -490,10 +552,17 @@ static MaceWs mace_ws(void* base, int64_t E, int C, bool backward) {
 static int gemm_launch(const float* A, const float* B, float* Cm, int64_t M, int N, int K, bool tb,
                        hipStream_t s) {
     if (M <= 0 || N <= 0 || K <= 0) return BM_OK;
-    dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
+    const bool narrow = N <= 64;  // 128 x 64 tiles for narrow outputs, else 128 x 128
+    const int bn = narrow ? 64 : 128;
+    dim3 grid((unsigned)ceil_div(N, bn), (unsigned)ceil_div(M, 128));
     if (grid.y > 65535) return BM_ERR_ARG;
-    if (tb) gemm_f32_kernel<true><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
-    else gemm_f32_kernel<false><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+    if (tb) {
+        if (narrow) gemm_f32_kernel<true, 64><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+        else gemm_f32_kernel<true, 128><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+    } else {
+        if (narrow) gemm_f32_kernel<false, 64><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+        else gemm_f32_kernel<false, 128><<<grid, 256, 0, s>>>(A, B, Cm, (int)M, N, K);
+    }
     return (int)hipGetLastError();
 }
 
