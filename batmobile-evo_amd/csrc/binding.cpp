@@ -496,7 +496,7 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t> mp_sch
     torch::Tensor ep = torch::empty({E}, i64);
     const c10::DeviceGuard guard(row_ptr.device());
     const size_t wsb = batteries_mp_schedule_workspace_bytes(nb, rpb);
-    torch::Tensor ws = torch::empty({ns}, i64);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
     check_status(batteries_mp_schedule(cptr<int64_t>(row_ptr, "row_ptr"), cp,
                                        cptr<int64_t>(order, "order"), N, E, (int)C, nb, rpb,
                                        rps.data_ptr<int64_t>(), dst.data_ptr<int64_t>(),

@@ -31,18 +31,24 @@ constexpr int kChanGroup = 64;    // channels per workgroup (4 waves x 16)
 constexpr int kPrefetch = 16;     // source-row gathers in flight per lane
 constexpr int kMaxRowsPerBlock = 64;    // destinations per workgroup (row_ptr slice in LDS)
 
+// Operator rows sit in LDS with their four 16-byte column quads permuted by
+// quad_swizzle(o): the phase-2 read of one edge (lane (o, g) reads quad g of
+// row o) then covers all 32 banks in every group of 8 lanes.
+__host__ __device__ constexpr int quad_swizzle(int o) { return (o >> 1) & 3; }
+
 // Phase 1: lane j of wave w builds rows 4w..4w+3 of M for edge j of the batch.
 template <int W>
 __device__ __forceinline__ void build_rows(const float* Y, float* sMj) {
     static_for<4>([&](auto rr) {
         constexpr int o = 4 * W + decltype(rr)::value;
+        constexpr int sw = quad_swizzle(o);
         float m[16];
         edge_operator_row<o>(Y, m);
         float4* dst = reinterpret_cast<float4*>(sMj + o * 16);
-        dst[0] = make_float4(m[0], m[1], m[2], m[3]);
-        dst[1] = make_float4(m[4], m[5], m[6], m[7]);
-        dst[2] = make_float4(m[8], m[9], m[10], m[11]);
-        dst[3] = make_float4(m[12], m[13], m[14], m[15]);
+        dst[0 ^ sw] = make_float4(m[0], m[1], m[2], m[3]);
+        dst[1 ^ sw] = make_float4(m[4], m[5], m[6], m[7]);
+        dst[2 ^ sw] = make_float4(m[8], m[9], m[10], m[11]);
+        dst[3 ^ sw] = make_float4(m[12], m[13], m[14], m[15]);
     });
 }
 
@@ -251,7 +257,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
                                               row_bytes);
                 first = false;
             }
-            const float* mrow = sM + i16 * 16 + 4 * g;
+            const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));
             float4 mr[2];
             mr[0] = *reinterpret_cast<const float4*>(mrow);
             if (lim >= kBatch + kPrefetch) {
@@ -322,7 +328,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kSBatch = 32;       // edges per batch (operators in LDS)
 constexpr int kRing = kSBatch;    // gathers in flight per lane
-constexpr int kScatterRows = 10;  // rows per workgroup (all staged in LDS)
+constexpr int kScatterRows = 11;  // row slots per workgroup (all staged in LDS)
 constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
 template <bool NORM, bool BUF, bool PERM>
@@ -411,7 +417,10 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         constexpr int u = decltype(uu)::value;
         ring[u] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, u), row_bytes);
     });
-    for (int64_t kb = e0; kb < e1; kb += kSBatch) {
+    // The loop's back edge is taken from full batches only; the last batch
+    // (full or not) leaves through the tail path, which issues no gathers and
+    // walks only the groups of 8 edges that hold real edges.
+    for (int64_t kb = e0;; kb += kSBatch) {
         const int nb = (int)min<int64_t>(kSBatch, e1 - kb);
         __syncthreads();
         phase1_build<NORM>(cur, nb, sM);
@@ -424,32 +433,49 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             if (row_last[r] >= 0 && p >= 0 && p < kSBatch) ends |= 1ull << p;
         });
         __syncthreads();
+        const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));
+        float4 mr[kLdsAhead + 1];
+        // edge j: four MFMAs into the row accumulator, the gather of the edge
+        // kRing positions ahead (GATHER), the row's staging when j closes it
+        auto edge = [&](auto jj, auto gather_c) {
+            constexpr int j = decltype(jj)::value;
+            if constexpr (j + kLdsAhead < kSBatch)
+                mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
+                    *reinterpret_cast<const float4*>(mrow + (j + kLdsAhead) * kMStride);
+            acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
+            if constexpr (decltype(gather_c)::value)
+                ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, j), row_bytes);
+            if ((ends >> j) & 1ull) {
+                sStage[w][slot][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                ++slot;
+                acc = zero4;
+            }
+        };
+        if (kb + kSBatch >= e1) {
+            static_for<kLdsAhead>([&](auto qq) {
+                constexpr int q = decltype(qq)::value;
+                mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
+            });
+            static_for<kSBatch / 8>([&](auto gg) {
+                constexpr int g8 = decltype(gg)::value;
+                if (8 * g8 < nb)
+                    static_for<8>([&](auto ii) {
+                        edge(std::integral_constant<int, 8 * g8 + decltype(ii)::value>{},
+                             std::false_type{});
+                    });
+            });
+            break;
+        }
         const EdgeRec nn = record(id2);
         id2 = edge_id(kb + 3 * kSBatch);
         // keep these loads ahead of the gathers: sunk below them, they would be
         // the youngest loads when the next batch needs them
         __builtin_amdgcn_sched_barrier(0);
-        {
-            const float* mrow = sM + i16 * 16 + 4 * g;
-            float4 mr[kLdsAhead + 1];
-            static_for<kLdsAhead>([&](auto qq) {
-                constexpr int q = decltype(qq)::value;
-                mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
-            });
-            static_for<kSBatch>([&](auto jj) {
-                constexpr int j = decltype(jj)::value;
-                if constexpr (j + kLdsAhead < kSBatch)
-                    mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
-                        *reinterpret_cast<const float4*>(mrow + (j + kLdsAhead) * kMStride);
-                acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
-                ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, j), row_bytes);
-                if ((ends >> j) & 1ull) {
-                    sStage[w][slot][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-                    ++slot;
-                    acc = zero4;
-                }
-            });
-        }
+        static_for<kLdsAhead>([&](auto qq) {
+            constexpr int q = decltype(qq)::value;
+            mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
+        });
+        static_for<kSBatch>([&](auto jj) { edge(jj, std::true_type{}); });
         cur = nxt;
         nxt = nn;
     }
@@ -740,32 +766,186 @@ extern "C" int batteries_edge_index_to_csr(const int64_t* edge_index, int64_t* r
 
 // ---------------------------------------------------------------------------
 // Destination schedule: the fused scatter kernel runs n_blocks workgroups of
-// rows_per_block scheduled rows.  Scheduled row q of workgroup b = q / R at
-// position t = q % R processes destination order[m] with
-//     m = x*P*R + k + t*P,   x = b / P (the XCD), k = b % P, P = n_blocks / 8,
-// so each XCD works on one contiguous eighth of the spatial order and its
-// resident workgroups step through consecutive rows of it together: the rows
-// in flight on an XCD stay spatially compact and their source rows stay in L2.
+// rows_per_block (R) row slots; slot t of workgroup b is scheduled row
+// q = b * R + t.  Workgroup b = x * P + k runs on XCD x (P = n_blocks / 8), and
+// the workgroups of an XCD run in generations of Q resident ones.
+//
+//   - Each (XCD, generation) group owns a contiguous range of the spatial
+//     order, cut so that every group holds edges in proportion to its number
+//     of workgroups (at most Qg * R rows).
+//   - Inside a group the rows are dealt in slices of Qg consecutive spatial
+//     positions: slice t goes to slot t of the group's workgroups, so the rows
+//     in flight on an XCD at one time stay spatially compact and their source
+//     rows stay in L2.  Within a slice the heaviest row goes to the lightest
+//     workgroup so far; a few rounds of pairwise swaps inside slices (the i-th
+//     heaviest workgroup with the i-th lightest) then even out the totals.
+//
+// The kernel time is that of the busiest compute unit, so equal edge counts
+// per workgroup matter: at configs[3] this brings the largest workgroup from
+// 361 edges (fixed rows per workgroup) to within a few percent of the mean.
+// Every destination is still summed by one wave in ascending edge order, so
+// the result does not depend on the schedule.
 // ---------------------------------------------------------------------------
 namespace bmhip {
 
-__global__ void sched_rows_kernel(const int64_t* __restrict__ row_ptr,
-                                  const int64_t* __restrict__ order, int64_t* __restrict__ row_dst,
-                                  int64_t* __restrict__ deg, int64_t n_dst, int64_t n_sched, int P,
-                                  int R, int Q) {
-    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= n_sched) return;
-    const int64_t b = q / R, t = q - b * R;
-    const int64_t x = b / P, k = b - x * P;
-    // workgroups of an XCD run in generations of Q resident ones; generation
-    // `gen` owns a contiguous chunk of Qg * R positions, interleaved by row
-    const int64_t gen = k / Q, kk = k - gen * Q;
-    const int64_t Qg = std::min<int64_t>(Q, P - gen * Q);
-    const int64_t m = x * P * R + gen * Q * R + kk + t * Qg;
-    const int64_t d = m < n_dst ? order[m] : -1;
-    const bool ok = d >= 0 && d < n_dst;
-    row_dst[q] = ok ? d : -1;
-    deg[q] = ok ? row_ptr[d + 1] - row_ptr[d] : 0;
+constexpr int kSchedMaxQ = 256;       // workgroups of one group (threads of the balancing block)
+constexpr int kSchedSwapRounds = 8;
+
+// degm[m] = in-degree of destination order[m]
+__global__ void sched_degm_kernel(const int64_t* __restrict__ row_ptr,
+                                  const int64_t* __restrict__ order, int64_t* __restrict__ degm,
+                                  int64_t n_dst) {
+    const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= n_dst) return;
+    const int64_t d = order[m];
+    degm[m] = (d >= 0 && d < n_dst) ? row_ptr[d + 1] - row_ptr[d] : 0;
+}
+
+// Group boundaries gb[0 .. 8G] in spatial positions (one thread; 8G groups).
+__global__ void sched_groups_kernel(const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
+                                    int R, int64_t* __restrict__ gb) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    const int G = (P + Q - 1) / Q;
+    const int64_t E = cum[n_dst];
+    const int64_t total_wg = 8LL * P;
+    int64_t start = 0;
+    gb[0] = 0;
+    int gi = 0;
+    for (int x = 0; x < 8; ++x) {
+        for (int gen = 0; gen < G; ++gen, ++gi) {
+            const int Qg = min(Q, P - gen * Q);
+            const int64_t w_end = (int64_t)x * P + (int64_t)gen * Q + Qg;
+            const double target = (double)E * (double)w_end / (double)total_wg;
+            // first position whose cumulative edge count reaches the target,
+            // or the one before it when that is closer
+            int64_t lo = 0, hi = n_dst;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi) >> 1;
+                if ((double)cum[mid] < target) lo = mid + 1;
+                else hi = mid;
+            }
+            int64_t pos = lo;
+            if (pos > 0 && target - (double)cum[pos - 1] < (double)cum[pos] - target) --pos;
+            // leave room for the rows of the later groups, and fit Qg * R slots
+            const int64_t low = max(start, n_dst - (total_wg - w_end) * (int64_t)R);
+            const int64_t high = min(n_dst, start + (int64_t)Qg * R);
+            pos = max(low, min(high, pos));
+            gb[gi + 1] = pos;
+            start = pos;
+        }
+    }
+}
+
+// One block per group: deal the group's rows to its workgroups' slots.
+__global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
+    const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
+    const int64_t* __restrict__ gb, int64_t n_dst, int P, int Q, int R,
+    int64_t* __restrict__ row_dst, int64_t* __restrict__ slot_deg) {
+    __shared__ int64_t sLoad[kSchedMaxQ];
+    __shared__ int64_t sA[kScatterRows][kSchedMaxQ];   // degree in (slot, workgroup)
+    __shared__ int sPos[kScatterRows][kSchedMaxQ];     // row (offset in the group) or -1
+    __shared__ int sAt[kSchedMaxQ];
+    const int G = (P + Q - 1) / Q;
+    const int gi = blockIdx.x;
+    const int x = gi / G, gen = gi - x * G;
+    const int Qg = min(Q, P - gen * Q);
+    const int k = threadIdx.x;
+    const int64_t s0 = gb[gi], s1 = gb[gi + 1];
+    const int n = (int)(s1 - s0);
+    const int T = (n + Qg - 1) / Qg;  // <= R: a group holds at most Qg * R rows
+    sLoad[k] = 0;
+    for (int t = 0; t < kScatterRows; ++t) {
+        sA[t][k] = 0;
+        sPos[t][k] = -1;
+    }
+    __syncthreads();
+    for (int t = 0; t < T; ++t) {
+        const int64_t m0 = s0 + (int64_t)t * Qg;
+        const int nt = (int)min<int64_t>(Qg, s1 - m0);
+        if (k < nt) {  // rank of row k in the slice, heaviest first
+            const int64_t dk = degm[m0 + k];
+            int r = 0;
+            for (int j = 0; j < nt; ++j) {
+                const int64_t dj = degm[m0 + j];
+                r += (dj > dk) || (dj == dk && j < k);
+            }
+            sAt[r] = k;
+        }
+        int rw = 0;  // rank of workgroup k, lightest first
+        if (k < Qg) {
+            const int64_t lk = sLoad[k];
+            for (int l = 0; l < Qg; ++l) {
+                const int64_t ll = sLoad[l];
+                rw += (ll < lk) || (ll == lk && l < k);
+            }
+        }
+        __syncthreads();
+        if (k < Qg && rw < nt) {
+            const int i = sAt[rw];
+            const int64_t d = degm[m0 + i];
+            sA[t][k] = d;
+            sPos[t][k] = (int)(m0 + i - s0);
+            sLoad[k] += d;
+        }
+        __syncthreads();
+    }
+    for (int rd = 0; rd < kSchedSwapRounds; ++rd) {
+        int rw = 0;
+        if (k < Qg) {
+            const int64_t lk = sLoad[k];
+            for (int l = 0; l < Qg; ++l) {
+                const int64_t ll = sLoad[l];
+                rw += (ll < lk) || (ll == lk && l < k);
+            }
+        }
+        __syncthreads();
+        if (k < Qg) sAt[rw] = k;
+        __syncthreads();
+        if (k < Qg / 2) {  // pair: k-th lightest with k-th heaviest
+            const int l = sAt[k], h = sAt[Qg - 1 - k];
+            const int64_t diff = sLoad[h] - sLoad[l];
+            int best = -1;
+            int64_t bv = diff;
+            for (int t = 0; t < T; ++t) {
+                const int64_t d = sA[t][h] - sA[t][l];
+                if (d > 0 && d < diff) {
+                    const int64_t v = diff > 2 * d ? diff - 2 * d : 2 * d - diff;
+                    if (v < bv) {
+                        bv = v;
+                        best = t;
+                    }
+                }
+            }
+            if (best >= 0) {
+                const int64_t d = sA[best][h] - sA[best][l];
+                const int64_t ah = sA[best][h];
+                const int ph = sPos[best][h];
+                sA[best][h] = sA[best][l];
+                sPos[best][h] = sPos[best][l];
+                sA[best][l] = ah;
+                sPos[best][l] = ph;
+                sLoad[h] -= d;
+                sLoad[l] += d;
+            }
+        }
+        __syncthreads();
+    }
+    if (k < Qg) {
+        const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
+        for (int t = 0; t < R; ++t) {
+            const int p = t < T ? sPos[t][k] : -1;
+            int64_t d = -1, dg = 0;
+            if (p >= 0) {
+                const int64_t o = order[s0 + p];
+                if (o >= 0 && o < n_dst) {
+                    d = o;
+                    dg = sA[t][k];
+                }
+            }
+            row_dst[b * R + t] = d;
+            slot_deg[b * R + t] = dg;
+        }
+    }
 }
 
 __global__ void sched_edges_kernel(const int64_t* __restrict__ row_ptr,
@@ -788,9 +968,11 @@ extern "C" int batteries_mp_schedule_shape(int64_t N_dst, int C, int* n_blocks,
     if (N_dst < 0 || C <= 0 || !n_blocks || !rows_per_block) return BM_ERR_ARG;
     int64_t P = blocks_per_xcd(C);
     int64_t R = std::max<int64_t>(1, ceil_div(N_dst, 8 * P));
-    if (R > kScatterRows) {
+    if (R + 1 <= kScatterRows) {
+        R += 1;  // one slot of headroom: groups are cut by edges, not rows
+    } else {
         R = kScatterRows;
-        P = ceil_div(N_dst, 8 * R);
+        P = ceil_div(N_dst, 8 * (R - 1));
     }
     if (8 * P > INT32_MAX) return BM_ERR_ARG;
     *n_blocks = (int)(8 * P);
@@ -798,8 +980,12 @@ extern "C" int batteries_mp_schedule_shape(int64_t N_dst, int C, int* n_blocks,
     return BM_OK;
 }
 
+// degm [N_dst], cum [N_dst + 1], group bounds [8 G + 1] (G <= n_blocks / 8),
+// slot degrees [n_blocks * rows_per_block]; N_dst <= n_blocks * rows_per_block.
 extern "C" size_t batteries_mp_schedule_workspace_bytes(int n_blocks, int rows_per_block) {
-    return sizeof(int64_t) * (size_t)n_blocks * (size_t)rows_per_block;
+    if (n_blocks <= 0 || rows_per_block <= 0) return 0;
+    const size_t ns = (size_t)n_blocks * (size_t)rows_per_block;
+    return sizeof(int64_t) * (3 * ns + (size_t)n_blocks + 2);
 }
 
 extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_perm,
@@ -814,13 +1000,22 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
     if (n_sched < N_dst) return BM_ERR_ARG;
     if (!workspace || workspace_bytes < batteries_mp_schedule_workspace_bytes(n_blocks, rows_per_block))
         return BM_ERR_WORKSPACE;
-    int64_t* deg = static_cast<int64_t*>(workspace);
     const int B = 256;
     const int P = n_blocks / 8;
-    const int Q = std::min(P, blocks_per_xcd(C));
-    sched_rows_kernel<<<(unsigned)ceil_div(n_sched, B), B, 0, stream>>>(
-        row_ptr, order, row_dst, deg, N_dst, n_sched, P, rows_per_block, Q);
-    int rc = batteries_exclusive_scan_i64(deg, row_ptr_s, n_sched, stream);
+    const int Q = std::min(std::min(P, blocks_per_xcd(C)), kSchedMaxQ);
+    const int G = (P + Q - 1) / Q;
+    int64_t* degm = static_cast<int64_t*>(workspace);
+    int64_t* cum = degm + N_dst;
+    int64_t* gb = cum + N_dst + 1;
+    int64_t* slot_deg = gb + 8 * (int64_t)G + 1;
+    if (N_dst > 0)
+        sched_degm_kernel<<<(unsigned)ceil_div(N_dst, B), B, 0, stream>>>(row_ptr, order, degm, N_dst);
+    int rc = batteries_exclusive_scan_i64(degm, cum, N_dst, stream);
+    if (rc != BM_OK) return rc;
+    sched_groups_kernel<<<1, 64, 0, stream>>>(cum, N_dst, P, Q, rows_per_block, gb);
+    sched_balance_kernel<<<(unsigned)(8 * G), kSchedMaxQ, 0, stream>>>(
+        degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
+    rc = batteries_exclusive_scan_i64(slot_deg, row_ptr_s, n_sched, stream);
     if (rc != BM_OK) return rc;
     sched_edges_kernel<<<(unsigned)ceil_div(n_sched, B), B, 0, stream>>>(row_ptr, col_perm, row_dst,
                                                                         row_ptr_s, edge_perm, n_sched);

@@ -136,9 +136,11 @@ int batteries_sh_tp_scatter_csr(const float* edge_vectors, const float* node_fea
  *                                their cell in a 32^3 grid over the box (host box[3])
  *   batteries_mp_schedule_shape  n_blocks (multiple of 8) x rows_per_block for C
  *   batteries_mp_schedule        row_ptr_s[n_blocks*rows_per_block + 1],
- *                                row_dst[n_blocks*rows_per_block] (-1 = padding),
+ *                                row_dst[n_blocks*rows_per_block] (-1 = empty slot),
  *                                edge_perm[E] (scheduled slot -> original edge; col_perm,
- *                                if given, is applied as in fused_message_passing_simple)
+ *                                if given, is applied as in fused_message_passing_simple);
+ *                                rows are dealt so that workgroups hold nearly equal
+ *                                numbers of edges
  * and consumed by batteries_sh_tp_scatter_scheduled, whose result equals
  * batteries_sh_tp_scatter_csr on the same graph. */
 size_t batteries_spatial_order_workspace_bytes(int64_t N);
