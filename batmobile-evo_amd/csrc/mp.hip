@@ -36,11 +36,16 @@ constexpr int kMaxRowsPerBlock = 64;    // destinations per workgroup (row_ptr s
 // row o) then covers all 32 banks in every group of 8 lanes.
 __host__ __device__ constexpr int quad_swizzle(int o) { return (o >> 1) & 3; }
 
-// Phase 1: lane j of wave w builds rows 4w..4w+3 of M for edge j of the batch.
+// Rows of M built by each wave in phase 1, chosen so that the four waves
+// carry nearly equal numbers of CG terms (168, 169, 168, 170 terms + writes;
+// rows in order of o would give 150, 189, 174, 162).
+constexpr int kRowsOfWave[4][4] = {{0, 1, 3, 5}, {2, 4, 6, 11}, {7, 9, 10, 14}, {8, 12, 13, 15}};
+
+// Phase 1: lane j of wave w builds rows kRowsOfWave[w] of M for edge j of the batch.
 template <int W>
 __device__ __forceinline__ void build_rows(const float* Y, float* sMj) {
     static_for<4>([&](auto rr) {
-        constexpr int o = 4 * W + decltype(rr)::value;
+        constexpr int o = kRowsOfWave[W][decltype(rr)::value];
         constexpr int sw = quad_swizzle(o);
         float m[16];
         edge_operator_row<o>(Y, m);
@@ -82,7 +87,13 @@ __device__ __forceinline__ void phase1_build(EdgeRec r, int nb, float* sM) {
     const int w = threadIdx.x >> 6;
     if (lane < nb) {
         float x = r.x, y = r.y, z = r.z;
-        if constexpr (NORM) normalize3(x, y, z);
+        if constexpr (NORM) {
+            // v / max(|v|, 1e-10) with one reciprocal square root (about 1 ulp)
+            const float inv = __builtin_amdgcn_rsqf(fmaxf(x * x + y * y + z * z, 1e-20f));
+            x *= inv;
+            y *= inv;
+            z *= inv;
+        }
         float Y[16];
         sh_forward<3>(x, y, z, Y);
         float* sMj = sM + lane * kMStride;
@@ -316,18 +327,19 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 // data-dependent condition has the same effect.  Hence the edge loop has
 // neither:
 //   - every batch is kSBatch edges fully unrolled, and every edge issues the
-//     gather for the edge kRing = kSBatch positions ahead (past the block's last
-//     edge it gathers row 0 of the same tensor, a valid address whose value is
-//     never used: edges past the end only touch the accumulator after the
-//     block's last row has been staged);
+//     gather for the edge kRing positions ahead (past the block's last edge it
+//     gathers row 0 of the same tensor, a valid address whose value is never
+//     used: edges past the end only touch the accumulator after the block's
+//     last row has been staged);
 //   - a finished row is staged in LDS (the workgroup owns at most kScatterRows
-//     rows) and all rows are written to HBM once, after the last batch.
+//     rows) and written to HBM only where no gather is in flight: at the start
+//     of the last batch and at the end.
 // The per-edge control is one scalar bit test: `ends` (a 64-bit mask per batch,
 // built with scalar arithmetic from the row ends) marks the edges that close a
 // row; there the accumulator is staged and reset to zero.
 // ---------------------------------------------------------------------------
 constexpr int kSBatch = 32;       // edges per batch (operators in LDS)
-constexpr int kRing = kSBatch;    // gathers in flight per lane
+constexpr int kRing = 32;         // gathers in flight per lane (edges ahead)
 constexpr int kScatterRows = 11;  // row slots per workgroup (all staged in LDS)
 constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
@@ -338,6 +350,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const int64_t* __restrict__ row_dst, float* __restrict__ out, int64_t n_rows, int C,
     int rows_per_block, int n_logical, uint32_t x_bytes) {
     static_assert(kSBatch % 2 == 0 && kSBatch <= 64, "one edge per lane in phase 1");
+    static_assert(kSBatch % kRing == 0, "ring slots must line up across batches");
     __shared__ __attribute__((aligned(16))) float sM[kSBatch * kMStride];
     __shared__ float4 sStage[4][kScatterRows][64];
     __shared__ int64_t sRow[kScatterRows + 1];
@@ -411,6 +424,18 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     // path, and the compiler would drain every gather at the loop latch.  (The
     // guard encloses the ring fill and the loop together for the same reason:
     // the loop header is reached only after the ring fill.)
+    // Write the rows that end at or before edge `upto` and are not written yet
+    // (staged rows in slot order; empty rows are zeros).
+    int r_out = 0, s_out = 0;
+    auto store_rows = [&](int64_t upto) {
+        for (; r_out < nrows && sRow[r_out + 1] <= upto; ++r_out) {
+            const int64_t orow = sDst[r_out];
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (sRow[r_out + 1] > sRow[r_out]) v = sStage[w][s_out++][lane];
+            if (c < C && orow >= 0)
+                *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
+        }
+    };
     float4 ring[kRing];
     if (e0 < e1) {
     static_for<kRing>([&](auto uu) {
@@ -436,15 +461,20 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));
         float4 mr[kLdsAhead + 1];
         // edge j: four MFMAs into the row accumulator, the gather of the edge
-        // kRing positions ahead (GATHER), the row's staging when j closes it
-        auto edge = [&](auto jj, auto gather_c) {
+        // kRing positions ahead (of the next batch only when NEXT), the row's
+        // staging when j closes it
+        auto edge = [&](auto jj, auto next_c) {
             constexpr int j = decltype(jj)::value;
+            constexpr int jn = j + kRing;
             if constexpr (j + kLdsAhead < kSBatch)
                 mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
                     *reinterpret_cast<const float4*>(mrow + (j + kLdsAhead) * kMStride);
-            acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
-            if constexpr (decltype(gather_c)::value)
-                ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, j), row_bytes);
+            acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j % kRing], acc);
+            if constexpr (jn < kSBatch)
+                ring[j % kRing] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, jn), row_bytes);
+            else if constexpr (decltype(next_c)::value)
+                ring[j % kRing] =
+                    gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, jn - kSBatch), row_bytes);
             if ((ends >> j) & 1ull) {
                 sStage[w][slot][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
                 ++slot;
@@ -452,6 +482,10 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             }
         };
         if (kb + kSBatch >= e1) {
+            // rows closed before this batch go to HBM now: the tail issues no
+            // gathers, so these stores hold nothing up, and the output is not
+            // written in one burst at the end of the kernel
+            store_rows(kb);
             static_for<kLdsAhead>([&](auto qq) {
                 constexpr int q = decltype(qq)::value;
                 mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
@@ -480,14 +514,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         nxt = nn;
     }
     }
-    int s = 0;
-    for (int r = 0; r < nrows; ++r) {
-        const int64_t orow = sDst[r];
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (sRow[r + 1] > sRow[r]) v = sStage[w][s++][lane];
-        if (c < C && orow >= 0)
-            *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
-    }
+    store_rows(e1);
 }
 
 // ---------------------------------------------------------------------------
