@@ -872,6 +872,7 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
     __shared__ int64_t sA[kScatterRows][kSchedMaxQ];   // degree in (slot, workgroup)
     __shared__ int sPos[kScatterRows][kSchedMaxQ];     // row (offset in the group) or -1
     __shared__ int sAt[kSchedMaxQ];
+    __shared__ int64_t sDeg[kScatterRows * kSchedMaxQ];  // degrees of the group's rows
     const int G = (P + Q - 1) / Q;
     const int gi = blockIdx.x;
     const int x = gi / G, gen = gi - x * G;
@@ -885,15 +886,16 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
         sA[t][k] = 0;
         sPos[t][k] = -1;
     }
+    for (int i = k; i < n; i += kSchedMaxQ) sDeg[i] = degm[s0 + i];
     __syncthreads();
     for (int t = 0; t < T; ++t) {
-        const int64_t m0 = s0 + (int64_t)t * Qg;
-        const int nt = (int)min<int64_t>(Qg, s1 - m0);
+        const int o0 = t * Qg;  // slice start, offset in the group
+        const int nt = min(Qg, n - o0);
         if (k < nt) {  // rank of row k in the slice, heaviest first
-            const int64_t dk = degm[m0 + k];
+            const int64_t dk = sDeg[o0 + k];
             int r = 0;
             for (int j = 0; j < nt; ++j) {
-                const int64_t dj = degm[m0 + j];
+                const int64_t dj = sDeg[o0 + j];
                 r += (dj > dk) || (dj == dk && j < k);
             }
             sAt[r] = k;
@@ -909,9 +911,9 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
         __syncthreads();
         if (k < Qg && rw < nt) {
             const int i = sAt[rw];
-            const int64_t d = degm[m0 + i];
+            const int64_t d = sDeg[o0 + i];
             sA[t][k] = d;
-            sPos[t][k] = (int)(m0 + i - s0);
+            sPos[t][k] = o0 + i;
             sLoad[k] += d;
         }
         __syncthreads();

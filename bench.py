@@ -32,6 +32,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "batmobile-evo_amd", "python"))
 sys.path.insert(0, REPO)
 
+SETTLE_STEPS = 500     # untimed launches before the warmup (GPU clock ramp)
 METRIC = "fused SH+TP+scatter edges/s (N=5k,C=64,~30 nbr) + % of HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_FP32_PEAK_TFLOPS = 157.3
@@ -237,6 +238,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time the configs[3] step only (skip the other configurations)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the workload, run 5 plain device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -265,6 +268,12 @@ def main():
     def step():
         return graph.sh_tp_scatter(w["x"], normalize=True)
 
+    # The GPU raises its clocks over the first ~25 ms of sustained load (this
+    # kernel: 82 us per launch cold, 65 us after ~350 launches).  SETTLE_STEPS
+    # untimed launches bring it to its loaded state before the W warmup steps,
+    # so that the K timed steps measure the steady state a serving loop sees.
+    for _ in range(SETTLE_STEPS):
+        out = step()
     for _ in range(a.warmup):
         out = step()
     torch.cuda.synchronize()
@@ -290,13 +299,14 @@ def main():
     traffic, traffic_note = measured_traffic("mp_scatter_kernel<true, true, true>", "configs[3]")
 
     extra = {}
-    pos_d = w["pos"].to(dev)
-    extra["neighbor_list_ms"] = round(time_call(torch, lambda: bm.neighbor_list(pos_d, w["cell"], CUTOFF, False)), 4)
-    extra["graph_build_ms"] = round(time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS)), 4)
-    extra["index_order_kernel_ms"] = round(time_call(torch, lambda: graph.sh_tp_scatter_index_order(w["x"]), 20), 4)
-    extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
-    extra.update(other_configs(torch, bm, dev))
-    extra.update(mace_config4(torch, bm, dev))
+    if not a.headline_only:
+        pos_d = w["pos"].to(dev)
+        extra["neighbor_list_ms"] = round(time_call(torch, lambda: bm.neighbor_list(pos_d, w["cell"], CUTOFF, False)), 4)
+        extra["graph_build_ms"] = round(time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS)), 4)
+        extra["index_order_kernel_ms"] = round(time_call(torch, lambda: graph.sh_tp_scatter_index_order(w["x"]), 20), 4)
+        extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
+        extra.update(other_configs(torch, bm, dev))
+        extra.update(mace_config4(torch, bm, dev))
 
     res = {
         "metric": METRIC,
@@ -305,6 +315,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
+        "settle_steps": SETTLE_STEPS,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -319,16 +330,20 @@ def main():
                       "(batmobile.Graph.sh_tp_scatter: spatial schedule)",
             "reference_published_rtx3090_ms": 5.935,
         },
+        # The kernel's measured HBM traffic (source rows served from L2) is a
+        # small fraction of its algorithmic bytes, whose rate exceeds the HBM
+        # peak; what bounds it is fp32 MFMA issue, so that is the roofline.
         "roofline": {
-            "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
-            "algorithmic_bytes_per_launch": bytes_alg, "kernel_ms": kernel_ms,
+            "bound": "mfma", "achieved": achieved_tf, "peak": MFMA_FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": achieved_tf / MFMA_FP32_PEAK_TFLOPS, "traffic": traffic,
+            "algorithmic_flops_per_launch": flops_alg, "kernel_ms": kernel_ms,
             "traffic_source": traffic_note,
         },
-        "roofline_mfma": {
-            "bound": "mfma", "achieved": achieved_tf, "peak": MFMA_FP32_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": achieved_tf / MFMA_FP32_PEAK_TFLOPS,
-            "algorithmic_flops_per_launch": flops_alg,
+        "roofline_hbm": {
+            "bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved_gbs / HBM_PEAK_GBS, "algorithmic_bytes_per_launch": bytes_alg,
+            "measured_bytes_per_launch": traffic,
+            "measured_GBs": (traffic / (kernel_ms * 1e-3) / 1e9) if traffic else None,
         },
         "also": extra,
     }

@@ -264,6 +264,29 @@ def test_scheduled_scatter_equals_index_order(bm, dev, n, c):
     assert normwise_err(a.cpu(), want) <= 1e-5
 
 
+def test_schedule_is_a_balanced_partition(bm, dev):
+    """Every destination in exactly one slot, edge_perm a permutation, workgroup
+    edge counts within 10% of the mean at the configs[3] density."""
+    import batmobile
+    n, c = 5000, 64
+    pos, cell = periodic_box(n, 3)
+    g = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+    rdst = g.row_dst.cpu()
+    assert torch.equal(torch.sort(rdst[rdst >= 0]).values, torch.arange(n))
+    assert torch.equal(torch.sort(g.edge_perm.cpu()).values, torch.arange(g.num_edges))
+    R, nb = g.rows_per_block, g.n_blocks
+    rps = g.row_ptr_s.cpu()
+    per_wg = (rps[torch.arange(1, nb + 1) * R] - rps[torch.arange(nb) * R]).double()
+    assert int(rps[-1]) == g.num_edges
+    assert per_wg.max().item() <= 1.10 * per_wg.mean().item()
+    # the slot degrees are the row lengths of the scheduled destinations
+    deg = (g.row_ptr[1:] - g.row_ptr[:-1]).cpu()
+    slot_deg = rps[1:] - rps[:-1]
+    ok = rdst >= 0
+    assert torch.equal(slot_deg[ok], deg[rdst[ok]])
+    assert int(slot_deg[~ok].abs().sum()) == 0
+
+
 def test_schedule_with_col_perm_matches_fused_message_passing_simple(bm, dev):
     n, e, c = 900, 20000, 32
     vec, x, src, dst = _random_graph(n, e, c, 51)
