@@ -72,7 +72,8 @@ def build_lib(force=False, jobs=4):
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, todo))
     if force or todo or _stale(LIB, objs):
-        _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", LIB] + objs)
+        _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", LIB] + objs
+             + ["-L" + os.path.join(ROCM, "lib"), "-lrocblas"])
     return LIB
 
 

@@ -204,3 +204,4 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 #define BM_OK 0
 #define BM_ERR_ARG -1
 #define BM_ERR_WORKSPACE -2
+#define BM_ERR_BLAS -3

@@ -7,11 +7,14 @@
  *   - Tensors are dense, row-major, fp32 (int64 for indices) as described.
  *   - Work is enqueued on `stream` and is asynchronous unless stated.
  *   - Return value: 0 on success, a hipError_t value (> 0) on a launch/runtime
- *     error, BM_ERR_ARG (-1) for invalid arguments, BM_ERR_WORKSPACE (-2) for a
- *     missing or too small workspace.
+ *     error, BATMOBILE_HIP_ERR_ARG (-1) for invalid arguments, BATMOBILE_HIP_ERR_WORKSPACE (-2) for a
+ *     missing or too small workspace, BATMOBILE_HIP_ERR_BLAS (-3) for a rocBLAS failure.
  *   - No function allocates device memory except the reference-compatible
  *     neighbor_list_cuda(); where scratch is needed the caller passes a
- *     workspace whose size is given by the matching *_workspace_bytes().
+ *     workspace whose size is given by the matching *_workspace_bytes().  The
+ *     MACE layer's plain GEMMs run on rocBLAS: its first call on a device
+ *     creates that device's rocBLAS handle (rocBLAS allocates its own
+ *     workspace then).
  *
  * Each entry point names the reference function it replaces
  * (paths relative to the reference repository).
@@ -33,6 +36,7 @@ extern "C" {
 #define BATMOBILE_HIP_OK 0
 #define BATMOBILE_HIP_ERR_ARG -1
 #define BATMOBILE_HIP_ERR_WORKSPACE -2
+#define BATMOBILE_HIP_ERR_BLAS -3
 
 /* ---------------------------------------------------------------------------
  * Spherical harmonics, L_max in [0, 6]
