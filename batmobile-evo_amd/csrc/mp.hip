@@ -828,38 +828,47 @@ __global__ void sched_degm_kernel(const int64_t* __restrict__ row_ptr,
     degm[m] = (d >= 0 && d < n_dst) ? row_ptr[d + 1] - row_ptr[d] : 0;
 }
 
-// Group boundaries gb[0 .. 8G] in spatial positions (one thread; 8G groups).
-__global__ void sched_groups_kernel(const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
-                                    int R, int64_t* __restrict__ gb) {
+// Group boundaries gb[0 .. 8G] in spatial positions.  First every group's
+// end is placed where the cumulative edge count reaches its share (one
+// thread per group), then one thread clamps the ends in order so that every
+// group fits its Qg * R slots and leaves room for the later groups.
+__global__ void sched_group_targets_kernel(const int64_t* __restrict__ cum, int64_t n_dst, int P,
+                                           int Q, int64_t* __restrict__ gb) {
+    const int G = (P + Q - 1) / Q;
+    const int gi = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= 8 * G) return;
+    const int x = gi / G, gen = gi - x * G;
+    const int Qg = min(Q, P - gen * Q);
+    const int64_t E = cum[n_dst];
+    const int64_t w_end = (int64_t)x * P + (int64_t)gen * Q + Qg;
+    const double target = (double)E * (double)w_end / (8.0 * (double)P);
+    // first position whose cumulative edge count reaches the target, or the
+    // one before it when that is closer
+    int64_t lo = 0, hi = n_dst;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((double)cum[mid] < target) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo > 0 && target - (double)cum[lo - 1] < (double)cum[lo] - target) --lo;
+    gb[gi + 1] = lo;
+}
+
+__global__ void sched_groups_kernel(int64_t n_dst, int P, int Q, int R, int64_t* __restrict__ gb) {
     if (blockIdx.x != 0 || threadIdx.x != 0) return;
     const int G = (P + Q - 1) / Q;
-    const int64_t E = cum[n_dst];
     const int64_t total_wg = 8LL * P;
     int64_t start = 0;
     gb[0] = 0;
-    int gi = 0;
-    for (int x = 0; x < 8; ++x) {
-        for (int gen = 0; gen < G; ++gen, ++gi) {
-            const int Qg = min(Q, P - gen * Q);
-            const int64_t w_end = (int64_t)x * P + (int64_t)gen * Q + Qg;
-            const double target = (double)E * (double)w_end / (double)total_wg;
-            // first position whose cumulative edge count reaches the target,
-            // or the one before it when that is closer
-            int64_t lo = 0, hi = n_dst;
-            while (lo < hi) {
-                const int64_t mid = (lo + hi) >> 1;
-                if ((double)cum[mid] < target) lo = mid + 1;
-                else hi = mid;
-            }
-            int64_t pos = lo;
-            if (pos > 0 && target - (double)cum[pos - 1] < (double)cum[pos] - target) --pos;
-            // leave room for the rows of the later groups, and fit Qg * R slots
-            const int64_t low = max(start, n_dst - (total_wg - w_end) * (int64_t)R);
-            const int64_t high = min(n_dst, start + (int64_t)Qg * R);
-            pos = max(low, min(high, pos));
-            gb[gi + 1] = pos;
-            start = pos;
-        }
+    for (int gi = 0; gi < 8 * G; ++gi) {
+        const int gen = gi % G;
+        const int Qg = min(Q, P - gen * Q);
+        const int64_t w_end = (int64_t)(gi / G) * P + (int64_t)gen * Q + Qg;
+        const int64_t low = max(start, n_dst - (total_wg - w_end) * (int64_t)R);
+        const int64_t high = min(n_dst, start + (int64_t)Qg * R);
+        const int64_t pos = max(low, min(high, gb[gi + 1]));
+        gb[gi + 1] = pos;
+        start = pos;
     }
 }
 
@@ -1041,7 +1050,9 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
         sched_degm_kernel<<<(unsigned)ceil_div(N_dst, B), B, 0, stream>>>(row_ptr, order, degm, N_dst);
     int rc = batteries_exclusive_scan_i64(degm, cum, N_dst, stream);
     if (rc != BM_OK) return rc;
-    sched_groups_kernel<<<1, 64, 0, stream>>>(cum, N_dst, P, Q, rows_per_block, gb);
+    sched_group_targets_kernel<<<(unsigned)ceil_div(8 * (int64_t)G, 64), 64, 0, stream>>>(cum, N_dst,
+                                                                                         P, Q, gb);
+    sched_groups_kernel<<<1, 64, 0, stream>>>(N_dst, P, Q, rows_per_block, gb);
     sched_balance_kernel<<<(unsigned)(8 * G), kSchedMaxQ, 0, stream>>>(
         degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
     rc = batteries_exclusive_scan_i64(slot_deg, row_ptr_s, n_sched, stream);
