@@ -287,6 +287,39 @@ def test_schedule_is_a_balanced_partition(bm, dev):
     assert int(slot_deg[~ok].abs().sum()) == 0
 
 
+@pytest.mark.parametrize("c", [64, 24])
+def test_schedule_with_skewed_degrees(bm, dev, c):
+    """One destination with more edges than a workgroup's share, rows of one
+    edge and isolated destinations: the scheduled kernel still matches the
+    oracle and the index-order kernel bit for bit."""
+    n = 3000
+    g = gen(61)
+    hub_src = torch.randint(0, n, (900,), generator=g)
+    hub_dst = torch.zeros(900, dtype=torch.int64)                 # destination 0: 900 edges
+    one_dst = torch.arange(1, 600)                                # destinations 1..599: one edge
+    one_src = torch.randint(0, n, (599,), generator=g)
+    mid_dst = torch.randint(600, 2000, (40000,), generator=g)     # 600..1999: ~29 edges each
+    mid_src = torch.randint(0, n, (40000,), generator=g)          # 2000..2999: no edges
+    src = torch.cat([hub_src, one_src, mid_src])
+    dst = torch.cat([hub_dst, one_dst, mid_dst])
+    e = src.numel()
+    vec = unit_vectors(e, 62) * (1.0 + torch.rand(e, 1, generator=g))
+    x = torch.randn(n, c, 16, generator=gen(63))
+    ei = torch.stack([src, dst]).to(dev)
+    rp, ci = bm.edge_index_to_csr(ei, n)
+    order = torch.randperm(n, generator=gen(64)).to(dev)
+    rps, ep, rdst, nb, rpb = bm.mp_schedule(rp, order, c, ci)
+    out = bm.sh_tp_scatter_scheduled(vec.to(dev), x.to(dev), ei[0].contiguous(), rps, ep, rdst, nb,
+                                     rpb, n, True)
+    idx = bm.sh_tp_scatter(vec.to(dev), x.to(dev), ei[0].contiguous(), rp, ci, True)
+    assert torch.equal(out, idx)
+    want = omp.sh_tp_scatter(vec.double().numpy(), x.double().numpy(), src.numpy(), dst.numpy(), n,
+                             normalize=True)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    assert out[2000:].abs().max().item() == 0.0
+    assert torch.equal(torch.sort(rdst[rdst >= 0].cpu()).values, torch.arange(n))
+
+
 def test_schedule_with_col_perm_matches_fused_message_passing_simple(bm, dev):
     n, e, c = 900, 20000, 32
     vec, x, src, dst = _random_graph(n, e, c, 51)
