@@ -53,6 +53,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, ui
 __device__ __forceinline__ float buffer_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
+// 16 bytes at a 4-byte aligned offset (one buffer_load_dwordx4)
+__device__ __forceinline__ float4 buffer_ld4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]),
+                       __int_as_float(v[3]));
+}
 
 __device__ __forceinline__ v4f mfma4(const float4 a, const float4 b, v4f acc) {
     acc = mfma1(a.x, b.x, acc);

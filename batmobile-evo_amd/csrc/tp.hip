@@ -373,12 +373,12 @@ template <int G, int KCO>
 __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const float* yb,
                                             const __amdgpu_buffer_rsrc_t wr, float* __restrict__ gx,
                                             int64_t n, int cin, int cout, int ct, const float* sG,
-                                            float* gyp) {
+                                            float* gyp, int64_t row0) {
     constexpr int PS = KCO * 16 + 4;
     constexpr int A0 = bwd_a0(G), NA = bwd_na(G);
     const int lane = threadIdx.x & 63;
     const int g4 = lane >> 4, i16 = lane & 15;
-    const int64_t row = (int64_t)blockIdx.x * kTile + i16;
+    const int64_t row = row0 + i16;
     const bool row_ok = row < n;
     const int64_t row_c = row_ok ? row : n - 1;  // clamped row for unconditional loads
     const int wpath_bytes = cin * cout * 4;
@@ -402,15 +402,25 @@ __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const f
     const int ciA = ci0 + i16;
     const int wrow = min(ciA, cin - 1) * cout;
     constexpr int NCB = KCO / 16;
+    // With cout % 4 == 0 a lane's 4 channels cb*16 + 4 g4 + (0..3) are either all
+    // below cout or all at or above it (then clamped to the last 4, which meet zero
+    // g rows): one 16-byte load per chunk instead of four.
+    const bool w_vec = (cout & 3) == 0;  // uniform
     auto load_w = [&](int p, float4* dst) {
         const int so = p * wpath_bytes;
+        if (w_vec) {
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            float a[4];
+            for (int cb = 0; cb < NCB; ++cb)
+                dst[cb] = buffer_ld4(wr, (wrow + min(cb * 16 + 4 * g4, cout - 4)) * 4, so);
+        } else {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                a[s] = buffer_ld(wr, (wrow + min(cb * 16 + 4 * g4 + s, cout - 1)) * 4, so);
-            dst[cb] = make_float4(a[0], a[1], a[2], a[3]);
+            for (int cb = 0; cb < NCB; ++cb) {
+                float a[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    a[s] = buffer_ld(wr, (wrow + min(cb * 16 + 4 * g4 + s, cout - 1)) * 4, so);
+                dst[cb] = make_float4(a[0], a[1], a[2], a[3]);
+            }
         }
     };
     // One path per iteration of a loop that is not unrolled: each path is a basic
@@ -491,62 +501,74 @@ __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const f
     }
 }
 
-template <int KCO>
+// RT row tiles per workgroup.  RT = 1: up to 8 waves share the 3 * (C_in / 16)
+// (path group, channel tile) units of one 16-row tile.  RT = 2 (C_in / 16 even):
+// 8 waves, 4 per row tile, each wave on one tile; the unit order of the second
+// tile is mirrored so that waves w and w + 4 (one SIMD when waves are placed
+// round-robin) carry the same number of units between them.  At C_in = 32 that
+// is 6 units per tile and 3 per SIMD, where RT = 1 leaves SIMDs with 2, 2, 1, 1.
+template <int KCO, int RT>
 __global__ __launch_bounds__(512) void tp_weighted_bwd_xy_mfma_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ g, float* __restrict__ gx, float* __restrict__ gy, int64_t n,
     int cin, int cout) {
     constexpr int PS = KCO * 16 + 4;
-    __shared__ __attribute__((aligned(16))) float sG[kTile * PS];
+    constexpr int TS = kTile * PS;  // floats of one row tile's g planes
+    __shared__ __attribute__((aligned(16))) float sG[RT * TS];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nwave = blockDim.x >> 6;
     const int g4 = lane >> 4, i16 = lane & 15;
-    const int64_t row0 = (int64_t)blockIdx.x * kTile;
+    const int64_t row0 = (int64_t)blockIdx.x * (kTile * RT);
     const int cout16 = (cout + 15) & ~15;  // MFMA chunks read channels below cout16
-    // stage g[row0 .. row0+15][co][o] (zeros past n and past cout)
-    for (int i = tid; i < kTile * cout16 * 4; i += blockDim.x) {
+    // stage g[row0 .. row0 + 16 RT - 1][co][o] (zeros past n and past cout)
+    for (int i = tid; i < RT * kTile * cout16 * 4; i += blockDim.x) {
         const int rr = i / (cout16 * 4), rem = i - rr * cout16 * 4;
         const int co = rem >> 2, j = rem & 3;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (row0 + rr < n && co < cout)
             v = *reinterpret_cast<const float4*>(g + ((row0 + rr) * cout + co) * 16 + 4 * j);
-        float* d = sG + (co >> 2) * 64 + rr * 4 + (co & 3);
+        float* d = sG + (rr / kTile) * TS + (co >> 2) * 64 + (rr % kTile) * 4 + (co & 3);
         d[(4 * j + 0) * PS] = v.x;
         d[(4 * j + 1) * PS] = v.y;
         d[(4 * j + 2) * PS] = v.z;
         d[(4 * j + 3) * PS] = v.w;
     }
     __syncthreads();
-    const int64_t row_c = min<int64_t>(row0 + i16, n - 1);
-    float yb[16];
-    load16(y, row_c * 16, yb);  // rows >= n only reach discarded outputs
     float gyp[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) gyp[k] = 0.0f;
     const int wpath_bytes = cin * cout * 4;
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
-    const int units = kBwdGroups * ((cin + 15) / 16);
-    for (int u = wv; u < units; u += nwave) {
+    const int units = kBwdGroups * ((cin + 15) / 16);  // per row tile
+    const int wpt = nwave / RT;                         // waves per row tile
+    const int rt = wv / wpt;
+    const int lw = (rt & 1) ? wpt - 1 - (wv - rt * wpt) : wv - rt * wpt;
+    const int64_t rbase = row0 + rt * kTile;
+    const float* sGt = sG + rt * TS;
+    float yb[16];
+    load16(y, min<int64_t>(rbase + i16, n - 1) * 16, yb);  // rows >= n reach discarded outputs
+    for (int u = lw; u < units; u += wpt) {
         const int ct = u / kBwdGroups;
         switch (u % kBwdGroups) {
-            case 0: bwd_xy_unit<0, KCO>(x, yb, wr, gx, n, cin, cout, ct, sG, gyp); break;
-            case 1: bwd_xy_unit<1, KCO>(x, yb, wr, gx, n, cin, cout, ct, sG, gyp); break;
-            default: bwd_xy_unit<2, KCO>(x, yb, wr, gx, n, cin, cout, ct, sG, gyp); break;
+            case 0: bwd_xy_unit<0, KCO>(x, yb, wr, gx, n, cin, cout, ct, sGt, gyp, rbase); break;
+            case 1: bwd_xy_unit<1, KCO>(x, yb, wr, gx, n, cin, cout, ct, sGt, gyp, rbase); break;
+            default: bwd_xy_unit<2, KCO>(x, yb, wr, gx, n, cin, cout, ct, sGt, gyp, rbase); break;
         }
     }
     if (!gy) return;   // uniform over the workgroup
     __syncthreads();   // sG is reused for the reduction
-    float* sRed = sG;  // [wave][g][row][16]
+    float* sRed = sG;  // [wave][g][row][16]; waves of tile t are t * wpt .. t * wpt + wpt - 1
 #pragma unroll
     for (int k = 0; k < 16; ++k) sRed[((wv * 4 + g4) * 16 + i16) * 16 + k] = gyp[k];
     __syncthreads();
-    for (int i = tid; i < kTile * 16; i += blockDim.x) {
-        const int rr = i >> 4, k = i & 15;
+    for (int i = tid; i < RT * kTile * 16; i += blockDim.x) {
+        const int t = i / (kTile * 16), rr = (i >> 4) % kTile, k = i & 15;
         float sum = 0.0f;
-        for (int v = 0; v < nwave; ++v)
+        for (int v = t * wpt; v < t * wpt + wpt; ++v)
 #pragma unroll
             for (int gg = 0; gg < 4; ++gg) sum += sRed[((v * 4 + gg) * 16 + rr) * 16 + k];
-        if (row0 + rr < n) gy[(row0 + rr) * 16 + k] = sum;
+        const int64_t row = row0 + t * kTile + rr;
+        if (row < n) gy[row * 16 + k] = sum;
     }
 }
 
@@ -736,14 +758,23 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
     }
 }
 
-// gW[i] = sum_s part[s, i] in ascending s (deterministic).
+// gW[i] = sum_s part[s, i] in ascending s (deterministic).  Eight segments'
+// loads are issued before their adds, which keep the ascending order.
 __global__ __launch_bounds__(kTpBlock) void reduce_segments_kernel(const float* __restrict__ part,
                                                                    float* __restrict__ out,
                                                                    int64_t count, int nseg) {
     const int64_t i = (int64_t)blockIdx.x * kTpBlock + threadIdx.x;
     if (i >= count) return;
     float s = 0.0f;
-    for (int k = 0; k < nseg; ++k) s += part[(int64_t)k * count + i];
+    int k = 0;
+    for (; k + 8 <= nseg; k += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(k + j) * count + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; k < nseg; ++k) s += part[(int64_t)k * count + i];
     out[i] = s;
 }
 
@@ -752,14 +783,25 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t count) {
     if (i < count) p[i] = 0.0f;
 }
 
-// Row segments of the grad_W reduction: a fixed function of N (not of the
-// device), so results are the same on every GPU.
-constexpr int64_t kGwMaxSegments = 96;
-static int64_t gw_segments(int64_t n) {
-    return std::max<int64_t>(1, std::min<int64_t>(kGwMaxSegments, ceil_div(n, kTile)));
+// Row segments of the grad_W reduction: a fixed function of (N, C_in, C_out),
+// not of the device, so results are the same on every GPU.  The grid
+// (segments x input-channel tiles x output-channel blocks x 3 groups) is sized
+// to about kGwTargetWorkgroups, one full round of the kernel's workgroups on
+// MI355X (256 CUs x 2 resident workgroups), so no second, mostly idle round
+// follows; segments hold whole 16-row chunks and none is empty.
+constexpr int64_t kGwTargetWorkgroups = 512;
+constexpr int64_t kGwMaxSegments = 256;
+static int64_t gw_combos(int cin, int cout) {
+    return ceil_div(cin, 16) * ceil_div(cout, 64) * kBwdGroups;
 }
-static int64_t gw_rows_per_seg(int64_t n) {
-    return ceil_div(ceil_div(n, kTile), gw_segments(n)) * kTile;
+static int64_t gw_rows_per_seg(int64_t n, int cin, int cout) {
+    const int64_t chunks = std::max<int64_t>(1, ceil_div(n, kTile));
+    const int64_t want = std::min<int64_t>(
+        kGwMaxSegments, std::max<int64_t>(1, kGwTargetWorkgroups / gw_combos(cin, cout)));
+    return ceil_div(chunks, std::min(want, chunks)) * kTile;
+}
+static int64_t gw_segments(int64_t n, int cin, int cout) {
+    return ceil_div(std::max<int64_t>(1, ceil_div(n, kTile)) * kTile, gw_rows_per_seg(n, cin, cout));
 }
 
 }  // namespace bmhip
@@ -816,7 +858,8 @@ extern "C" int batteries_tensor_product_l3(const float* input1, const float* inp
 extern "C" size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in,
                                                                     int C_out) {
     if (N <= 0 || C_in <= 0 || C_out <= 0) return 0;
-    return (size_t)gw_segments(N) * kNumPaths * (size_t)C_in * (size_t)C_out * sizeof(float);
+    return (size_t)gw_segments(N, C_in, C_out) * kNumPaths * (size_t)C_in * (size_t)C_out *
+           sizeof(float);
 }
 
 extern "C" int batteries_tensor_product_backward_l3(
@@ -841,16 +884,23 @@ extern "C" int batteries_tensor_product_backward_l3(
     float* gw_part = static_cast<float*>(workspace);
     if (grad_input1 || grad_input2) {
         if (C_out <= 128 && (int64_t)kNumPaths * C_in * C_out * 4 <= INT32_MAX) {
-            // one wave per (path group, 16-channel tile), at most 8 per workgroup
-            const int units = kBwdGroups * (int)ceil_div(C_in, 16);
-            const int nwave = std::min(units, 8);
-            const unsigned grid = (unsigned)ceil_div(N, kTile);
-            if (C_out <= 64)
-                tp_weighted_bwd_xy_mfma_kernel<64><<<grid, 64 * nwave, 0, stream>>>(
+            // one wave per (path group, 16-channel tile), at most 8 per workgroup;
+            // two row tiles on 8 waves when that spreads the units evenly over the SIMDs
+            const int nct = (int)ceil_div(C_in, 16);
+            const int units = kBwdGroups * nct;
+            if (C_out <= 64 && nct % 2 == 0 && N >= 2 * kTile) {
+                tp_weighted_bwd_xy_mfma_kernel<64, 2><<<(unsigned)ceil_div(N, 2 * kTile), 512, 0, stream>>>(
                     input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
-            else
-                tp_weighted_bwd_xy_mfma_kernel<128><<<grid, 64 * nwave, 0, stream>>>(
-                    input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+            } else {
+                const int nwave = std::min(units, 8);
+                const unsigned grid = (unsigned)ceil_div(N, kTile);
+                if (C_out <= 64)
+                    tp_weighted_bwd_xy_mfma_kernel<64, 1><<<grid, 64 * nwave, 0, stream>>>(
+                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+                else
+                    tp_weighted_bwd_xy_mfma_kernel<128, 1><<<grid, 64 * nwave, 0, stream>>>(
+                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+            }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return (int)e;
         } else {
@@ -864,8 +914,8 @@ extern "C" int batteries_tensor_product_backward_l3(
         }
     }
     if (grad_weights) {
-        const int64_t segs = gw_segments(N);
-        const int64_t rps = gw_rows_per_seg(N);
+        const int64_t segs = gw_segments(N, C_in, C_out);
+        const int64_t rps = gw_rows_per_seg(N, C_in, C_out);
         if (ceil_div(C_in, 16) > 65535 || ceil_div(C_out, 64) * kBwdGroups > 65535) return BM_ERR_ARG;
         dim3 grid((unsigned)segs, (unsigned)ceil_div(C_in, 16),
                   (unsigned)(ceil_div(C_out, 64) * kBwdGroups));
