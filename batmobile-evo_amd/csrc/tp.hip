@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_fwd_mfma_kernel(
 // entries of p to its own 4 channels: the group's gx columns, and a grad_y
 // partial in gyp.  The partials are summed over lanes and waves in a fixed order.
 template <int G, int KCO>
-__device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const float* yb,
+__device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, float* yb,
                                             const __amdgpu_buffer_rsrc_t wr, float* __restrict__ gx,
                                             int64_t n, int cin, int cout, int ct, const float* sG,
                                             float* gyp, int64_t row0) {
@@ -429,17 +429,17 @@ __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const f
     // accumulators live at once).
     constexpr int NPG = bwd_group_paths(G);
     constexpr bool PF = KCO <= 64;  // next-path prefetch (registers allow it up to 64 channels)
-    float4 wcur[NCB], wnxt[NCB];
+    // two operand buffers used in turn (path kc reads wbuf[kc & 1] and fills the
+    // other one), so no per-path register copies
+    float4 wbuf[2][NCB];
     constexpr int p0 = bwd_path_at(0, G);
-    load_w(p0, wcur);
+    load_w(p0, wbuf[0]);
 #pragma clang loop unroll(disable)
     for (int k = 0; k < NPG; ++k) {
-        // y through an empty asm each iteration: the products c * y[b] are then
-        // formed per path instead of being hoisted out of the loop (some 200
-        // loop-invariant values that would not fit in registers)
-        float yk[16];
-#pragma unroll
-        for (int b = 0; b < 16; ++b) yk[b] = yb[b];
+        // y through an empty asm each iteration, in place: the products c * y[b]
+        // are then formed per path instead of being hoisted out of the loop (some
+        // 200 loop-invariant values that would not fit in registers)
+        float* yk = yb;
         asm volatile("" : "+v"(yk[0]), "+v"(yk[1]), "+v"(yk[2]), "+v"(yk[3]), "+v"(yk[4]),
                           "+v"(yk[5]), "+v"(yk[6]), "+v"(yk[7]), "+v"(yk[8]), "+v"(yk[9]),
                           "+v"(yk[10]), "+v"(yk[11]), "+v"(yk[12]), "+v"(yk[13]),
@@ -448,28 +448,35 @@ __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const f
             constexpr int kc = decltype(kk)::value;
             if (k == kc) {
                 constexpr int p = bwd_path_at(kc, G);
+                float4* wcur = wbuf[PF ? (kc & 1) : 0];
                 if constexpr (!PF && kc > 0) load_w(p, wcur);
                 if constexpr (PF && kc + 1 < NPG) {
                     constexpr int pn = bwd_path_at(kc + 1, G);
-                    load_w(pn, wnxt);
+                    load_w(pn, wbuf[(kc + 1) & 1]);
                 }
                 constexpr int lo = kPathL[p][2];
                 constexpr int NM = 2 * lo + 1;
                 v4f h[NM];
+                // B operands of output component m (all chunks) are read from LDS
+                // while the MFMAs of component m - 1 run.  Chunks past cout meet
+                // the zero-padded g tile (no per-chunk branches).
+                float4 bq[2][NCB];
+                auto read_b = [&](int m, float4* dst) {
 #pragma unroll
-                for (int m = 0; m < NM; ++m) h[m] = v4f{0.f, 0.f, 0.f, 0.f};
+                    for (int cb = 0; cb < NCB; ++cb)
+                        dst[cb] = *reinterpret_cast<const float4*>(
+                            sG + (lo * lo + m) * PS + (cb * 4 + g4) * 64 + i16 * 4);
+                };
+                read_b(0, bq[0]);
+                static_for<NM>([&](auto mm) {
+                    constexpr int m = decltype(mm)::value;
+                    if constexpr (m + 1 < NM) read_b(m + 1, bq[(m + 1) & 1]);
+                    // chunk 0 starts from a zero accumulator operand (no register zeroing)
+                    h[m] = mfma4(wcur[0], bq[m & 1][0], v4f{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) {
-                    if (cb * 16 < cout) {  // uniform
-                        static_for<NM>([&](auto mm) {
-                            constexpr int m = decltype(mm)::value;
-                            const float4 b4 = *reinterpret_cast<const float4*>(
-                                sG + (lo * lo + m) * PS + (cb * 4 + g4) * 64 + i16 * 4);
-                            h[m] = mfma4(wcur[cb], b4, h[m]);
-                        });
-                    }
-                    __builtin_amdgcn_sched_barrier(0);  // bound the B reads in flight
-                }
+                    for (int cb = 1; cb < NCB; ++cb) h[m] = mfma4(wcur[cb], bq[m & 1][cb], h[m]);
+                    __builtin_amdgcn_sched_barrier(0);  // one component's reads ahead, no more
+                });
                 static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
                     constexpr CGEntry e = kCG[kPathEntry[p] + decltype(ee)::value];
                     constexpr int m = e.o - lo * lo;
@@ -483,10 +490,6 @@ __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const f
                     }
                     gyp[e.b] = fmaf(e.c, sacc, gyp[e.b]);
                 });
-                if constexpr (PF && kc + 1 < NPG) {
-#pragma unroll
-                    for (int cb = 0; cb < NCB; ++cb) wcur[cb] = wnxt[cb];
-                }
             }
         });
     }
@@ -501,37 +504,64 @@ __device__ __forceinline__ void bwd_xy_unit(const float* __restrict__ x, const f
     }
 }
 
-// RT row tiles per workgroup.  RT = 1: up to 8 waves share the 3 * (C_in / 16)
-// (path group, channel tile) units of one 16-row tile.  RT = 2 (C_in / 16 even):
-// 8 waves, 4 per row tile, each wave on one tile; the unit order of the second
-// tile is mirrored so that waves w and w + 4 (one SIMD when waves are placed
-// round-robin) carry the same number of units between them.  At C_in = 32 that
-// is 6 units per tile and 3 per SIMD, where RT = 1 leaves SIMDs with 2, 2, 1, 1.
+// Up to RT row tiles per workgroup.  One tile: up to 8 waves share the
+// 3 * (C_in / 16) (path group, channel tile) units of one 16-row tile.  Two
+// tiles (RT = 2, C_in / 16 even): 8 waves, 4 per row tile, each wave on one
+// tile; the unit order of the second tile is mirrored so that waves w and w + 4
+// (one SIMD when waves are placed round-robin) carry the same number of units
+// between them.  At C_in = 32 that is 6 units per tile and 3 per SIMD, where
+// one tile leaves SIMDs with 2, 2, 1, 1.  Workgroups below npair take two
+// tiles, the rest one (rows from 32 npair on): single-tile workgroups fill the
+// last, partial round of the grid in about 2/3 of the time of a pair.
 template <int KCO, int RT>
 __global__ __launch_bounds__(512) void tp_weighted_bwd_xy_mfma_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ g, float* __restrict__ gx, float* __restrict__ gy, int64_t n,
-    int cin, int cout) {
+    int cin, int cout, int64_t npair) {
     constexpr int PS = KCO * 16 + 4;
     constexpr int TS = kTile * PS;  // floats of one row tile's g planes
     __shared__ __attribute__((aligned(16))) float sG[RT * TS];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nwave = blockDim.x >> 6;
     const int g4 = lane >> 4, i16 = lane & 15;
-    const int64_t row0 = (int64_t)blockIdx.x * (kTile * RT);
-    const int cout16 = (cout + 15) & ~15;  // MFMA chunks read channels below cout16
-    // stage g[row0 .. row0 + 16 RT - 1][co][o] (zeros past n and past cout)
-    for (int i = tid; i < RT * kTile * cout16 * 4; i += blockDim.x) {
-        const int rr = i / (cout16 * 4), rem = i - rr * cout16 * 4;
-        const int co = rem >> 2, j = rem & 3;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row0 + rr < n && co < cout)
-            v = *reinterpret_cast<const float4*>(g + ((row0 + rr) * cout + co) * 16 + 4 * j);
-        float* d = sG + (rr / kTile) * TS + (co >> 2) * 64 + (rr % kTile) * 4 + (co & 3);
-        d[(4 * j + 0) * PS] = v.x;
-        d[(4 * j + 1) * PS] = v.y;
-        d[(4 * j + 2) * PS] = v.z;
-        d[(4 * j + 3) * PS] = v.w;
+    const bool pair = RT == 2 && (int64_t)blockIdx.x < npair;  // uniform
+    const int rtn = pair ? 2 : 1;                               // row tiles of this workgroup
+    const int64_t row0 = pair ? (int64_t)blockIdx.x * (2 * kTile)
+                              : npair * (2 * kTile) + ((int64_t)blockIdx.x - npair) * kTile;
+    const int cout16 = KCO;  // every MFMA chunk of the tile is staged
+    // stage g[row0 .. row0 + 16 rtn - 1][co][o] (zeros past n and past cout).
+    // Eight float4 loads per thread are in flight before their LDS writes: the
+    // loads are unconditional (clamped addresses, masked values), since a
+    // conditional load is a branch with a full wait behind it.
+    {
+        const int total = rtn * kTile * cout16 * 4;
+        constexpr int kStage = 8;
+        for (int i0 = tid; i0 < total; i0 += kStage * (int)blockDim.x) {
+            float4 v[kStage];
+#pragma unroll
+            for (int k = 0; k < kStage; ++k) {
+                const int i = min(i0 + k * (int)blockDim.x, total - 1);
+                const int rr = i / (cout16 * 4), rem = i - rr * cout16 * 4;
+                const int co = rem >> 2, j = rem & 3;
+                const bool ok = row0 + rr < n && co < cout;
+                const float4 t = *reinterpret_cast<const float4*>(
+                    g + (min<int64_t>(row0 + rr, n - 1) * cout + min(co, cout - 1)) * 16 + 4 * j);
+                v[k] = make_float4(mask0(t.x, ok), mask0(t.y, ok), mask0(t.z, ok), mask0(t.w, ok));
+            }
+#pragma unroll
+            for (int k = 0; k < kStage; ++k) {
+                const int i = i0 + k * (int)blockDim.x;
+                if (i < total) {
+                    const int rr = i / (cout16 * 4), rem = i - rr * cout16 * 4;
+                    const int co = rem >> 2, j = rem & 3;
+                    float* d = sG + (rr / kTile) * TS + (co >> 2) * 64 + (rr % kTile) * 4 + (co & 3);
+                    d[(4 * j + 0) * PS] = v[k].x;
+                    d[(4 * j + 1) * PS] = v[k].y;
+                    d[(4 * j + 2) * PS] = v[k].z;
+                    d[(4 * j + 3) * PS] = v[k].w;
+                }
+            }
+        }
     }
     __syncthreads();
     float gyp[16];
@@ -540,7 +570,7 @@ __global__ __launch_bounds__(512) void tp_weighted_bwd_xy_mfma_kernel(
     const int wpath_bytes = cin * cout * 4;
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
     const int units = kBwdGroups * ((cin + 15) / 16);  // per row tile
-    const int wpt = nwave / RT;                         // waves per row tile
+    const int wpt = nwave / rtn;                        // waves per row tile
     const int rt = wv / wpt;
     const int lw = (rt & 1) ? wpt - 1 - (wv - rt * wpt) : wv - rt * wpt;
     const int64_t rbase = row0 + rt * kTile;
@@ -561,7 +591,7 @@ __global__ __launch_bounds__(512) void tp_weighted_bwd_xy_mfma_kernel(
 #pragma unroll
     for (int k = 0; k < 16; ++k) sRed[((wv * 4 + g4) * 16 + i16) * 16 + k] = gyp[k];
     __syncthreads();
-    for (int i = tid; i < RT * kTile * 16; i += blockDim.x) {
+    for (int i = tid; i < rtn * kTile * 16; i += blockDim.x) {
         const int t = i / (kTile * 16), rr = (i >> 4) % kTile, k = i & 15;
         float sum = 0.0f;
         for (int v = t * wpt; v < t * wpt + wpt; ++v)
@@ -639,24 +669,25 @@ __device__ __forceinline__ void bwd_w_group(const float* __restrict__ x, const f
             for (int q = 0; q < NS; ++q) sT[q * 256 + tid] = t[q];
         }
         __syncthreads();
-        if (live) {
-            static_for<kNumPaths>([&](auto pp) {
-                constexpr int p = decltype(pp)::value;
-                if constexpr (bwd_path_in_group(p, G)) {
-                    constexpr int lo = kPathL[p][2];
-                    constexpr int pl = bwd_path_local(p, G);
-                    static_for<2 * lo + 1>([&](auto mm) {
-                        constexpr int m = decltype(mm)::value;
-                        constexpr int sl = bwd_slot_local(kPathSlot[p] + m, G);
-                        const float4 a4 =
-                            *reinterpret_cast<const float4*>(sT + sl * 256 + g4 * 64 + i16 * 4);
-                        const float4 b4 = make_float4(gv[0][lo * lo + m], gv[1][lo * lo + m],
-                                                      gv[2][lo * lo + m], gv[3][lo * lo + m]);
-                        acc[pl] = mfma4(a4, b4, acc[pl]);
-                    });
-                }
-            });
-        }
+        // Unconditional, also in waves whose channels are all past cout (their
+        // results are not stored): under a branch, the compiler sinks the g loads
+        // above into it, right in front of their first use.
+        static_for<kNumPaths>([&](auto pp) {
+            constexpr int p = decltype(pp)::value;
+            if constexpr (bwd_path_in_group(p, G)) {
+                constexpr int lo = kPathL[p][2];
+                constexpr int pl = bwd_path_local(p, G);
+                static_for<2 * lo + 1>([&](auto mm) {
+                    constexpr int m = decltype(mm)::value;
+                    constexpr int sl = bwd_slot_local(kPathSlot[p] + m, G);
+                    const float4 a4 =
+                        *reinterpret_cast<const float4*>(sT + sl * 256 + g4 * 64 + i16 * 4);
+                    const float4 b4 = make_float4(gv[0][lo * lo + m], gv[1][lo * lo + m],
+                                                  gv[2][lo * lo + m], gv[3][lo * lo + m]);
+                    acc[pl] = mfma4(a4, b4, acc[pl]);
+                });
+            }
+        });
     }
     // D[4 g4 + r][i16]: input channel ci0 + 4 g4 + r, output channel co0 + i16
     if (live) {
@@ -783,6 +814,20 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t count) {
     if (i < count) p[i] = 0.0f;
 }
 
+// Two-tile workgroups of the grad_x / grad_y kernel (one per CU at a time):
+// whole rounds of them (kBwdXyRound, MI355X's 256 CUs), and single-tile
+// workgroups for the rest of the tiles when those fill at most half a round of
+// pairs (each takes about 2/3 of a pair's time, so one round of singles ends
+// before half a round of pairs would); otherwise pairs throughout.  A function
+// of the tile count only, so results do not depend on the device.
+constexpr int64_t kBwdXyRound = 256;
+static int64_t bwd_xy_pairs(int64_t tiles) {
+    const int64_t full = tiles / (2 * kBwdXyRound) * kBwdXyRound;
+    const int64_t rest = tiles - 2 * full;  // tiles past the whole rounds of pairs
+    if (rest <= kBwdXyRound) return full;   // one round of single-tile workgroups
+    return ceil_div(tiles, 2);
+}
+
 // Row segments of the grad_W reduction: a fixed function of (N, C_in, C_out),
 // not of the device, so results are the same on every GPU.  The grid
 // (segments x input-channel tiles x output-channel blocks x 3 groups) is sized
@@ -888,18 +933,25 @@ extern "C" int batteries_tensor_product_backward_l3(
             // two row tiles on 8 waves when that spreads the units evenly over the SIMDs
             const int nct = (int)ceil_div(C_in, 16);
             const int units = kBwdGroups * nct;
-            if (C_out <= 64 && nct % 2 == 0 && N >= 2 * kTile) {
-                tp_weighted_bwd_xy_mfma_kernel<64, 2><<<(unsigned)ceil_div(N, 2 * kTile), 512, 0, stream>>>(
-                    input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+            const int64_t tiles = ceil_div(N, kTile);
+            if (C_out <= 64 && nct % 2 == 0 && tiles >= 2) {
+                const int64_t npair = bwd_xy_pairs(tiles);
+                const int64_t nsingle = tiles - 2 * npair;  // may be -1: a last half-empty pair
+                tp_weighted_bwd_xy_mfma_kernel<64, 2>
+                    <<<(unsigned)(npair + std::max<int64_t>(nsingle, 0)), 512, 0, stream>>>(
+                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in,
+                        C_out, npair);
             } else {
                 const int nwave = std::min(units, 8);
-                const unsigned grid = (unsigned)ceil_div(N, kTile);
+                const unsigned grid = (unsigned)tiles;
                 if (C_out <= 64)
                     tp_weighted_bwd_xy_mfma_kernel<64, 1><<<grid, 64 * nwave, 0, stream>>>(
-                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in,
+                        C_out, 0);
                 else
                     tp_weighted_bwd_xy_mfma_kernel<128, 1><<<grid, 64 * nwave, 0, stream>>>(
-                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in,
+                        C_out, 0);
             }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return (int)e;

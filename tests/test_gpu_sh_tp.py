@@ -137,8 +137,9 @@ def _tp_backward_oracle_chunked(x, y, w, g, chunk=2000):
     (40, 20, 100),     # C_out in (64, 128]: the 128-channel grad_output tile
     (20, 8, 160),      # C_out > 128: the per-(row, channel) grad_x / grad_y kernel
     (33, 80, 24),      # 15 (group, channel-tile) units on 8 waves: waves loop over units
-    (45, 32, 48),      # two row tiles per workgroup, the second one partly past N
-    (35, 64, 20),      # two row tiles per workgroup, the second one wholly past N
+    (45, 32, 48),      # single-tile workgroups of the two-tile kernel, the last tile partly past N
+    (35, 64, 20),      # the same with C_in = 64 and C_out not a multiple of 16
+    (12810, 32, 16),   # 801 tiles: two-tile workgroups throughout, the last pair half past N
 ])
 def test_tp_weighted_backward(bm, dev, n, cin, cout):
     # (20000, 32, 64) is configs[2]: upstream grad ~ N(0,1)
