@@ -220,28 +220,35 @@ __device__ __forceinline__ void load16_mask(const float* __restrict__ p, int64_t
 }
 
 // ---- forward ---------------------------------------------------------------
-// Workgroup: 16 rows x 64 output channels x one output group G; wave w owns
-// output channels co0 .. co0+15.  Per chunk of 16 input channels: thread
-// (row, ci) builds the group's T values into LDS, then each wave runs
+// Workgroup: 16 rows x 64 output channels x one output group G, in H halves of
+// 4 waves (H = 2 when C_in > 16): wave w of a half owns output channels
+// co0 .. co0+15, and half h takes the 16-channel input chunks h, h + H, ...
+// into its own LDS buffer.  Per chunk: thread (row, ci) builds the group's T
+// values into LDS, then each wave runs
 //   D[co][row] += W[p][ci][co] (A, global/L2) x T[row][ci][q] (B, LDS)
-// for every slot q of the group, one accumulator per output component.
+// for every slot q of the group, one accumulator per output component.  The
+// halves' accumulators are added in LDS in a fixed order.  Two halves put two
+// waves on each SIMD: one hides the other's load latency, and the pair issues
+// VALU work at about twice the rate of a lone wave.
 // LDS layout sT[slot][g][row][s] with ci = 4g + s: the B read of lane
 // (row = lane % 16, g) is one float4, and a wave's T writes are contiguous.
 template <int G>
 __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const float* __restrict__ w,
                                           float* __restrict__ out, int64_t n, int cin, int cout,
-                                          float* sT, const float* sY) {
+                                          float* sTall, const float* __restrict__ y) {
     constexpr int NS = fwd_group_size(G);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x & 255, lane = tid & 63, wv = tid >> 6;
+    const int half = threadIdx.x >> 8, nhalf = blockDim.x >> 8;
+    float* sT = sTall + half * (kFwdMaxSlots * 256);
     const int g4 = lane >> 4, i16 = lane & 15;
     const int64_t row0 = (int64_t)blockIdx.x * kTile;
     const int co0 = (blockIdx.y * 4 + wv) * 16;
     const bool live = co0 < cout;
     const int trow = tid & 15, tcl = tid >> 4;
-    const bool trow_ok = row0 + trow < n;
+    // y of the T thread's row, straight from global memory (issued with the
+    // first chunk's x and W loads; rows past n only reach discarded outputs)
     float yb[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) yb[k] = sY[trow * 16 + k];
+    load16(y, min<int64_t>(row0 + trow, n - 1) * 16, yb);
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -250,7 +257,10 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
     const int co = co0 + i16;
     const int wpath_bytes = cin * cout * 4;
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
-    for (int c0 = 0; c0 < cin; c0 += 16) {
+    // every half runs the same number of chunks (a chunk past cin builds T = 0)
+    const int nchunk = (cin + 16 * nhalf - 1) / (16 * nhalf);
+    for (int ch = 0; ch < nchunk; ++ch) {
+        const int c0 = (ch * nhalf + half) * 16;
         // A operands W[p][c0 + 4 g4 + s][co] of the group's paths through a
         // register ring of kWRing paths: the first ones are issued before the T
         // computation (their latency hides behind it), and each path's MFMAs
@@ -327,6 +337,22 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
             });
         }
     }
+    if (nhalf == 2) {  // uniform: half 1 hands its sums to half 0
+        __syncthreads();  // the last chunk's B reads are done
+        float* sAcc = sTall;  // [wave][j][r][lane]
+        if (half == 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sAcc[((wv * 4 + j) * 4 + r) * 64 + lane] = acc[j][r];
+        }
+        __syncthreads();
+        if (half == 1) return;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[j][r] += sAcc[((wv * 4 + j) * 4 + r) * 64 + lane];
+    }
     // D[4 g4 + r][i16]: output channel co0 + 4 g4 + r of row row0 + i16
     const int64_t row = row0 + i16;
     if (live && row < n) {
@@ -340,22 +366,15 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
     }
 }
 
-__global__ __launch_bounds__(kTpBlock) void tp_weighted_fwd_mfma_kernel(
+__global__ __launch_bounds__(2 * kTpBlock) void tp_weighted_fwd_mfma_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     float* __restrict__ out, int64_t n, int cin, int cout) {
-    __shared__ __attribute__((aligned(16))) float sT[kFwdMaxSlots * 256];
-    __shared__ float sY[kTile * 16];
-    const int64_t row0 = (int64_t)blockIdx.x * kTile;
-    {
-        const int r = threadIdx.x >> 4, k = threadIdx.x & 15;
-        sY[threadIdx.x] = row0 + r < n ? y[(row0 + r) * 16 + k] : 0.0f;
-    }
-    __syncthreads();
+    __shared__ __attribute__((aligned(16))) float sT[2 * kFwdMaxSlots * 256];
     switch (blockIdx.z) {
-        case 0: fwd_group<0>(x, w, out, n, cin, cout, sT, sY); break;
-        case 1: fwd_group<1>(x, w, out, n, cin, cout, sT, sY); break;
-        case 2: fwd_group<2>(x, w, out, n, cin, cout, sT, sY); break;
-        default: fwd_group<3>(x, w, out, n, cin, cout, sT, sY); break;
+        case 0: fwd_group<0>(x, w, out, n, cin, cout, sT, y); break;
+        case 1: fwd_group<1>(x, w, out, n, cin, cout, sT, y); break;
+        case 2: fwd_group<2>(x, w, out, n, cin, cout, sT, y); break;
+        default: fwd_group<3>(x, w, out, n, cin, cout, sT, y); break;
     }
 }
 
@@ -891,13 +910,12 @@ extern "C" int batteries_tensor_product_l3(const float* input1, const float* inp
     if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(output)) & 15)
         return BM_ERR_ARG;
     dim3 grid((unsigned)ceil_div(N, kTile), (unsigned)ceil_div(C_out, 64), kFwdGroups);
-    tp_weighted_fwd_mfma_kernel<<<grid, kTpBlock, 0, stream>>>(input1, input2, weights, output, N,
-                                                               C_in, C_out);
+    const int halves = C_in > 16 ? 2 : 1;  // input-channel chunks split over two wave halves
+    tp_weighted_fwd_mfma_kernel<<<grid, halves * kTpBlock, 0, stream>>>(
+        input1, input2, weights, output, N, C_in, C_out);
     return (int)hipGetLastError();
 }
 
-// Workspace of the weighted backward: grad_y partials of the three path groups
-// [3][N][16], then grad_W partials of the row segments [S][34][C_in][C_out].
 // Workspace of the weighted backward: grad_W partials of the row segments
 // [S][34][C_in][C_out] (grad_input1 / grad_input2 alone need none).
 extern "C" size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, int C_in,
