@@ -30,7 +30,20 @@ namespace bmhip {
 
 constexpr int kNBasis = 8;
 constexpr int kHidden = 64;
-constexpr int64_t kMaceChunk = 65536;  // edges per chunk (R and its gradient live per chunk)
+// Edges per chunk (R and its gradient live per chunk): up to kMaceChunkMax, and
+// all chunks of a graph equally long (multiples of 256, the last one shorter by
+// less than 256 per chunk), so the GEMMs run every chunk at one height.  Larger
+// chunks run faster on MI355X (configs[4], forward / backward: 8192 edges
+// 36.3 / 88.7 ms, 65536 19.3 / 34.5 ms, 131072 16.6 / 32.0 ms, 262144 16.2 /
+// 31.3 ms); R is 17 KB per edge at C = 128, 4.6 GB for a chunk of 262144.
+constexpr int64_t kMaceChunkMax = 262144;
+static int64_t mace_chunk(int64_t E, int C) {
+    // R offsets within a chunk stay below 2^31 (32-bit GEMM and kernel offsets)
+    const int64_t cap = std::min<int64_t>(kMaceChunkMax, INT32_MAX / ((int64_t)C * 34) / 256 * 256);
+    const int64_t e = std::max<int64_t>(E, 1);
+    const int64_t n = (e + cap - 1) / cap;
+    return ((e + n - 1) / n + 255) / 256 * 256;
+}
 
 #pragma clang fp contract(off)
 // v = pos[dst] - pos[src] with the minimum image of an orthorhombic box, in the
@@ -246,15 +259,17 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 // LDS each broadcast read still moves 1 KB per wave, from memory the scalar
 // loads stall.)
 // ---------------------------------------------------------------------------
-constexpr int kMaceRowBlocks = kMaceChunk / 4;           // grid of the product kernels
+// grid of the product kernels: at most chunk / 4 destination rows hold edges of
+// a chunk when every row has 4 or more (grid-stride loop over the rows beyond)
+static unsigned mace_row_blocks(int64_t chunk) { return (unsigned)(chunk / 4); }
 
 // rows[2i], rows[2i+1]: first and one-past-last destination with an edge in
-// chunk i = [i * kMaceChunk, min(E, (i + 1) * kMaceChunk)).
+// chunk i = [i * chunk, min(E, (i + 1) * chunk)).
 __global__ void mace_chunk_rows_kernel(const int64_t* __restrict__ row_ptr, int64_t N, int64_t E,
-                                       int n_chunks, int64_t* __restrict__ rows) {
+                                       int64_t chunk, int n_chunks, int64_t* __restrict__ rows) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_chunks) return;
-    const int64_t e0 = (int64_t)i * kMaceChunk, e1 = min(E, e0 + kMaceChunk);
+    const int64_t e0 = (int64_t)i * chunk, e1 = min(E, e0 + chunk);
     auto row_of = [&](int64_t k) {  // the row holding edge k: largest d with row_ptr[d] <= k
         int64_t lo = 0, hi = N - 1;
         while (lo < hi) {
@@ -590,7 +605,8 @@ struct MaceWs {
 static size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
 static MaceWs mace_ws(void* base, int64_t E, int C, bool backward) {
-    const int64_t eb = std::min<int64_t>(std::max<int64_t>(E, 1), kMaceChunk);
+    const int64_t chunk = mace_chunk(E, C);
+    const int64_t eb = std::min<int64_t>(std::max<int64_t>(E, 1), chunk);
     char* p = static_cast<char*>(base);
     size_t o = 0;
     MaceWs w{};
@@ -600,7 +616,8 @@ static MaceWs mace_ws(void* base, int64_t E, int C, bool backward) {
         return r;
     };
     w.vec = take(sizeof(float) * 3 * (size_t)E);
-    w.rows = reinterpret_cast<int64_t*>(take(sizeof(int64_t) * 2 * (size_t)ceil_div(std::max<int64_t>(E, 1), kMaceChunk)));
+    w.rows = reinterpret_cast<int64_t*>(
+        take(sizeof(int64_t) * 2 * (size_t)ceil_div(std::max<int64_t>(E, 1), chunk)));
     w.h = take(sizeof(float) * (size_t)eb * kHidden);
     w.R = take(sizeof(float) * (size_t)eb * C * kNumPaths);
     if (backward) {
@@ -663,12 +680,12 @@ static int blas_gemm(const float* A, const float* B, float* Cm, int64_t M, int N
 }
 
 // Rows of a chunk's GEMMs: a graph of more than one chunk runs every chunk's
-// GEMMs at the full chunk height (the workspace holds kMaceChunk rows; rows
+// GEMMs at the full chunk height (the workspace holds a chunk's rows; rows
 // past the chunk's last edge hold the previous chunk's finite values and their
 // results are never read), so that rocBLAS picks the same kernel for the last,
 // shorter chunk (65536 x 64 x 4352 at 323 us; 57844 rows picked a 992 us one).
-static int64_t gemm_rows(int64_t n_edges, int64_t eb) {
-    return n_edges > kMaceChunk ? (int64_t)kMaceChunk : eb;
+static int64_t gemm_rows(int64_t n_edges, int64_t eb, int64_t chunk) {
+    return n_edges > chunk ? chunk : eb;
 }
 
 }  // namespace bmhip
@@ -701,7 +718,7 @@ static bool mace_args_ok(const float* box, int64_t N, int64_t E, int C, float cu
     if (!box || N < 0 || E < 0 || C <= 0 || C > 256 || !(cutoff > 0.0f)) return false;
     for (int k = 0; k < 3; ++k)
         if (!(box[k] > 0.0f)) return false;
-    return (int64_t)kMaceChunk * C * kNumPaths < INT32_MAX;
+    return true;  // chunk offsets are kept within 32 bits by mace_chunk
 }
 
 static MaceBox mace_box(const float* box) {
@@ -730,19 +747,20 @@ extern "C" int batteries_mace_forward(const float* positions, const float* box,
     mace_edge_vectors_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
         positions, bx, src, dst, w.vec, N_edges);
     const int nthr = C >= 256 ? 256 : (int)ceil_div(C, 64) * 64;
-    const int n_chunks = (int)ceil_div(N_edges, kMaceChunk);
-    mace_chunk_rows_kernel<<<(unsigned)ceil_div(n_chunks, 64), 64, 0, stream>>>(row_ptr, N, N_edges,
-                                                                               n_chunks, w.rows);
-    for (int64_t e0 = 0; e0 < N_edges; e0 += kMaceChunk) {
-        const int64_t e1 = std::min(N_edges, e0 + kMaceChunk), eb = e1 - e0;
+    const int64_t chunk = mace_chunk(N_edges, C);
+    const int n_chunks = (int)ceil_div(N_edges, chunk);
+    mace_chunk_rows_kernel<<<(unsigned)ceil_div(n_chunks, 64), 64, 0, stream>>>(
+        row_ptr, N, N_edges, chunk, n_chunks, w.rows);
+    for (int64_t e0 = 0; e0 < N_edges; e0 += chunk) {
+        const int64_t e1 = std::min(N_edges, e0 + chunk), eb = e1 - e0;
         mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
                                                                              e1, cutoff);
-        int rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb), C * kNumPaths, kHidden, false,
+        int rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
                            stream);
         if (rc != BM_OK) return rc;
-        dim3 grid((unsigned)kMaceRowBlocks, (unsigned)ceil_div(C, nthr));
+        dim3 grid(mace_row_blocks(chunk), (unsigned)ceil_div(C, nthr));
         mace_tp_scatter_kernel<<<grid, nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, w.R,
-                                                          w.rows + 2 * (e0 / kMaceChunk), e0, e1,
+                                                          w.rows + 2 * (e0 / chunk), e0, e1,
                                                           out, C);
     }
     return (int)hipGetLastError();
@@ -768,20 +786,21 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
     mace_edge_vectors_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
         positions, bx, src, dst, w.vec, N_edges);
     const int nthr = (int)ceil_div(C, 64) * 64;
-    const int n_chunks = (int)ceil_div(N_edges, kMaceChunk);
-    mace_chunk_rows_kernel<<<(unsigned)ceil_div(n_chunks, 64), 64, 0, stream>>>(row_ptr, N, N_edges,
-                                                                               n_chunks, w.rows);
-    for (int64_t e0 = 0; e0 < N_edges; e0 += kMaceChunk) {
-        const int64_t e1 = std::min(N_edges, e0 + kMaceChunk), eb = e1 - e0;
+    const int64_t chunk = mace_chunk(N_edges, C);
+    const int n_chunks = (int)ceil_div(N_edges, chunk);
+    mace_chunk_rows_kernel<<<(unsigned)ceil_div(n_chunks, 64), 64, 0, stream>>>(
+        row_ptr, N, N_edges, chunk, n_chunks, w.rows);
+    for (int64_t e0 = 0; e0 < N_edges; e0 += chunk) {
+        const int64_t e1 = std::min(N_edges, e0 + chunk), eb = e1 - e0;
         mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
                                                                              e1, cutoff);
-        int rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb), C * kNumPaths, kHidden, false,
+        int rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
                            stream);
         if (rc != BM_OK) return rc;
-        mace_tp_backward_kernel<<<(unsigned)kMaceRowBlocks, nthr, 0, stream>>>(
-            w.vec, node_features, src, row_ptr, w.R, grad_out, w.rows + 2 * (e0 / kMaceChunk), e0,
+        mace_tp_backward_kernel<<<mace_row_blocks(chunk), nthr, 0, stream>>>(
+            w.vec, node_features, src, row_ptr, w.R, grad_out, w.rows + 2 * (e0 / chunk), e0,
             e1, w.gR, w.gY, C);
-        rc = blas_gemm(w.gR, w2, w.gh, gemm_rows(N_edges, eb), kHidden, C * kNumPaths, true, stream);
+        rc = blas_gemm(w.gR, w2, w.gh, gemm_rows(N_edges, eb, chunk), kHidden, C * kNumPaths, true, stream);
         if (rc != BM_OK) return rc;
         mace_radial_backward_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(
             w.vec, w1, b1, w.gh, w.gY, e0, e1, cutoff, w.gv);

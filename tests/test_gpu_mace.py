@@ -53,9 +53,9 @@ def test_mace_layer_forward_and_forces(bm, dev, n, c):
 
 
 def test_mace_layer_two_edge_chunks(bm, dev):
-    """~75k edges: two chunks of 65536 (rows split across chunks add up)."""
-    pos, cell, graph, layer, x, go = _layer_inputs(dev, 2500, 2, 21)
-    assert graph.num_edges > 65536
+    """~285k edges: two chunks (at most 262144 edges each; rows split across chunks add up)."""
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, 9500, 2, 21)
+    assert graph.num_edges > 262144
     p = pos.to(dev).requires_grad_(True)
     out = layer(graph, p, x.to(dev))
     out.backward(go.to(dev))
