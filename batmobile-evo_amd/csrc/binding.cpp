@@ -443,6 +443,66 @@ torch::Tensor sh_tp_scatter(const torch::Tensor& edge_vectors, const torch::Tens
     return out;
 }
 
+// Extension: the weighted scatter, out[d] = sum_{k in CSR row d}
+// tensor_product(X[source_idx[e_k]], Y(v_{e_k}), weights) with e_k = perm[k] if perm
+// is given else k -- the reference's interaction block SH -> tensor_product ->
+// scatter_add (benchmarks/benchmark_e2e_mace.py:308-349) without the per-edge
+// messages.  order (optional) lists the destinations in the order they are
+// processed (any permutation of 0..N_dst-1; a spatial order keeps source rows in L2).
+torch::Tensor sh_tp_scatter_weighted(const torch::Tensor& edge_vectors,
+                                     const torch::Tensor& node_features,
+                                     const torch::Tensor& weights, const torch::Tensor& source_idx,
+                                     const torch::Tensor& row_ptr,
+                                     const c10::optional<torch::Tensor>& perm,
+                                     const c10::optional<torch::Tensor>& order, bool normalize) {
+    check_vectors(edge_vectors);
+    check_features(node_features, "node_features");
+    TORCH_CHECK(weights.dim() == 3, "weights must be 3D [num_paths, C_in, C_out]");
+    TORCH_CHECK(weights.dtype() == torch::kFloat32, "weights must be float32");
+    check_device(weights, "weights");
+    const int num_paths = batteries_get_num_paths_l3();
+    TORCH_CHECK(weights.size(0) == num_paths, "weights must have ", num_paths, " paths");
+    const int64_t C_in = node_features.size(1);
+    TORCH_CHECK(weights.size(1) == C_in, "weights second dim must match C_in");
+    const int64_t C_out = weights.size(2);
+    TORCH_CHECK(C_out > 0, "C_out must be positive");
+    TORCH_CHECK(source_idx.dim() == 1 && source_idx.dtype() == torch::kInt64,
+                "source_idx must be int64 [N_edges]");
+    TORCH_CHECK(row_ptr.dim() == 1 && row_ptr.dtype() == torch::kInt64 && row_ptr.numel() >= 1,
+                "row_ptr must be int64 [N_dst + 1]");
+    const int64_t E = edge_vectors.size(0);
+    const int64_t N_dst = row_ptr.numel() - 1;
+    TORCH_CHECK(source_idx.numel() == E, "source_idx must have N_edges elements");
+    const int64_t* pp = nullptr;
+    if (perm.has_value() && perm->defined()) {
+        TORCH_CHECK(perm->dtype() == torch::kInt64 && perm->numel() == E,
+                    "perm must be int64 [N_edges]");
+        pp = cptr<int64_t>(*perm, "perm");
+    }
+    const int64_t* op = nullptr;
+    if (order.has_value() && order->defined()) {
+        TORCH_CHECK(order->dtype() == torch::kInt64 && order->numel() == N_dst,
+                    "order must be int64 [N_dst]");
+        op = cptr<int64_t>(*order, "order");
+    }
+    torch::Tensor out = torch::empty({N_dst, C_out, 16}, f32_like(node_features));
+    if (N_dst == 0) return out;
+    TORCH_CHECK(E == 0 || node_features.size(0) > 0, "edges need source nodes");
+    const c10::DeviceGuard guard(node_features.device());
+    torch::Tensor x = aligned16(node_features);
+    torch::Tensor w = weights.contiguous();
+    const size_t wsb = batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, E, (int)C_in);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 15) / 16), 4}, f32_like(node_features));
+    check_status(batteries_sh_tp_scatter_weighted(
+                     cptr<float>(edge_vectors, "edge_vectors"), cptr<float>(x, "node_features"),
+                     cptr<float>(w, "weights"), cptr<int64_t>(source_idx, "source_idx"), pp,
+                     cptr<int64_t>(row_ptr, "row_ptr"), op, mptr<float>(out, "output"),
+                     node_features.size(0), N_dst, E, (int)C_in, (int)C_out, normalize ? 1 : 0,
+                     ws.data_ptr(), wsb, current_stream(node_features)),
+                 "sh_tp_scatter_weighted");
+    return out;
+}
+
 // Extension: atoms in Morton order of a 32^3 grid over the (orthorhombic) box.
 torch::Tensor spatial_order(const torch::Tensor& positions, const torch::Tensor& cell) {
     TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
@@ -770,6 +830,10 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("source_idx"), py::arg("row_ptr"), py::arg("perm") = py::none(),
           py::arg("normalize") = false,
           "Fused SH + simple TP + scatter-add over CSR rows (no messages tensor, no atomics)");
+    m.def("sh_tp_scatter_weighted", &sh_tp_scatter_weighted, py::arg("edge_vectors"),
+          py::arg("node_features"), py::arg("weights"), py::arg("source_idx"), py::arg("row_ptr"),
+          py::arg("perm") = py::none(), py::arg("order") = py::none(), py::arg("normalize") = true,
+          "Fused SH + weighted TP (W [34, C_in, C_out]) + scatter-add over CSR rows");
     m.def("neighbor_list", &neighbor_list, py::arg("positions"), py::arg("cell"),
           py::arg("cutoff"), py::arg("self_loops") = false,
           "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], row_offsets)");

@@ -200,6 +200,38 @@ __device__ __forceinline__ void tp_per_path_backward(const float* x, const float
 }
 
 // ---------------------------------------------------------------------------
+// Output groups of the weighted product: slot q (path, m_out) belongs to group
+// kSlotOut[q] / 4, i.e. output components o in [4G, 4G + 4).  Per-path sums
+// stored for the mixing stage ([row][slot][channel]) list the slots group by
+// group, in slot order within a group (fwd_slot_pos).
+// ---------------------------------------------------------------------------
+constexpr int kFwdGroups = 4;
+constexpr bool fwd_in_group(int q, int G) { return kSlotOut[q] / 4 == G; }
+constexpr int fwd_group_size(int G) {
+    int c = 0;
+    for (int q = 0; q < kNumSlots; ++q) c += fwd_in_group(q, G) ? 1 : 0;
+    return c;
+}
+constexpr int fwd_local(int q, int G) {
+    int c = 0;
+    for (int i = 0; i < q; ++i) c += fwd_in_group(i, G) ? 1 : 0;
+    return c;
+}
+constexpr int fwd_group_base(int G) {
+    int c = 0;
+    for (int i = 0; i < G; ++i) c += fwd_group_size(i);
+    return c;
+}
+constexpr int fwd_slot_pos(int q) {
+    return fwd_group_base(kSlotOut[q] / 4) + fwd_local(q, kSlotOut[q] / 4);
+}
+
+// Mixing stage of the weighted scatter (tp.hip): out[n, co, o] =
+// sum_{q -> o} sum_ci W[p(q), ci, co] T[n][fwd_slot_pos(q)][ci] on `stream`.
+int tp_weighted_mix_launch(const float* tsum, const float* w, float* out, int64_t n, int cin,
+                           int cout, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
 // small helpers
 // ---------------------------------------------------------------------------
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -1079,3 +1079,264 @@ extern "C" int batteries_sh_tp_scatter_scheduled(const float* edge_vectors,
                      source_idx, edge_perm, row_ptr_s, row_dst, node_output, n_sched, N_edges, C,
                      rows_per_block, n_blocks, stream);
 }
+
+// ---------------------------------------------------------------------------
+// Weighted scatter: one W [34, C_in, C_out] shared by every edge,
+//   out[d, co, o] = sum_{e -> d} TP_W(X[src_e], Y(v_e))[co, o].
+// Because W is shared, the sum over the edges of d moves in front of both the
+// CG contraction and the channel mixing:
+//   S[d, ci, a, b] = sum_{e -> d} X[src_e, ci, a] Y_e[b]              MFMA over edges
+//   T[d, q, ci]    = sum_{(a, b) in slot q} c S[d, ci, a, b]           CG table, VALU
+//   out[d, co, o]  = sum_{q -> o} sum_ci W[p(q), ci, co] T[d, q, ci]   MFMA (tp.hip)
+// Work: 2 * 256 * C_in flops per edge (S), 2 * 611 * C_in + 2 * 156 * C_in * C_out per
+// destination (T, mixing).  T is [N_dst][156][Cp] (slots in fwd_slot_pos order,
+// channels padded to Cp = 16 * ceil(C_in / 16) and zero past C_in).
+// ---------------------------------------------------------------------------
+namespace bmhip {
+
+// Y and the source row of CSR slot k (edge perm[k] when perm is given), so that
+// the path-sum kernel reads both without indirection.
+__global__ __launch_bounds__(256) void mp_edge_prep_kernel(
+    const float* __restrict__ vec, const int64_t* __restrict__ src_idx,
+    const int64_t* __restrict__ perm, int64_t n_edges, int normalize, float* __restrict__ yc,
+    int* __restrict__ srcc) {
+    const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (k >= n_edges) return;
+    const int64_t e = perm ? perm[k] : k;
+    float x = vec[e * 3 + 0], y = vec[e * 3 + 1], z = vec[e * 3 + 2];
+    if (normalize) normalize3(x, y, z);
+    float Y[16];
+    sh_forward<3>(x, y, z, Y);
+    float4* o = reinterpret_cast<float4*>(yc + k * 16);
+    o[0] = make_float4(Y[0], Y[1], Y[2], Y[3]);
+    o[1] = make_float4(Y[4], Y[5], Y[6], Y[7]);
+    o[2] = make_float4(Y[8], Y[9], Y[10], Y[11]);
+    o[3] = make_float4(Y[12], Y[13], Y[14], Y[15]);
+    srcc[k] = (int)src_idx[e];
+}
+
+// S of one (destination, channel) in LDS: 16 rows b of 16 a, the four 16-byte
+// quads of row b at positions quad ^ ps_swz(b), rows of successive channels
+// kPsStride floats apart.  The MFMA-layout writes (8 lanes = 8 values of b) and
+// the contraction's reads (8 lanes = 8 channels) are then free of bank conflicts.
+constexpr int kPsStride = 260;
+__host__ __device__ constexpr int ps_swz(int b) { return (b >> 1) & 3; }
+
+// CG blocks (l1, l2) contracted by each wave: 166, 149, 149, 147 CG terms.
+constexpr int kPsBlocks[4][5][2] = {{{1, 0}, {3, 1}, {3, 3}, {-1, -1}, {-1, -1}},
+                                    {{0, 2}, {1, 3}, {2, 3}, {3, 0}, {-1, -1}},
+                                    {{0, 0}, {0, 1}, {0, 3}, {1, 2}, {3, 2}},
+                                    {{1, 1}, {2, 0}, {2, 1}, {2, 2}, {-1, -1}}};
+
+// The slots of the paths (L1, L2, *) for this lane's (destination, channel):
+// reads S[a in l1][b in l2], contracts with the CG terms, stores T[row][pos(q)][ch].
+template <int L1, int L2>
+__device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__ T, int64_t tbase,
+                                         int cp, bool store, bool chan_ok) {
+    constexpr int a0 = L1 * L1, na = 2 * L1 + 1, b0 = L2 * L2, nb = 2 * L2 + 1;
+    constexpr int qa0 = a0 / 4, qa1 = (a0 + na - 1) / 4;
+    float s[nb][na];
+    static_for<nb>([&](auto bb) {
+        constexpr int b = b0 + decltype(bb)::value;
+        static_for<qa1 - qa0 + 1>([&](auto qq) {
+            constexpr int qa = qa0 + decltype(qq)::value;
+            const float4 v =
+                *reinterpret_cast<const float4*>(sSrow + b * 16 + (qa ^ ps_swz(b)) * 4);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            static_for<4>([&](auto ii) {
+                constexpr int i = decltype(ii)::value;
+                constexpr int a = 4 * qa + i;
+                if constexpr (a >= a0 && a < a0 + na) s[b - b0][a - a0] = vv[i];
+            });
+        });
+    });
+    static_for<kNumPaths>([&](auto pp) {
+        constexpr int p = decltype(pp)::value;
+        if constexpr (kPathL[p][0] == L1 && kPathL[p][1] == L2) {
+            constexpr int no = 2 * kPathL[p][2] + 1;
+            float t[no];
+            static_for<no>([&](auto m) { t[decltype(m)::value] = 0.0f; });
+            static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto kk) {
+                constexpr CGEntry e = kCG[kPathEntry[p] + decltype(kk)::value];
+                constexpr int m = e.q - kPathSlot[p];
+                t[m] = fmaf(e.c, s[e.b - b0][e.a - a0], t[m]);
+            });
+            if (store) {
+                static_for<no>([&](auto mm) {
+                    constexpr int m = decltype(mm)::value;
+                    constexpr int pos = fwd_slot_pos(kPathSlot[p] + m);  // compile time
+                    T[tbase + (int64_t)pos * cp] = chan_ok ? t[m] : 0.0f;
+                });
+            }
+        }
+    });
+}
+
+template <int W>
+__device__ __forceinline__ void ps_contract(const float* sSrow, float* __restrict__ T,
+                                            int64_t tbase, int cp, bool store, bool chan_ok) {
+    static_for<5>([&](auto kk) {
+        constexpr int k = decltype(kk)::value;
+        if constexpr (kPsBlocks[W][k][0] >= 0)
+            ps_block<kPsBlocks[W][k][0], kPsBlocks[W][k][1]>(sSrow, T, tbase, cp, store, chan_ok);
+    });
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint64_t u = (uint64_t)v;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// One workgroup per unit (4 destinations at consecutive positions of `order`,
+// 16 input channels).  S phase: wave w sums the edges of destination w, four
+// edges per k-step: lane (g = lane / 16, i = lane % 16) supplies
+//   A[i][g] = X[src of edge g][c0 + 4t + i / 4][4 (i % 4) + j]   (MFMA (t, j), float4 over j)
+//   B[g][i] = Y[edge g][b = i]
+// so that MFMA (t, j) accumulates S[c0 + 4t + m / 4][a = 4 (m % 4) + j][b] in row m.
+// Lane (g, i) then holds S[c0 + 4t + g][all a][b = i] and writes it to LDS.
+// Contraction phase: lane (dd, ch) = (lane / 16, lane % 16) of every wave takes
+// destination dd and channel c0 + ch; wave w contracts its CG blocks.
+__global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
+    const float* __restrict__ yc, const int* __restrict__ srcc, const float* __restrict__ X,
+    const int64_t* __restrict__ row_ptr, const int64_t* __restrict__ order, float* __restrict__ T,
+    int64_t n_dst, int C, int64_t n_units) {
+    __shared__ __attribute__((aligned(16))) float sS[4 * 16 * kPsStride];
+    const int64_t per_xcd = (n_units + 7) / 8;
+    const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (logical >= n_units) return;
+    const int64_t nquad = (n_dst + 3) >> 2;
+    const int chunk = (int)(logical / nquad);  // channel-chunk major: an XCD works on a
+    const int64_t quad = logical - chunk * nquad;  // compact range of destinations
+    const int cp = (C + 15) & ~15;
+    const int c0 = chunk * 16;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i16 = lane & 15;
+
+    int64_t r0 = 0, r1 = 0;
+    {
+        const int64_t pos = quad * 4 + w;
+        if (pos < n_dst) {
+            const int64_t d = order ? order[pos] : pos;
+            r0 = row_ptr[d];
+            r1 = row_ptr[d + 1];
+        }
+        r0 = uniform64(r0);
+        r1 = uniform64(r1);
+    }
+    const int64_t rowf = (int64_t)C * 16;  // floats per source row
+    int coff[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) coff[t] = min(c0 + 4 * t + (i16 >> 2), C - 1) * 16 + (i16 & 3) * 4;
+    v4f acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t kb = r0; kb < r1; kb += 64) {  // groups of up to 64 edges
+        const int ng = (int)min<int64_t>(64, r1 - kb);
+        const int my_src = srcc[kb + min(lane, ng - 1)];
+        const int nst = (ng + 3) >> 2;
+        // gathers of k-step s (edges past the group read a real edge and meet Y = 0)
+        auto load_step = [&](int s, float4* xa, float& yb) {
+            const int jr = 4 * s + g;
+            const int j = min(jr, ng - 1);
+            const int sr = __shfl(my_src, j);
+            const float* rowp = X + (int64_t)sr * rowf;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xa[t] = *reinterpret_cast<const float4*>(rowp + coff[t]);
+            const float yv = yc[(kb + j) * 16 + i16];
+            yb = jr < ng ? yv : 0.0f;
+        };
+        float4 xa[4], xn[4];
+        float ya, yn;
+        load_step(0, xa, ya);
+        for (int s = 0; s < nst; ++s) {
+            load_step(min(s + 1, nst - 1), xn, yn);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                acc[t][0] = mfma1(xa[t].x, ya, acc[t][0]);
+                acc[t][1] = mfma1(xa[t].y, ya, acc[t][1]);
+                acc[t][2] = mfma1(xa[t].z, ya, acc[t][2]);
+                acc[t][3] = mfma1(xa[t].w, ya, acc[t][3]);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xa[t] = xn[t];
+            ya = yn;
+        }
+    }
+    // S[c0 + 4t + g][a = 4r + j][b = i16] -> LDS block (w, 4t + g), row b, quad r
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        float* blk = sS + (w * 16 + 4 * t + g) * kPsStride + i16 * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<float4*>(blk + ((r ^ ps_swz(i16)) * 4)) =
+                make_float4(acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]);
+    }
+    __syncthreads();
+
+    // contraction: lane (dd, ch)
+    const int dd = lane >> 4, ch = lane & 15;
+    const int64_t pos = quad * 4 + dd;
+    const bool store = pos < n_dst;
+    int64_t d = 0;
+    if (store) d = order ? order[pos] : pos;
+    const int64_t tbase = d * kNumSlots * cp + c0 + ch;
+    const float* sSrow = sS + (dd * 16 + ch) * kPsStride;
+    const bool chan_ok = c0 + ch < C;
+    switch (w) {
+        case 0: ps_contract<0>(sSrow, T, tbase, cp, store, chan_ok); break;
+        case 1: ps_contract<1>(sSrow, T, tbase, cp, store, chan_ok); break;
+        case 2: ps_contract<2>(sSrow, T, tbase, cp, store, chan_ok); break;
+        default: ps_contract<3>(sSrow, T, tbase, cp, store, chan_ok); break;
+    }
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace bmhip
+
+extern "C" size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges,
+                                                                   int C_in) {
+    if (N_dst < 0 || N_edges < 0 || C_in <= 0) return 0;
+    const size_t cp = (size_t)((C_in + 15) / 16) * 16;
+    return align256((size_t)N_edges * 16 * sizeof(float)) + align256((size_t)N_edges * sizeof(int)) +
+           align256((size_t)N_dst * kNumSlots * cp * sizeof(float));
+}
+
+extern "C" int batteries_sh_tp_scatter_weighted(
+    const float* edge_vectors, const float* node_features, const float* weights,
+    const int64_t* source_idx, const int64_t* perm, const int64_t* row_ptr, const int64_t* order,
+    float* node_output, int64_t N_src, int64_t N_dst, int64_t N_edges, int C_in, int C_out,
+    int normalize, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (N_src < 0 || N_dst < 0 || N_edges < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
+    if (N_edges > 0 && N_src == 0) return BM_ERR_ARG;
+    if (N_dst == 0) return BM_OK;
+    if (N_edges > INT32_MAX || N_src > INT32_MAX) return BM_ERR_ARG;  // int32 source rows in workspace
+    if ((int64_t)kNumPaths * C_in * C_out * 4 > INT32_MAX) return BM_ERR_ARG;  // W via 32-bit offsets
+    if (ceil_div(N_dst, 16) > INT32_MAX || ceil_div(C_out, 64) > 65535) return BM_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(node_features) | reinterpret_cast<uintptr_t>(node_output) |
+         reinterpret_cast<uintptr_t>(workspace)) & 15)
+        return BM_ERR_ARG;
+    const size_t need = batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, N_edges, C_in);
+    if (!workspace || workspace_bytes < need) return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    float* yc = reinterpret_cast<float*>(ws);
+    int* srcc = reinterpret_cast<int*>(ws + align256((size_t)N_edges * 16 * sizeof(float)));
+    float* tsum = reinterpret_cast<float*>(ws + align256((size_t)N_edges * 16 * sizeof(float)) +
+                                           align256((size_t)N_edges * sizeof(int)));
+    if (N_edges > 0)
+        mp_edge_prep_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
+            edge_vectors, source_idx, perm, N_edges, normalize, yc, srcc);
+    const int64_t nquad = ceil_div(N_dst, 4);
+    const int64_t n_units = nquad * ceil_div(C_in, 16);
+    const int64_t grid = ceil_div(n_units, 8) * 8;
+    if (grid > INT32_MAX) return BM_ERR_ARG;
+    mp_path_sums_kernel<<<(unsigned)grid, 256, 0, stream>>>(yc, srcc, node_features, row_ptr,
+                                                            order, tsum, N_dst, C_in, n_units);
+    const int rc = tp_weighted_mix_launch(tsum, weights, node_output, N_dst, C_in, C_out, stream);
+    if (rc != 0) return rc;
+    return (int)hipGetLastError();
+}

@@ -49,6 +49,7 @@ from _batteries import (  # noqa: E402
     spherical_harmonics_normalized,
     spherical_harmonics_normalized_backward,
     sh_tp_scatter,
+    sh_tp_scatter_weighted,
     neighbor_list,
     spatial_order,
     mp_schedule,
@@ -99,6 +100,7 @@ __all__ = [
     "spherical_harmonics_normalized",
     "spherical_harmonics_normalized_backward",
     "sh_tp_scatter",
+    "sh_tp_scatter_weighted",
     "neighbor_list",
     "spatial_order",
     "mp_schedule",

@@ -44,8 +44,15 @@ class Graph:
             self._rev = _batmobile.mace_reverse_edges(self.row_ptr, self.src)
         return self._rev
 
-    def sh_tp_scatter(self, node_features, normalize=True):
-        """out[d] = sum_{e -> d} TP_simple(X[src_e], Y_lm(v_e)); one kernel, spatial schedule."""
+    def sh_tp_scatter(self, node_features, normalize=True, weights=None):
+        """out[d] = sum_{e -> d} TP_simple(X[src_e], Y_lm(v_e)); one kernel, spatial schedule.
+
+        With weights [34, C_in, C_out]: out[d] = sum_{e -> d} tensor_product(X[src_e],
+        Y_lm(v_e), weights), the per-path sums over each destination's edges mixed once
+        per destination (destinations processed in the spatial order)."""
+        if weights is not None:
+            return _batmobile.sh_tp_scatter_weighted(self.vec, node_features, weights, self.src,
+                                                     self.row_ptr, None, self.order, normalize)
         assert node_features.shape[1] == self.channels, "schedule was built for another C"
         return _batmobile.sh_tp_scatter_scheduled(
             self.vec, node_features, self.src, self.row_ptr_s, self.edge_perm, self.row_dst,

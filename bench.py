@@ -169,6 +169,29 @@ def other_configs(torch, bm, dev):
     return res
 
 
+def weighted_config3(torch, bm, dev, w, reps=100):
+    """configs[3], weighted variant: the same graph and X with W [34, 64, 64] ~ N(0, 1/64)
+    (seed 3 continued), out[d] = sum_{e -> d} tensor_product(X[src_e], Y(v_e), W).
+    Flop models: the survey's minimal exact count E (1222 C) + N (312 C^2) (per-edge CG
+    products, mixing once per destination), and the count this build executes,
+    E (512 C) + N (1222 C + 312 C^2) (edge sums of X Y^T on MFMA, CG and mixing per
+    destination)."""
+    g = torch.Generator().manual_seed(SEED + 100)
+    wt = (torch.randn(34, CHANNELS, CHANNELS, generator=g) / math.sqrt(CHANNELS)).to(dev)
+    graph, x = w["graph"], w["x"]
+    t = event_ms(torch, lambda: graph.sh_tp_scatter(x, weights=wt), reps)
+    e, n, c = graph.num_edges, N_ATOMS, CHANNELS
+    f_survey = e * 1222 * c + n * 312 * c * c
+    f_exec = e * 512 * c + n * (1222 * c + 312 * c * c)
+    return {
+        "cfg3_weighted_ms": round(t, 5),
+        "cfg3_weighted_edges_per_s": round(e / (t * 1e-3), 1),
+        "cfg3_weighted_TFLOPs_survey_model": round(f_survey / (t * 1e-3) / 1e12, 2),
+        "cfg3_weighted_mfma_frac_survey_model": round(f_survey / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4),
+        "cfg3_weighted_TFLOPs_executed": round(f_exec / (t * 1e-3) / 1e12, 2),
+    }
+
+
 def mace_config4(torch, bm, dev, reps=3):
     """MACE-style layer with per-edge radial weights at N = 50,000, C = 128
     (uniform periodic box at ~30 neighbours within 5 A, seed 4): GPU neighbor list +
@@ -305,6 +328,7 @@ def main():
         extra["graph_build_ms"] = round(time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS)), 4)
         extra["index_order_kernel_ms"] = round(time_call(torch, lambda: graph.sh_tp_scatter_index_order(w["x"]), 20), 4)
         extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
+        extra.update(weighted_config3(torch, bm, dev, w))
         extra.update(other_configs(torch, bm, dev))
         extra.update(mace_config4(torch, bm, dev))
 

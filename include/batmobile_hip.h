@@ -163,6 +163,25 @@ int batteries_sh_tp_scatter_scheduled(const float* edge_vectors, const float* no
                                       int64_t N_src, int64_t N_edges, int C, int normalize,
                                       hipStream_t stream);
 
+/* Weighted scatter: node_output[N_dst, C_out, 16] with
+ *   node_output[d] = sum_{k in [row_ptr[d], row_ptr[d+1])}
+ *                    tensor_product(X[source_idx[e_k]], Y(v_{e_k}), weights),  e_k = perm ? perm[k] : k,
+ * weights [34, C_in, C_out] shared by every edge, Y of v / |v| when normalize.
+ * Replaces the reference interaction block's SH -> batteries::tensor_product ->
+ * scatter_add (benchmarks/benchmark_e2e_mace.py:308-349; examples/mace_inference.py:
+ * 152-168), without the [E, C_out, 16] messages.  order (optional, [N_dst]) is the
+ * order in which destinations are processed (any permutation; a spatial order keeps
+ * source rows in L2).  Workspace: per-edge Y and source rows, and the per-path sums
+ * [N_dst][156][16 ceil(C_in / 16)]. */
+size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges, int C_in);
+int batteries_sh_tp_scatter_weighted(const float* edge_vectors, const float* node_features,
+                                     const float* weights, const int64_t* source_idx,
+                                     const int64_t* perm, const int64_t* row_ptr,
+                                     const int64_t* order, float* node_output, int64_t N_src,
+                                     int64_t N_dst, int64_t N_edges, int C_in, int C_out,
+                                     int normalize, void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream);
+
 /* node_output[N_atoms, C, 16]; CSR slot k is edge col_idx[k], whose source is
  * edge_index[0, col_idx[k]] and vector edge_vectors[col_idx[k]].
  * Replaces batteries::fused_message_passing_simple,

@@ -87,6 +87,9 @@ def test_extension_module_names(bm):
     lambda b: b.fused_message_passing(torch.zeros(2, 3, 16), torch.zeros(4, 3), torch.zeros(4, 5),
                                       torch.zeros(3, dtype=torch.int64),
                                       torch.zeros(4, dtype=torch.int64)),
+    lambda b: b.sh_tp_scatter_weighted(torch.zeros(4, 3), torch.zeros(2, 3, 16),
+                                       torch.zeros(33, 3, 3), torch.zeros(4, dtype=torch.int64),
+                                       torch.zeros(3, dtype=torch.int64)),
 ])
 def test_argument_errors_raise_runtime_error(bm, call):
     with pytest.raises(RuntimeError):

@@ -1,0 +1,131 @@
+"""GPU parity: the weighted scatter (fused SH + weighted TP + scatter-add).
+
+out[d] = sum_{e -> d} tensor_product(X[src_e], Y(v_e), W) with one W [34, C_in, C_out],
+the reference interaction block's SH -> tensor_product -> scatter_add
+(benchmarks/benchmark_e2e_mace.py:308-349).  Compared with the float64 oracle
+composition (oracle.mp.weighted_message_passing) within 1e-5 normwise; at the full
+configs[3] size through a sampled set of destinations, the reduction to the simple
+scatter for identity mixing, and linearity in W.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import gen, normwise_err, periodic_box, unit_vectors
+from oracle import mp as omp
+
+pytestmark = pytest.mark.gpu
+
+
+def _csr(dst, n):
+    order = torch.argsort(dst, stable=True)
+    rp = torch.zeros(n + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(torch.bincount(dst, minlength=n), 0)
+    return order, rp
+
+
+def _weights(ci, co, seed):
+    return torch.randn(34, ci, co, generator=gen(seed)) / np.sqrt(ci)
+
+
+@pytest.mark.parametrize("n,e,ci,co,normalize", [
+    (200, 3000, 32, 64, True),
+    (150, 2500, 16, 16, False),
+    (64, 900, 5, 3, True),      # channels below one 16-channel chunk
+    (50, 700, 20, 70, True),    # a partial input chunk, two output-channel groups
+    (33, 400, 48, 8, False),    # an odd number of input chunks
+])
+def test_weighted_scatter_random_graph(bm, dev, n, e, ci, co, normalize):
+    vec = unit_vectors(e, 40 + ci)
+    if normalize:
+        vec = vec * (0.5 + torch.rand(e, 1, generator=gen(41)) * 3.0)
+    x = torch.randn(n, ci, 16, generator=gen(42))
+    w = _weights(ci, co, 43)
+    src = torch.randint(0, n, (e,), generator=gen(44))
+    dst = torch.randint(0, n, (e,), generator=gen(45))
+    order, rp = _csr(dst, n)
+    want = omp.weighted_message_passing(vec.double().numpy(), x.double().numpy(),
+                                        w.double().numpy(), src.numpy(), dst.numpy(), n,
+                                        normalize=normalize)
+    # edge data in its original order, reached through perm
+    out = bm.sh_tp_scatter_weighted(vec.to(dev), x.to(dev), w.to(dev), src.to(dev), rp.to(dev),
+                                    order.to(dev), None, normalize)
+    assert out.shape == (n, co, 16)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    # the same edges stored in CSR order, destinations processed in a shuffled order
+    shuffle = torch.randperm(n, generator=gen(46))
+    out2 = bm.sh_tp_scatter_weighted(vec[order].to(dev), x.to(dev), w.to(dev),
+                                     src[order].to(dev), rp.to(dev), None, shuffle.to(dev),
+                                     normalize)
+    assert torch.equal(out, out2)
+
+
+def test_weighted_scatter_empty_rows_long_rows_and_no_edges(bm, dev):
+    n, ci, co = 30, 32, 64
+    x = torch.randn(n, ci, 16, generator=gen(50))
+    w = _weights(ci, co, 51)
+    # odd destinations have no edges; destination 4 has 203 edges (several 64-edge groups)
+    dst = torch.cat([torch.arange(0, n, 2).repeat_interleave(3), torch.full((200,), 4)])
+    dst, _ = torch.sort(dst)
+    e = dst.numel()
+    src = torch.randint(0, n, (e,), generator=gen(52))
+    vec = unit_vectors(e, 53)
+    _, rp = _csr(dst, n)
+    out = bm.sh_tp_scatter_weighted(vec.to(dev), x.to(dev), w.to(dev), src.to(dev), rp.to(dev))
+    want = omp.weighted_message_passing(vec.double().numpy(), x.double().numpy(),
+                                        w.double().numpy(), src.numpy(), dst.numpy(), n)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    assert torch.count_nonzero(out[1::2]).item() == 0
+    # no edges at all: zeros; no destinations: empty
+    z = bm.sh_tp_scatter_weighted(torch.zeros(0, 3, device=dev), x.to(dev), w.to(dev),
+                                  torch.zeros(0, dtype=torch.int64, device=dev),
+                                  torch.zeros(n + 1, dtype=torch.int64, device=dev))
+    assert z.shape == (n, co, 16) and torch.count_nonzero(z).item() == 0
+    z = bm.sh_tp_scatter_weighted(torch.zeros(0, 3, device=dev), x.to(dev), w.to(dev),
+                                  torch.zeros(0, dtype=torch.int64, device=dev),
+                                  torch.zeros(1, dtype=torch.int64, device=dev))
+    assert z.shape == (0, co, 16)
+
+
+def test_weighted_scatter_matches_reference_composition_on_gpu(bm, dev):
+    """SH -> tensor_product(X[src], Y, W) -> index_add_, the reference's own calls, on this GPU."""
+    n, e, c = 300, 5000, 32
+    vec = unit_vectors(e, 60).to(dev)
+    x = torch.randn(n, c, 16, generator=gen(61)).to(dev)
+    w = _weights(c, c, 62).to(dev)
+    src = torch.randint(0, n, (e,), generator=gen(63)).to(dev)
+    dst = torch.randint(0, n, (e,), generator=gen(64)).to(dev)
+    order, rp = _csr(dst.cpu(), n)
+    fused = bm.sh_tp_scatter_weighted(vec, x, w, src, rp.to(dev), order.to(dev), None, True)
+    msg = bm.tensor_product(x[src], bm.spherical_harmonics(vec, 3), w)
+    ref = torch.zeros(n, c, 16, device=dev).index_add_(0, dst, msg)
+    assert normwise_err(fused.cpu(), ref.cpu()) <= 1e-5
+
+
+def test_config3_weighted_full_size(bm, dev):
+    """configs[3] weighted variant: N = 5000, C = 64, W [34, 64, 64] ~ N(0, 1/64)."""
+    import batmobile
+    n, c = 5000, 64
+    pos, cell = periodic_box(n, 3)
+    graph = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+    x = torch.randn(n, c, 16, generator=gen(70)).to(dev)
+    w = _weights(c, c, 71).to(dev)
+    out = graph.sh_tp_scatter(x, weights=w)
+    # identity mixing reduces the weighted product to the simple one
+    eye = torch.eye(c).expand(34, c, c).contiguous().to(dev)
+    simple = graph.sh_tp_scatter(x)
+    assert normwise_err(graph.sh_tp_scatter(x, weights=eye).cpu(), simple.cpu()) <= 1e-5
+    # linearity in W
+    w2 = _weights(c, c, 72).to(dev)
+    both = graph.sh_tp_scatter(x, weights=w + w2)
+    sep = out + graph.sh_tp_scatter(x, weights=w2)
+    assert normwise_err(both.cpu(), sep.cpu()) <= 1e-5
+    # oracle on a sample of destinations (all of their edges)
+    rp = graph.row_ptr.cpu()
+    pick = torch.randperm(n, generator=gen(73))[:120].sort().values
+    ks = torch.cat([torch.arange(int(rp[d]), int(rp[d + 1])) for d in pick.tolist()])
+    dloc = torch.repeat_interleave(torch.arange(pick.numel()), rp[pick + 1] - rp[pick])
+    want = omp.weighted_message_passing(graph.vec.cpu()[ks].double().numpy(),
+                                        x.cpu().double().numpy(), w.cpu().double().numpy(),
+                                        graph.src.cpu()[ks].numpy(), dloc.numpy(), pick.numel())
+    assert normwise_err(out.cpu()[pick], want) <= 1e-5
