@@ -491,7 +491,8 @@ torch::Tensor sh_tp_scatter_weighted(const torch::Tensor& edge_vectors,
     const c10::DeviceGuard guard(node_features.device());
     torch::Tensor x = aligned16(node_features);
     torch::Tensor w = weights.contiguous();
-    const size_t wsb = batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, E, (int)C_in);
+    const size_t wsb =
+        batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, E, (int)C_in, (int)C_out);
     torch::Tensor ws = torch::empty({(int64_t)((wsb + 15) / 16), 4}, f32_like(node_features));
     check_status(batteries_sh_tp_scatter_weighted(
                      cptr<float>(edge_vectors, "edge_vectors"), cptr<float>(x, "node_features"),

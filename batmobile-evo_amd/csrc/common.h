@@ -202,8 +202,8 @@ __device__ __forceinline__ void tp_per_path_backward(const float* x, const float
 // ---------------------------------------------------------------------------
 // Output groups of the weighted product: slot q (path, m_out) belongs to group
 // kSlotOut[q] / 4, i.e. output components o in [4G, 4G + 4).  Per-path sums
-// stored for the mixing stage ([row][slot][channel]) list the slots group by
-// group, in slot order within a group (fwd_slot_pos).
+// stored for the weighted scatter's mixing stage list the slots group by group,
+// in slot order within a group (fwd_slot_pos).
 // ---------------------------------------------------------------------------
 constexpr int kFwdGroups = 4;
 constexpr bool fwd_in_group(int q, int G) { return kSlotOut[q] / 4 == G; }
@@ -225,11 +225,6 @@ constexpr int fwd_group_base(int G) {
 constexpr int fwd_slot_pos(int q) {
     return fwd_group_base(kSlotOut[q] / 4) + fwd_local(q, kSlotOut[q] / 4);
 }
-
-// Mixing stage of the weighted scatter (tp.hip): out[n, co, o] =
-// sum_{q -> o} sum_ci W[p(q), ci, co] T[n][fwd_slot_pos(q)][ci] on `stream`.
-int tp_weighted_mix_launch(const float* tsum, const float* w, float* out, int64_t n, int cin,
-                           int cout, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // small helpers

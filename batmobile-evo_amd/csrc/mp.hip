@@ -1089,17 +1089,36 @@ extern "C" int batteries_sh_tp_scatter_scheduled(const float* edge_vectors,
 //   T[d, q, ci]    = sum_{(a, b) in slot q} c S[d, ci, a, b]           CG table, VALU
 //   out[d, co, o]  = sum_{q -> o} sum_ci W[p(q), ci, co] T[d, q, ci]   MFMA (tp.hip)
 // Work: 2 * 256 * C_in flops per edge (S), 2 * 611 * C_in + 2 * 156 * C_in * C_out per
-// destination (T, mixing).  T is [N_dst][156][Cp] (slots in fwd_slot_pos order,
-// channels padded to Cp = 16 * ceil(C_in / 16) and zero past C_in).
+// destination (T, mixing).  T is [chunk][slot][position][16]: 16-channel chunks of
+// C_in (zero past C_in), slots in fwd_slot_pos order, destinations by their position
+// in the processing order (padded to a multiple of 16), so that the mixing kernel's
+// operand loads and the path-sum kernel's stores are contiguous 1 KB / 256 B blocks
+// (whole 128-byte lines: a load that uses half of each line it touches runs at half
+// the rate).
 // ---------------------------------------------------------------------------
 namespace bmhip {
 
-// Y and the source row of CSR slot k (edge perm[k] when perm is given), so that
-// the path-sum kernel reads both without indirection.
+// Blocks [0, edge_blocks): Y and the source row of CSR slot k (edge perm[k] when
+// perm is given), so that the path-sum kernel reads both without indirection.
+// Blocks past them: wt[chunk][p][co][16] = W[p][16 chunk + i][co], zero past cin (the
+// mixing kernel's B operand: 16 output channels x 16 input channels = 1 KB contiguous).
 __global__ __launch_bounds__(256) void mp_edge_prep_kernel(
     const float* __restrict__ vec, const int64_t* __restrict__ src_idx,
     const int64_t* __restrict__ perm, int64_t n_edges, int normalize, float* __restrict__ yc,
-    int* __restrict__ srcc) {
+    int* __restrict__ srcc, int64_t edge_blocks, const float* __restrict__ w,
+    float* __restrict__ wt, int cin, int cout, int cp) {
+    if ((int64_t)blockIdx.x >= edge_blocks) {
+        const int64_t i = ((int64_t)blockIdx.x - edge_blocks) * 256 + threadIdx.x;
+        if (i >= (int64_t)kNumPaths * cout * cp) return;
+        const int cl = (int)(i & 15);
+        const int64_t r = i >> 4;  // (chunk * 34 + p) * cout + co
+        const int co = (int)(r % cout);
+        const int64_t cpp = r / cout;
+        const int p = (int)(cpp % kNumPaths);
+        const int ci = (int)(cpp / kNumPaths) * 16 + cl;
+        wt[i] = ci < cin ? w[((int64_t)p * cin + ci) * cout + co] : 0.0f;
+        return;
+    }
     const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (k >= n_edges) return;
     const int64_t e = perm ? perm[k] : k;
@@ -1129,10 +1148,11 @@ constexpr int kPsBlocks[4][5][2] = {{{1, 0}, {3, 1}, {3, 3}, {-1, -1}, {-1, -1}}
                                     {{1, 1}, {2, 0}, {2, 1}, {2, 2}, {-1, -1}}};
 
 // The slots of the paths (L1, L2, *) for this lane's (destination, channel):
-// reads S[a in l1][b in l2], contracts with the CG terms, stores T[row][pos(q)][ch].
+// reads S[a in l1][b in l2], contracts with the CG terms, stores
+// T[tbase + pos(q) * sstride].
 template <int L1, int L2>
 __device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__ T, int64_t tbase,
-                                         int cp, bool store, bool chan_ok) {
+                                         int64_t sstride, bool store, bool chan_ok) {
     constexpr int a0 = L1 * L1, na = 2 * L1 + 1, b0 = L2 * L2, nb = 2 * L2 + 1;
     constexpr int qa0 = a0 / 4, qa1 = (a0 + na - 1) / 4;
     float s[nb][na];
@@ -1165,7 +1185,7 @@ __device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__
                 static_for<no>([&](auto mm) {
                     constexpr int m = decltype(mm)::value;
                     constexpr int pos = fwd_slot_pos(kPathSlot[p] + m);  // compile time
-                    T[tbase + (int64_t)pos * cp] = chan_ok ? t[m] : 0.0f;
+                    T[tbase + pos * sstride] = chan_ok ? t[m] : 0.0f;
                 });
             }
         }
@@ -1174,11 +1194,13 @@ __device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__
 
 template <int W>
 __device__ __forceinline__ void ps_contract(const float* sSrow, float* __restrict__ T,
-                                            int64_t tbase, int cp, bool store, bool chan_ok) {
+                                            int64_t tbase, int64_t sstride, bool store,
+                                            bool chan_ok) {
     static_for<5>([&](auto kk) {
         constexpr int k = decltype(kk)::value;
         if constexpr (kPsBlocks[W][k][0] >= 0)
-            ps_block<kPsBlocks[W][k][0], kPsBlocks[W][k][1]>(sSrow, T, tbase, cp, store, chan_ok);
+            ps_block<kPsBlocks[W][k][0], kPsBlocks[W][k][1]>(sSrow, T, tbase, sstride, store,
+                                                             chan_ok);
     });
 }
 
@@ -1189,28 +1211,34 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// One workgroup per unit (4 destinations at consecutive positions of `order`,
-// 16 input channels).  S phase: wave w sums the edges of destination w, four
-// edges per k-step: lane (g = lane / 16, i = lane % 16) supplies
+// One workgroup per unit: 4 destinations at consecutive positions of `order`
+// and `cpw` consecutive 16-channel chunks.  Per chunk:
+// S phase: wave w sums the edges of destination w, four edges per k-step: lane
+// (g = lane / 16, i = lane % 16) supplies
 //   A[i][g] = X[src of edge g][c0 + 4t + i / 4][4 (i % 4) + j]   (MFMA (t, j), float4 over j)
 //   B[g][i] = Y[edge g][b = i]
 // so that MFMA (t, j) accumulates S[c0 + 4t + m / 4][a = 4 (m % 4) + j][b] in row m.
 // Lane (g, i) then holds S[c0 + 4t + g][all a][b = i] and writes it to LDS.
 // Contraction phase: lane (dd, ch) = (lane / 16, lane % 16) of every wave takes
 // destination dd and channel c0 + ch; wave w contracts its CG blocks.
+// The k-steps of a wave run through a three-stage load pipeline that continues
+// across chunks: the source index and Y of step i + 2, the source-row gathers of
+// step i + 1, the MFMAs of step i.  The next chunk's first gathers are therefore
+// in flight during this chunk's contraction.
 __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
     const float* __restrict__ yc, const int* __restrict__ srcc, const float* __restrict__ X,
     const int64_t* __restrict__ row_ptr, const int64_t* __restrict__ order, float* __restrict__ T,
-    int64_t n_dst, int C, int64_t n_units) {
+    int64_t n_dst, int64_t npad, int C, int cpw, int64_t n_units) {
     __shared__ __attribute__((aligned(16))) float sS[4 * 16 * kPsStride];
     const int64_t per_xcd = (n_units + 7) / 8;
     const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (logical >= n_units) return;
     const int64_t nquad = (n_dst + 3) >> 2;
-    const int chunk = (int)(logical / nquad);  // channel-chunk major: an XCD works on a
-    const int64_t quad = logical - chunk * nquad;  // compact range of destinations
-    const int cp = (C + 15) & ~15;
-    const int c0 = chunk * 16;
+    const int nchunk = (C + 15) >> 4;
+    const int cgrp = (int)(logical / nquad);  // chunk-group major: an XCD works on a
+    const int64_t quad = logical - cgrp * nquad;  // compact range of destinations
+    const int ch0 = cgrp * cpw;                   // first chunk of this unit
+    const int nch = min(cpw, nchunk - ch0);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i16 = lane & 15;
 
     int64_t r0 = 0, r1 = 0;
@@ -1224,36 +1252,64 @@ __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
         r0 = uniform64(r0);
         r1 = uniform64(r1);
     }
+    const int deg = (int)(r1 - r0);
+    const int nst = (deg + 3) >> 2;  // k-steps per chunk
     const int64_t rowf = (int64_t)C * 16;  // floats per source row
-    int coff[4];
+    // CSR slot of this lane's edge in step s (past the row: its last edge, Y masked to 0)
+    auto slot = [&](int s) { return r0 + min(4 * s + g, deg - 1); };
+    auto gather = [&](int src, int chunk, float4(&xv)[4]) {
+        const float* rowp = X + (int64_t)src * rowf;
+        const int c0 = (ch0 + chunk) * 16;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) coff[t] = min(c0 + 4 * t + (i16 >> 2), C - 1) * 16 + (i16 & 3) * 4;
+        for (int t = 0; t < 4; ++t)
+            xv[t] = *reinterpret_cast<const float4*>(
+                rowp + min(c0 + 4 * t + (i16 >> 2), C - 1) * 16 + (i16 & 3) * 4);
+    };
+    // the step after (c, s), or (c, s) itself past the last step
+    auto next = [&](int& c, int& s) {
+        if (s + 1 < nst) {
+            ++s;
+        } else if (c + 1 < nch) {
+            ++c;
+            s = 0;
+        }
+    };
+    // pipeline state: stage A (source index, Y) and stage B (gathers)
+    int cA = 0, sA = 0, cB = 0, sB = 0;
+    int srcA = 0;
+    float yA = 0.f, yB = 0.f;
+    float4 xB[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xB[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (nst > 0) {
+        srcA = srcc[slot(0)];
+        yA = 4 * 0 + g < deg ? yc[slot(0) * 16 + i16] : 0.f;
+        gather(srcA, 0, xB);
+        yB = yA;
+        next(cA, sA);
+        srcA = srcc[slot(sA)];
+        yA = 4 * sA + g < deg ? yc[slot(sA) * 16 + i16] : 0.f;
+    }
     v4f acc[4][4];
+    for (int c = 0; c < nch; ++c) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    for (int64_t kb = r0; kb < r1; kb += 64) {  // groups of up to 64 edges
-        const int ng = (int)min<int64_t>(64, r1 - kb);
-        const int my_src = srcc[kb + min(lane, ng - 1)];
-        const int nst = (ng + 3) >> 2;
-        // gathers of k-step s (edges past the group read a real edge and meet Y = 0)
-        auto load_step = [&](int s, float4* xa, float& yb) {
-            const int jr = 4 * s + g;
-            const int j = min(jr, ng - 1);
-            const int sr = __shfl(my_src, j);
-            const float* rowp = X + (int64_t)sr * rowf;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) xa[t] = *reinterpret_cast<const float4*>(rowp + coff[t]);
-            const float yv = yc[(kb + j) * 16 + i16];
-            yb = jr < ng ? yv : 0.0f;
-        };
-        float4 xa[4], xn[4];
-        float ya, yn;
-        load_step(0, xa, ya);
+            for (int j = 0; j < 4; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
         for (int s = 0; s < nst; ++s) {
-            load_step(min(s + 1, nst - 1), xn, yn);
+            float4 xa[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xa[t] = xB[t];
+            const float ya = yB;
+            next(cB, sB);  // stage B: gathers of the following step
+            gather(srcA, cB, xB);
+            yB = yA;
+            next(cA, sA);  // stage A: index and Y two steps ahead
+            srcA = srcc[slot(sA)];
+            {
+                const float yv = yc[slot(sA) * 16 + i16];
+                yA = 4 * sA + g < deg ? yv : 0.f;
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 acc[t][0] = mfma1(xa[t].x, ya, acc[t][0]);
@@ -1261,36 +1317,165 @@ __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
                 acc[t][2] = mfma1(xa[t].z, ya, acc[t][2]);
                 acc[t][3] = mfma1(xa[t].w, ya, acc[t][3]);
             }
+        }
+        if (c > 0) __syncthreads();  // the previous chunk's contraction reads are done
+        // S[c0 + 4t + g][a = 4r + j][b = i16] -> LDS block (w, 4t + g), row b, quad r
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xa[t] = xn[t];
-            ya = yn;
+        for (int t = 0; t < 4; ++t) {
+            float* blk = sS + (w * 16 + 4 * t + g) * kPsStride + i16 * 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<float4*>(blk + ((r ^ ps_swz(i16)) * 4)) =
+                    make_float4(acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]);
+        }
+        __syncthreads();
+        // contraction: lane (dd, ch)
+        // T[chunk][slot][position][16]: the 4 positions x 16 channels of one slot are
+        // 256 contiguous bytes
+        const int dd = lane >> 4, ch = lane & 15;
+        const int c0 = (ch0 + c) * 16;
+        const int64_t pos = quad * 4 + dd;
+        const bool store = pos < n_dst;
+        const int64_t sstride = npad * 16;
+        const int64_t tbase = (int64_t)(ch0 + c) * kNumSlots * sstride + pos * 16 + ch;
+        const float* sSrow = sS + (dd * 16 + ch) * kPsStride;
+        const bool chan_ok = c0 + ch < C;
+        switch (w) {
+            case 0: ps_contract<0>(sSrow, T, tbase, sstride, store, chan_ok); break;
+            case 1: ps_contract<1>(sSrow, T, tbase, sstride, store, chan_ok); break;
+            case 2: ps_contract<2>(sSrow, T, tbase, sstride, store, chan_ok); break;
+            default: ps_contract<3>(sSrow, T, tbase, sstride, store, chan_ok); break;
         }
     }
-    // S[c0 + 4t + g][a = 4r + j][b = i16] -> LDS block (w, 4t + g), row b, quad r
+}
+
+// Mixing stage: out[order[r], co, o] = sum_{q: out(q) = o} sum_ci W[p(q), ci, co] T[., q, r, ci]
+// over positions r.  One wave per (16 positions, output component o, 64 output
+// channels), no LDS until the output: per slot q of o and 16-channel chunk, four
+// k-steps of
+//   D[r][co] += A[r][ci] B[ci][co],  A = T (lane (r = l % 16, k = l / 16): float4
+//   over ci = 4k .. 4k + 3),  B = wt (lane (k, co = l % 16), the same four ci)
+// for the four 16-channel tiles of co.  Each operand load is 1 KB contiguous.  A path
+// reaches o through one slot only, so every slot brings its own W.  Operands are
+// loaded kMixAhead slots ahead, across chunk boundaries.
+constexpr int kMixAhead = 2;
+constexpr int n_slots_out(int o) {
+    int c = 0;
+    for (int q = 0; q < kNumSlots; ++q) c += kSlotOut[q] == o ? 1 : 0;
+    return c;
+}
+constexpr int slot_of_out(int o, int k) {
+    for (int q = 0; q < kNumSlots; ++q)
+        if (kSlotOut[q] == o) {
+            if (k == 0) return q;
+            --k;
+        }
+    return -1;
+}
+
+template <int O>
+__device__ __forceinline__ void mix_component(const float* __restrict__ T,
+                                              const float* __restrict__ wt, float* sOut, int64_t n,
+                                              int64_t npad, int nchunk, int cout, int64_t row0,
+                                              int co0) {
+    constexpr int NS = n_slots_out(O);
+    static_assert(NS >= kMixAhead, "ring deeper than the slot list");
+    const int lane = threadIdx.x & 63, g4 = lane >> 4, i16 = lane & 15;
+    // buffer loads: lane offsets in VGPRs, (chunk, slot, path) offsets in SGPRs
+    const int64_t tchunk = (int64_t)kNumSlots * npad * 16;  // floats per chunk of T
+    const uint32_t tchunk_bytes = (uint32_t)(tchunk * sizeof(float));
+    const int toff = ((int)min<int64_t>(i16, n - 1 - row0) * 16 + 4 * g4) * 4;
+    const int trow = (int)(row0 * 64);   // bytes of the tile's first position in a slot
+    const int tslot = (int)(npad * 64);  // bytes per slot
+    const __amdgpu_buffer_rsrc_t wr =
+        buffer_rsrc(wt, (uint32_t)((int64_t)nchunk * kNumPaths * cout * 64));
+    const int wpath = cout * 64, wchunk = kNumPaths * cout * 64;
+    int wco[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        float* blk = sS + (w * 16 + 4 * t + g) * kPsStride + i16 * 16;
+    for (int t = 0; t < 4; ++t) wco[t] = (min(co0 + 16 * t + i16, cout - 1) * 16 + 4 * g4) * 4;
+    v4f acc[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<float4*>(blk + ((r ^ ps_swz(i16)) * 4)) =
-                make_float4(acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]);
+    for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto load = [&](int chunk, auto kk, float4& a, float4 (&b)[4]) {
+        constexpr int k = decltype(kk)::value;
+        constexpr int q = slot_of_out(O, k);
+        constexpr int pos = fwd_slot_pos(q);
+        constexpr int p = kSlotPath[q];
+        const __amdgpu_buffer_rsrc_t tr = buffer_rsrc(T + chunk * tchunk, tchunk_bytes);
+        a = buffer_ld4(tr, toff, pos * tslot + trow);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[t] = buffer_ld4(wr, wco[t], chunk * wchunk + p * wpath);
+    };
+    float4 hA[kMixAhead], hB[kMixAhead][4];  // first slots of the current chunk
+    static_for<kMixAhead>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        load(0, jj, hA[j], hB[j]);
+    });
+    for (int c = 0; c < nchunk; ++c) {
+        float4 oA[NS], oB[NS][4];
+        static_for<kMixAhead>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            oA[j] = hA[j];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) oB[j][t] = hB[j][t];
+        });
+        static_for<NS>([&](auto kk) {
+            constexpr int k = decltype(kk)::value;
+            constexpr int kn = k + kMixAhead;
+            if constexpr (kn < NS)
+                load(c, std::integral_constant<int, kn>{}, oA[kn], oB[kn]);
+            else
+                load(min(c + 1, nchunk - 1), std::integral_constant<int, kn - NS>{}, hA[kn - NS],
+                     hB[kn - NS]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = mfma4(oA[k], oB[k][t], acc[t]);
+            // keep the ring: no load moves ahead of the slot it belongs to
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    // D[4 g4 + r][i16]: position 4 g4 + r of the tile, channel 16 t + i16 of the 64; the
+    // workgroup's four components of one (position, channel) meet in LDS
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sOut[((4 * g4 + r) * 64 + 16 * t + i16) * 4 + w] = acc[t][r];
+}
+
+// grid (4 x 16-position tiles, 64-channel tiles of C_out): block x is group G = x % 4 of
+// tile x / 4 (a tile's four blocks are dispatched together), wave w takes o = 4 G + w,
+// and the block stores float4 (o = 4 G .. 4 G + 3) per (destination, channel).
+__global__ __launch_bounds__(256) void mp_weighted_mix_kernel(const float* __restrict__ T,
+                                                              const float* __restrict__ wt,
+                                                              const int64_t* __restrict__ order,
+                                                              float* __restrict__ out, int64_t n,
+                                                              int64_t npad, int nchunk, int cout) {
+    __shared__ __attribute__((aligned(16))) float sOut[16 * 64 * 4];
+    const int G = blockIdx.x & 3;
+    const int64_t row0 = (int64_t)(blockIdx.x >> 2) * 16;
+    const int co0 = blockIdx.y * 64;
+    switch (G * 4 + (threadIdx.x >> 6)) {
+#define BM_MIX_CASE(o) \
+    case o: mix_component<o>(T, wt, sOut, n, npad, nchunk, cout, row0, co0); break;
+        BM_MIX_CASE(0) BM_MIX_CASE(1) BM_MIX_CASE(2) BM_MIX_CASE(3)
+        BM_MIX_CASE(4) BM_MIX_CASE(5) BM_MIX_CASE(6) BM_MIX_CASE(7)
+        BM_MIX_CASE(8) BM_MIX_CASE(9) BM_MIX_CASE(10) BM_MIX_CASE(11)
+        BM_MIX_CASE(12) BM_MIX_CASE(13) BM_MIX_CASE(14)
+#undef BM_MIX_CASE
+        default: mix_component<15>(T, wt, sOut, n, npad, nchunk, cout, row0, co0); break;
     }
     __syncthreads();
-
-    // contraction: lane (dd, ch)
-    const int dd = lane >> 4, ch = lane & 15;
-    const int64_t pos = quad * 4 + dd;
-    const bool store = pos < n_dst;
-    int64_t d = 0;
-    if (store) d = order ? order[pos] : pos;
-    const int64_t tbase = d * kNumSlots * cp + c0 + ch;
-    const float* sSrow = sS + (dd * 16 + ch) * kPsStride;
-    const bool chan_ok = c0 + ch < C;
-    switch (w) {
-        case 0: ps_contract<0>(sSrow, T, tbase, cp, store, chan_ok); break;
-        case 1: ps_contract<1>(sSrow, T, tbase, cp, store, chan_ok); break;
-        case 2: ps_contract<2>(sSrow, T, tbase, cp, store, chan_ok); break;
-        default: ps_contract<3>(sSrow, T, tbase, cp, store, chan_ok); break;
+    // 16 positions x 64 channels of float4: four per thread
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + 256 * k;  // position i / 64, channel i % 64
+        const int64_t r = row0 + (i >> 6);
+        const int co = co0 + (i & 63);
+        if (r < n && co < cout) {
+            const int64_t d = order ? order[r] : r;
+            *reinterpret_cast<float4*>(out + (d * cout + co) * 16 + 4 * G) =
+                *reinterpret_cast<const float4*>(sOut + i * 4);
+        }
     }
 }
 
@@ -1299,11 +1484,13 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace bmhip
 
 extern "C" size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges,
-                                                                   int C_in) {
-    if (N_dst < 0 || N_edges < 0 || C_in <= 0) return 0;
+                                                                   int C_in, int C_out) {
+    if (N_dst < 0 || N_edges < 0 || C_in <= 0 || C_out <= 0) return 0;
     const size_t cp = (size_t)((C_in + 15) / 16) * 16;
+    const size_t npad = (size_t)((N_dst + 15) / 16) * 16;
     return align256((size_t)N_edges * 16 * sizeof(float)) + align256((size_t)N_edges * sizeof(int)) +
-           align256((size_t)N_dst * kNumSlots * cp * sizeof(float));
+           align256(npad * kNumSlots * cp * sizeof(float)) +
+           align256((size_t)kNumPaths * C_out * cp * sizeof(float));
 }
 
 extern "C" int batteries_sh_tp_scatter_weighted(
@@ -1320,23 +1507,39 @@ extern "C" int batteries_sh_tp_scatter_weighted(
     if ((reinterpret_cast<uintptr_t>(node_features) | reinterpret_cast<uintptr_t>(node_output) |
          reinterpret_cast<uintptr_t>(workspace)) & 15)
         return BM_ERR_ARG;
-    const size_t need = batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, N_edges, C_in);
+    const size_t need =
+        batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, N_edges, C_in, C_out);
     if (!workspace || workspace_bytes < need) return BM_ERR_WORKSPACE;
+    const int cp = (C_in + 15) / 16 * 16;
+    const int64_t npad = ceil_div(N_dst, 16) * 16;
+    // 32-bit byte offsets inside one chunk of T and inside wt
+    if ((int64_t)kNumSlots * npad * 64 > INT32_MAX) return BM_ERR_ARG;
+    if ((int64_t)kNumPaths * C_out * cp * 4 > INT32_MAX) return BM_ERR_ARG;
     char* ws = static_cast<char*>(workspace);
     float* yc = reinterpret_cast<float*>(ws);
-    int* srcc = reinterpret_cast<int*>(ws + align256((size_t)N_edges * 16 * sizeof(float)));
-    float* tsum = reinterpret_cast<float*>(ws + align256((size_t)N_edges * 16 * sizeof(float)) +
-                                           align256((size_t)N_edges * sizeof(int)));
-    if (N_edges > 0)
-        mp_edge_prep_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
-            edge_vectors, source_idx, perm, N_edges, normalize, yc, srcc);
+    ws += align256((size_t)N_edges * 16 * sizeof(float));
+    int* srcc = reinterpret_cast<int*>(ws);
+    ws += align256((size_t)N_edges * sizeof(int));
+    float* tsum = reinterpret_cast<float*>(ws);
+    ws += align256((size_t)npad * kNumSlots * cp * sizeof(float));
+    float* wt = reinterpret_cast<float*>(ws);
+    const int64_t edge_blocks = ceil_div(N_edges, 256);
+    const int64_t wt_blocks = ceil_div((int64_t)kNumPaths * C_out * cp, 256);
+    if (edge_blocks + wt_blocks > INT32_MAX) return BM_ERR_ARG;
+    mp_edge_prep_kernel<<<(unsigned)(edge_blocks + wt_blocks), 256, 0, stream>>>(
+        edge_vectors, source_idx, perm, N_edges, normalize, yc, srcc, edge_blocks, weights, wt,
+        C_in, C_out, cp);
     const int64_t nquad = ceil_div(N_dst, 4);
-    const int64_t n_units = nquad * ceil_div(C_in, 16);
+    const int nchunk = (C_in + 15) / 16;
+    const int cpw = std::min(nchunk, 2);  // 16-channel chunks per workgroup
+    const int64_t n_units = nquad * ceil_div(nchunk, cpw);
     const int64_t grid = ceil_div(n_units, 8) * 8;
     if (grid > INT32_MAX) return BM_ERR_ARG;
-    mp_path_sums_kernel<<<(unsigned)grid, 256, 0, stream>>>(yc, srcc, node_features, row_ptr,
-                                                            order, tsum, N_dst, C_in, n_units);
-    const int rc = tp_weighted_mix_launch(tsum, weights, node_output, N_dst, C_in, C_out, stream);
-    if (rc != 0) return rc;
+    mp_path_sums_kernel<<<(unsigned)grid, 256, 0, stream>>>(
+        yc, srcc, node_features, row_ptr, order, tsum, N_dst, npad, C_in, cpw, n_units);
+    if (ceil_div(N_dst, 16) * 4 > INT32_MAX) return BM_ERR_ARG;
+    dim3 mgrid((unsigned)(ceil_div(N_dst, 16) * 4), (unsigned)ceil_div(C_out, 64), 1);
+    mp_weighted_mix_kernel<<<mgrid, 256, 0, stream>>>(tsum, wt, order, node_output, N_dst, npad,
+                                                      nchunk, C_out);
     return (int)hipGetLastError();
 }

@@ -220,10 +220,7 @@ __device__ __forceinline__ void load16_mask(const float* __restrict__ p, int64_t
 // VALU work at about twice the rate of a lone wave.
 // LDS layout sT[slot][g][row][s] with ci = 4g + s: the B read of lane
 // (row = lane % 16, g) is one float4, and a wave's T writes are contiguous.
-// FROM_T: x holds the per-path sums T[row][fwd_slot_pos(q)][ci] (channels padded
-// to a multiple of 16, zero past cin) and y is unused: the chunk's T values are
-// loaded instead of built (the mixing stage of the weighted scatter).
-template <int G, bool FROM_T>
+template <int G>
 __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const float* __restrict__ w,
                                           float* __restrict__ out, int64_t n, int cin, int cout,
                                           float* sTall, const float* __restrict__ y) {
@@ -239,7 +236,7 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
     // y of the T thread's row, straight from global memory (issued with the
     // first chunk's x and W loads; rows past n only reach discarded outputs)
     float yb[16];
-    if constexpr (!FROM_T) load16(y, min<int64_t>(row0 + trow, n - 1) * 16, yb);
+    load16(y, min<int64_t>(row0 + trow, n - 1) * 16, yb);
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -250,26 +247,8 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (uint32_t)(kNumPaths * wpath_bytes));
     // every half runs the same number of chunks (a chunk past cin builds T = 0)
     const int nchunk = (cin + 16 * nhalf - 1) / (16 * nhalf);
-    const int cp = (cin + 15) & ~15;  // FROM_T: padded channel count of x
-    constexpr int kItems = (NS * 64 + 255) / 256;  // FROM_T: float4 loads per thread and chunk
     for (int ch = 0; ch < nchunk; ++ch) {
         const int c0 = (ch * nhalf + half) * 16;
-        // FROM_T: item i of the chunk is row i % 16, channel quad (i / 16) % 4 and
-        // slot i / 64 (8 consecutive lanes write 8 rows: no LDS bank conflict).
-        // Issued before the W loads, so that waiting for them leaves W in flight.
-        float4 tv[FROM_T ? kItems : 1];
-        if constexpr (FROM_T) {
-            const int cc = min(c0, cp - 16);  // a chunk past cp reads chunk cp - 16 (zeroed below)
-            constexpr int gbase = fwd_group_base(G);  // compile time
-            static_for<kItems>([&](auto ii) {
-                constexpr int it = decltype(ii)::value;
-                const int i = min(tid + 256 * it, NS * 64 - 1);
-                const int64_t row = min<int64_t>(row0 + (i & 15), n - 1);
-                tv[it] = *reinterpret_cast<const float4*>(
-                    x + (row * kNumSlots + gbase + (i >> 6)) * (int64_t)cp + cc +
-                        4 * ((i >> 4) & 3));
-            });
-        }
         // A operands W[p][c0 + 4 g4 + s][co] of the group's paths through a
         // register ring of kWRing paths: the first ones are issued before the T
         // computation (their latency hides behind it), and each path's MFMAs
@@ -292,7 +271,7 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
             wring[k] = load_w(pk);
         });
         float t[NS];
-        if constexpr (!FROM_T) {
+        {
             const int ci = c0 + tcl;
             // y through an empty asm each chunk: the products c * y[b] are formed
             // here instead of being hoisted out of the chunk loop (and kept live)
@@ -318,22 +297,8 @@ __device__ __forceinline__ void fwd_group(const float* __restrict__ x, const flo
             });
         }
         __syncthreads();  // the previous chunk's B reads are done
-        if constexpr (FROM_T) {
-            const bool cok = c0 < cp;
-            static_for<kItems>([&](auto ii) {
-                constexpr int it = decltype(ii)::value;
-                const int i = tid + 256 * it;
-                if (i < NS * 64) {
-                    float4 v = tv[it];
-                    if (!cok) v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    *reinterpret_cast<float4*>(sT + (i >> 6) * 256 + ((i >> 4) & 3) * 64 +
-                                               (i & 15) * 4) = v;
-                }
-            });
-        } else {
 #pragma unroll
-            for (int q = 0; q < NS; ++q) sT[q * 256 + (tcl >> 2) * 64 + trow * 4 + (tcl & 3)] = t[q];
-        }
+        for (int q = 0; q < NS; ++q) sT[q * 256 + (tcl >> 2) * 64 + trow * 4 + (tcl & 3)] = t[q];
         __syncthreads();
         if (live) {
             static_for<kNumPaths>([&](auto pp) {
@@ -394,25 +359,10 @@ __global__ __launch_bounds__(2 * kTpBlock) void tp_weighted_fwd_mfma_kernel(
     float* __restrict__ out, int64_t n, int cin, int cout) {
     __shared__ __attribute__((aligned(16))) float sT[2 * kFwdMaxSlots * 256];
     switch (blockIdx.z) {
-        case 0: fwd_group<0, false>(x, w, out, n, cin, cout, sT, y); break;
-        case 1: fwd_group<1, false>(x, w, out, n, cin, cout, sT, y); break;
-        case 2: fwd_group<2, false>(x, w, out, n, cin, cout, sT, y); break;
-        default: fwd_group<3, false>(x, w, out, n, cin, cout, sT, y); break;
-    }
-}
-
-// Mixing stage of the weighted scatter: out[n, co, o] = sum_{q -> o} sum_ci
-// W[p(q), ci, co] T[n, q, ci] from stored per-path sums T (same tiles, grid and
-// MFMA schedule as the forward).
-__global__ __launch_bounds__(2 * kTpBlock) void tp_weighted_mix_mfma_kernel(
-    const float* __restrict__ tsum, const float* __restrict__ w, float* __restrict__ out,
-    int64_t n, int cin, int cout) {
-    __shared__ __attribute__((aligned(16))) float sT[2 * kFwdMaxSlots * 256];
-    switch (blockIdx.z) {
-        case 0: fwd_group<0, true>(tsum, w, out, n, cin, cout, sT, nullptr); break;
-        case 1: fwd_group<1, true>(tsum, w, out, n, cin, cout, sT, nullptr); break;
-        case 2: fwd_group<2, true>(tsum, w, out, n, cin, cout, sT, nullptr); break;
-        default: fwd_group<3, true>(tsum, w, out, n, cin, cout, sT, nullptr); break;
+        case 0: fwd_group<0>(x, w, out, n, cin, cout, sT, y); break;
+        case 1: fwd_group<1>(x, w, out, n, cin, cout, sT, y); break;
+        case 2: fwd_group<2>(x, w, out, n, cin, cout, sT, y); break;
+        default: fwd_group<3>(x, w, out, n, cin, cout, sT, y); break;
     }
 }
 
@@ -904,14 +854,6 @@ static int64_t gw_rows_per_seg(int64_t n, int cin, int cout) {
 }
 static int64_t gw_segments(int64_t n, int cin, int cout) {
     return ceil_div(std::max<int64_t>(1, ceil_div(n, kTile)) * kTile, gw_rows_per_seg(n, cin, cout));
-}
-
-int tp_weighted_mix_launch(const float* tsum, const float* w, float* out, int64_t n, int cin,
-                           int cout, hipStream_t stream) {
-    dim3 grid((unsigned)ceil_div(n, kTile), (unsigned)ceil_div(cout, 64), kFwdGroups);
-    const int halves = cin > 16 ? 2 : 1;
-    tp_weighted_mix_mfma_kernel<<<grid, halves * kTpBlock, 0, stream>>>(tsum, w, out, n, cin, cout);
-    return (int)hipGetLastError();
 }
 
 }  // namespace bmhip

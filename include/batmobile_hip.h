@@ -171,9 +171,10 @@ int batteries_sh_tp_scatter_scheduled(const float* edge_vectors, const float* no
  * scatter_add (benchmarks/benchmark_e2e_mace.py:308-349; examples/mace_inference.py:
  * 152-168), without the [E, C_out, 16] messages.  order (optional, [N_dst]) is the
  * order in which destinations are processed (any permutation; a spatial order keeps
- * source rows in L2).  Workspace: per-edge Y and source rows, and the per-path sums
- * [N_dst][156][16 ceil(C_in / 16)]. */
-size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges, int C_in);
+ * source rows in L2).  Workspace: per-edge Y and source rows, the per-path sums
+ * [N_dst][156][16 ceil(C_in / 16)] and W transposed to [34][C_out][16 ceil(C_in / 16)]. */
+size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges, int C_in,
+                                                        int C_out);
 int batteries_sh_tp_scatter_weighted(const float* edge_vectors, const float* node_features,
                                      const float* weights, const int64_t* source_idx,
                                      const int64_t* perm, const int64_t* row_ptr,
