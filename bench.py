@@ -263,6 +263,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--headline-only", action="store_true",
                     help="time the configs[3] step only (skip the other configurations)")
+    ap.add_argument("--weighted-only", action="store_true",
+                    help="time only the configs[3] weighted variant and print its figures "
+                         "(for counter passes)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the workload, run 5 plain device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -285,6 +288,10 @@ def main():
         del s, d
     w = make_workload(torch, bm, dev)
     E = int(w["src"].numel())
+    if a.weighted_only:
+        weighted_config3(torch, bm, dev, w, reps=SETTLE_STEPS // 2)  # clock settle
+        print(json.dumps(weighted_config3(torch, bm, dev, w, reps=max(a.steps, 1))), flush=True)
+        return
 
     graph = w["graph"]
 
