@@ -1246,8 +1246,10 @@ __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
         const int64_t pos = quad * 4 + w;
         if (pos < n_dst) {
             const int64_t d = order ? order[pos] : pos;
-            r0 = row_ptr[d];
-            r1 = row_ptr[d + 1];
+            if (d >= 0 && d < n_dst) {  // an order entry out of range sums no edges
+                r0 = row_ptr[d];
+                r1 = row_ptr[d + 1];
+            }
         }
         r0 = uniform64(r0);
         r1 = uniform64(r1);
@@ -1473,8 +1475,9 @@ __global__ __launch_bounds__(256) void mp_weighted_mix_kernel(const float* __res
         const int co = co0 + (i & 63);
         if (r < n && co < cout) {
             const int64_t d = order ? order[r] : r;
-            *reinterpret_cast<float4*>(out + (d * cout + co) * 16 + 4 * G) =
-                *reinterpret_cast<const float4*>(sOut + i * 4);
+            if (d >= 0 && d < n)  // an order entry out of range is not written
+                *reinterpret_cast<float4*>(out + (d * cout + co) * 16 + 4 * G) =
+                    *reinterpret_cast<const float4*>(sOut + i * 4);
         }
     }
 }

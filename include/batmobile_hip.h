@@ -170,8 +170,9 @@ int batteries_sh_tp_scatter_scheduled(const float* edge_vectors, const float* no
  * Replaces the reference interaction block's SH -> batteries::tensor_product ->
  * scatter_add (benchmarks/benchmark_e2e_mace.py:308-349; examples/mace_inference.py:
  * 152-168), without the [E, C_out, 16] messages.  order (optional, [N_dst]) is the
- * order in which destinations are processed (any permutation; a spatial order keeps
- * source rows in L2).  Workspace: per-edge Y and source rows, the per-path sums
+ * order in which destinations are processed: a permutation of 0..N_dst-1 (a spatial
+ * order keeps source rows in L2); entries outside [0, N_dst) are skipped, leaving rows
+ * that no entry names unwritten.  Workspace: per-edge Y and source rows, the per-path sums
  * [N_dst][156][16 ceil(C_in / 16)] and W transposed to [34][C_out][16 ceil(C_in / 16)]. */
 size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges, int C_in,
                                                         int C_out);
