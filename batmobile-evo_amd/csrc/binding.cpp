@@ -158,8 +158,9 @@ torch::Tensor tensor_product_simple(const torch::Tensor& input1, const torch::Te
     torch::Tensor out = torch::empty({N, 16}, f32_like(input1));
     if (N == 0) return out;
     const c10::DeviceGuard guard(input1.device());
-    check_status(batteries_tensor_product_simple_l3(cptr<float>(input1, "input1"),
-                                                    cptr<float>(input2, "input2"),
+    const torch::Tensor x1 = aligned16(input1), x2 = aligned16(input2);
+    check_status(batteries_tensor_product_simple_l3(cptr<float>(x1, "input1"),
+                                                    cptr<float>(x2, "input2"),
                                                     mptr<float>(out, "output"), N,
                                                     current_stream(input1)),
                  "tensor_product_simple");
@@ -221,9 +222,11 @@ std::tuple<torch::Tensor, torch::Tensor> tensor_product_simple_backward(
     torch::Tensor g2 = torch::empty({N, 16}, f32_like(input1));
     if (N == 0) return {g1, g2};
     const c10::DeviceGuard guard(input1.device());
+    const torch::Tensor x1 = aligned16(input1), x2 = aligned16(input2),
+                        go = aligned16(grad_output);
     check_status(batteries_tensor_product_simple_backward_l3(
-                     cptr<float>(input1, "input1"), cptr<float>(input2, "input2"),
-                     cptr<float>(grad_output, "grad_output"), mptr<float>(g1, "grad_input1"),
+                     cptr<float>(x1, "input1"), cptr<float>(x2, "input2"),
+                     cptr<float>(go, "grad_output"), mptr<float>(g1, "grad_input1"),
                      mptr<float>(g2, "grad_input2"), N, current_stream(input1)),
                  "tensor_product_simple_backward");
     return {g1, g2};

@@ -18,9 +18,74 @@ constexpr int kShBlock = 256;
 
 __host__ __device__ constexpr int odd_stride(int k) { return k | 1; }
 
+// A block of `rows` consecutive rows of a row-major [n, K] array (rows * K
+// contiguous floats from g) to LDS rows of stride KS, and back.  A full block
+// (256 rows: 64 K floats) of 16-byte aligned arrays (vec4) moves as float4s,
+// every thread issuing all of its loads before its LDS writes; otherwise (the
+// grid's last block, or unaligned arrays) float by float.
+template <int K, int KS>
+__device__ __forceinline__ void block_to_lds(const float* __restrict__ g, float* s, int rows,
+                                             bool vec4) {
+    const int tid = threadIdx.x;
+    if (vec4 && rows == kShBlock) {
+        constexpr int NQ = kShBlock * K / 4;  // float4s in the block
+        constexpr int PER = (NQ + kShBlock - 1) / kShBlock;
+        const float4* g4 = reinterpret_cast<const float4*>(g);
+        float4 v[PER];
+#pragma unroll
+        for (int it = 0; it < PER; ++it) v[it] = g4[min(tid + kShBlock * it, NQ - 1)];
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int i = tid + kShBlock * it;
+            if (i < NQ) {
+                const float vv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * i + j, r = e / K;
+                    s[r * KS + (e - r * K)] = vv[j];
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < rows * K; i += kShBlock) {
+            const int r = i / K;
+            s[r * KS + (i - r * K)] = g[i];
+        }
+    }
+}
+template <int K, int KS>
+__device__ __forceinline__ void lds_to_block(const float* s, float* __restrict__ g, int rows,
+                                             bool vec4) {
+    const int tid = threadIdx.x;
+    if (vec4 && rows == kShBlock) {
+        constexpr int NQ = kShBlock * K / 4;
+        constexpr int PER = (NQ + kShBlock - 1) / kShBlock;
+        float4* g4 = reinterpret_cast<float4*>(g);
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int i = tid + kShBlock * it;
+            if (i < NQ) {
+                float vv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * i + j, r = e / K;
+                    vv[j] = s[r * KS + (e - r * K)];
+                }
+                g4[i] = make_float4(vv[0], vv[1], vv[2], vv[3]);
+            }
+        }
+    } else {
+        for (int i = tid; i < rows * K; i += kShBlock) {
+            const int r = i / K;
+            g[i] = s[r * KS + (i - r * K)];
+        }
+    }
+}
+
 template <int L, bool NORM>
 __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(const float* __restrict__ v,
-                                                                float* __restrict__ Y, int64_t n) {
+                                                                float* __restrict__ Y, int64_t n,
+                                                                bool vec4) {
     constexpr int K = sh_dim(L);
     constexpr int KS = odd_stride(K);
     __shared__ float sv[kShBlock * 3];
@@ -28,7 +93,7 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(const float* __res
     const int64_t base = (int64_t)blockIdx.x * kShBlock;
     const int rows = (int)min<int64_t>(kShBlock, n - base);
     const int tid = threadIdx.x;
-    for (int i = tid; i < rows * 3; i += kShBlock) sv[i] = v[base * 3 + i];
+    block_to_lds<3, 3>(v + base * 3, sv, rows, vec4);
     __syncthreads();
     if (tid < rows) {
         float x = sv[tid * 3 + 0], y = sv[tid * 3 + 1], z = sv[tid * 3 + 2];
@@ -39,11 +104,7 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(const float* __res
         for (int k = 0; k < K; ++k) sy[tid * KS + k] = out[k];
     }
     __syncthreads();
-    float* dst = Y + base * K;
-    for (int i = tid; i < rows * K; i += kShBlock) {
-        const int r = i / K;
-        dst[i] = sy[r * KS + (i - r * K)];
-    }
+    lds_to_block<K, KS>(sy, Y + base * K, rows, vec4);
 }
 
 // grad_xyz = sum_k g_k dY_k/d(x,y,z).  With NORM the input is the raw vector v,
@@ -52,7 +113,8 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(const float* __res
 template <int L, bool NORM>
 __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(const float* __restrict__ v,
                                                                  const float* __restrict__ gY,
-                                                                 float* __restrict__ gv, int64_t n) {
+                                                                 float* __restrict__ gv, int64_t n,
+                                                                 bool vec4) {
     constexpr int K = sh_dim(L);
     constexpr int KS = odd_stride(K);
     __shared__ float sv[kShBlock * 3];
@@ -60,12 +122,8 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(const float* __re
     const int64_t base = (int64_t)blockIdx.x * kShBlock;
     const int rows = (int)min<int64_t>(kShBlock, n - base);
     const int tid = threadIdx.x;
-    for (int i = tid; i < rows * 3; i += kShBlock) sv[i] = v[base * 3 + i];
-    const float* src = gY + base * K;
-    for (int i = tid; i < rows * K; i += kShBlock) {
-        const int r = i / K;
-        sg[r * KS + (i - r * K)] = src[i];
-    }
+    block_to_lds<3, 3>(v + base * 3, sv, rows, vec4);
+    block_to_lds<K, KS>(gY + base * K, sg, rows, vec4);
     __syncthreads();
     float res[3] = {0.0f, 0.0f, 0.0f};
     if (tid < rows) {
@@ -96,20 +154,23 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(const float* __re
         sv[tid * 3 + 2] = res[2];
     }
     __syncthreads();
-    for (int i = tid; i < rows * 3; i += kShBlock) gv[base * 3 + i] = sv[i];
+    lds_to_block<3, 3>(sv, gv + base * 3, rows, vec4);
 }
+
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <bool NORM>
 static int launch_sh_forward(const float* v, float* Y, int64_t n, int L, hipStream_t s) {
     const dim3 grid((unsigned)ceil_div(n, kShBlock));
+    const bool vec4 = al16(v) && al16(Y);
     switch (L) {
-        case 0: sh_forward_kernel<0, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
-        case 1: sh_forward_kernel<1, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
-        case 2: sh_forward_kernel<2, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
-        case 3: sh_forward_kernel<3, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
-        case 4: sh_forward_kernel<4, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
-        case 5: sh_forward_kernel<5, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
-        case 6: sh_forward_kernel<6, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n); break;
+        case 0: sh_forward_kernel<0, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+        case 1: sh_forward_kernel<1, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+        case 2: sh_forward_kernel<2, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+        case 3: sh_forward_kernel<3, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+        case 4: sh_forward_kernel<4, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+        case 5: sh_forward_kernel<5, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+        case 6: sh_forward_kernel<6, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
         default: return BM_ERR_ARG;
     }
     return (int)hipGetLastError();
@@ -119,14 +180,15 @@ template <bool NORM>
 static int launch_sh_backward(const float* v, const float* g, float* gv, int64_t n, int L,
                               hipStream_t s) {
     const dim3 grid((unsigned)ceil_div(n, kShBlock));
+    const bool vec4 = al16(v) && al16(g) && al16(gv);
     switch (L) {
-        case 0: sh_backward_kernel<0, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
-        case 1: sh_backward_kernel<1, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
-        case 2: sh_backward_kernel<2, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
-        case 3: sh_backward_kernel<3, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
-        case 4: sh_backward_kernel<4, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
-        case 5: sh_backward_kernel<5, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
-        case 6: sh_backward_kernel<6, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n); break;
+        case 0: sh_backward_kernel<0, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
+        case 1: sh_backward_kernel<1, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
+        case 2: sh_backward_kernel<2, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
+        case 3: sh_backward_kernel<3, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
+        case 4: sh_backward_kernel<4, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
+        case 5: sh_backward_kernel<5, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
+        case 6: sh_backward_kernel<6, NORM><<<grid, kShBlock, 0, s>>>(v, g, gv, n, vec4); break;
         default: return BM_ERR_ARG;
     }
     return (int)hipGetLastError();

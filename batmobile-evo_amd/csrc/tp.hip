@@ -14,17 +14,87 @@ constexpr int kTpBlock = 256;
 constexpr int kRowStride = 17;  // odd LDS stride for 16-float rows
 
 // ---------------------------------------------------------------------------
-// simple product: one thread per row, rows staged through LDS
+// simple product: one thread per row, rows staged through LDS.  A block's rows
+// are contiguous, so each thread issues its four 16-byte loads per input before
+// any LDS write (item t + 256 k of the block: row item / 4, quad item % 4), and
+// writes its results back as 16-byte stores of the same items.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void stage_rows16(float* s, const float* __restrict__ g, int64_t base,
-                                             int rows) {
-    const float* src = g + base * 16;
-    for (int i = threadIdx.x; i < rows * 16; i += kTpBlock) s[(i >> 4) * kRowStride + (i & 15)] = src[i];
+__device__ __forceinline__ void load_rows16(const float* __restrict__ g, int64_t base, int rows,
+                                            float4 (&v)[4]) {
+    const float4* g4 = reinterpret_cast<const float4*>(g + base * 16);
+    const int nq = rows * 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = g4[min((int)threadIdx.x + kTpBlock * k, nq - 1)];
 }
-__device__ __forceinline__ void unstage_rows16(const float* s, float* __restrict__ g, int64_t base,
-                                               int rows) {
-    float* dst = g + base * 16;
-    for (int i = threadIdx.x; i < rows * 16; i += kTpBlock) dst[i] = s[(i >> 4) * kRowStride + (i & 15)];
+__device__ __forceinline__ void put_rows16(float* s, int rows, const float4 (&v)[4]) {
+    const int nq = rows * 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + kTpBlock * k;
+        if (i < nq) {
+            float* d = s + (i >> 2) * kRowStride + (i & 3) * 4;
+            d[0] = v[k].x;
+            d[1] = v[k].y;
+            d[2] = v[k].z;
+            d[3] = v[k].w;
+        }
+    }
+}
+__device__ __forceinline__ void store_rows16(const float* s, float* __restrict__ g, int64_t base,
+                                             int rows) {
+    float4* g4 = reinterpret_cast<float4*>(g + base * 16);
+    const int nq = rows * 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = threadIdx.x + kTpBlock * k;
+        if (i < nq) {
+            const float* d = s + (i >> 2) * kRowStride + (i & 3) * 4;
+            g4[i] = make_float4(d[0], d[1], d[2], d[3]);
+        }
+    }
+}
+
+// out = M(y) x with M[o][a] = sum_b c y[b] built row by row (611 + 256 VALU
+// operations per row, against 2 x 611 for the term-by-term form)
+__device__ __forceinline__ void tp_simple_rows(const float* x, const float* y, float* out) {
+    static_for<16>([&](auto oo) {
+        constexpr int O = decltype(oo)::value;
+        float m[16];
+        edge_operator_row<O>(y, m);
+        float acc = m[0] * x[0];
+#pragma unroll
+        for (int a = 1; a < 16; ++a) acc = fmaf(m[a], x[a], acc);
+        out[O] = acc;
+    });
+}
+
+// Adjoint, row o of the operators at a time:
+//   gx[a] = sum_o M[o][a] g[o],  M[o][a] = sum_b c y[b]
+//   gy[b] = sum_o N[o][b] g[o],  N[o][b] = sum_a c x[a]
+// (2 x (611 + 256) VALU operations per row, with 32 accumulators live)
+__device__ __forceinline__ void tp_simple_backward_rows(const float* x, const float* y,
+                                                        const float* g, float* gx, float* gy) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        gx[k] = 0.0f;
+        gy[k] = 0.0f;
+    }
+    static_for<16>([&](auto oo) {
+        constexpr int O = decltype(oo)::value;
+        float m[16], nb[16];
+        edge_operator_row<O>(y, m);
+#pragma unroll
+        for (int b = 0; b < 16; ++b) nb[b] = 0.0f;
+        static_for<kNumEntries>([&](auto kk) {
+            constexpr CGEntry e = kCG[decltype(kk)::value];
+            if constexpr (e.o == O) nb[e.b] = fmaf(e.c, x[e.a], nb[e.b]);
+        });
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            gx[k] = fmaf(m[k], g[O], gx[k]);
+            gy[k] = fmaf(nb[k], g[O], gy[k]);
+        }
+    });
 }
 
 __global__ __launch_bounds__(kTpBlock) void tp_simple_kernel(const float* __restrict__ x,
@@ -34,8 +104,11 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_kernel(const float* __rest
     __shared__ float sy[kTpBlock * kRowStride];
     const int64_t base = (int64_t)blockIdx.x * kTpBlock;
     const int rows = (int)min<int64_t>(kTpBlock, n - base);
-    stage_rows16(sx, x, base, rows);
-    stage_rows16(sy, y, base, rows);
+    float4 vx[4], vy[4];
+    load_rows16(x, base, rows, vx);
+    load_rows16(y, base, rows, vy);
+    put_rows16(sx, rows, vx);
+    put_rows16(sy, rows, vy);
     __syncthreads();
     const int t = threadIdx.x;
     if (t < rows) {
@@ -45,12 +118,12 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_kernel(const float* __rest
             a[k] = sx[t * kRowStride + k];
             b[k] = sy[t * kRowStride + k];
         }
-        tp_simple(a, b, o);
+        tp_simple_rows(a, b, o);
 #pragma unroll
         for (int k = 0; k < 16; ++k) sx[t * kRowStride + k] = o[k];
     }
     __syncthreads();
-    unstage_rows16(sx, out, base, rows);
+    store_rows16(sx, out, base, rows);
 }
 
 __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
@@ -61,9 +134,13 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
     __shared__ float sg[kTpBlock * kRowStride];
     const int64_t base = (int64_t)blockIdx.x * kTpBlock;
     const int rows = (int)min<int64_t>(kTpBlock, n - base);
-    stage_rows16(sx, x, base, rows);
-    stage_rows16(sy, y, base, rows);
-    stage_rows16(sg, g, base, rows);
+    float4 vx[4], vy[4], vg[4];
+    load_rows16(x, base, rows, vx);
+    load_rows16(y, base, rows, vy);
+    load_rows16(g, base, rows, vg);
+    put_rows16(sx, rows, vx);
+    put_rows16(sy, rows, vy);
+    put_rows16(sg, rows, vg);
     __syncthreads();
     const int t = threadIdx.x;
     if (t < rows) {
@@ -74,7 +151,7 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
             b[k] = sy[t * kRowStride + k];
             c[k] = sg[t * kRowStride + k];
         }
-        tp_simple_backward(a, b, c, ga, gb);
+        tp_simple_backward_rows(a, b, c, ga, gb);
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             sx[t * kRowStride + k] = ga[k];
@@ -82,8 +159,8 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
         }
     }
     __syncthreads();
-    unstage_rows16(sx, gx, base, rows);
-    unstage_rows16(sy, gy, base, rows);
+    store_rows16(sx, gx, base, rows);
+    store_rows16(sy, gy, base, rows);
 }
 
 // ---------------------------------------------------------------------------
@@ -867,10 +944,13 @@ extern "C" void batteries_get_path_info_l3(int* path_info) {
         for (int k = 0; k < 3; ++k) path_info[p * 3 + k] = kPathL[p][k];
 }
 
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 extern "C" int batteries_tensor_product_simple_l3(const float* input1, const float* input2,
                                                   float* output, int64_t N, hipStream_t stream) {
     if (N < 0) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
+    if (!aligned16(input1) || !aligned16(input2) || !aligned16(output)) return BM_ERR_ARG;
     tp_simple_kernel<<<(unsigned)ceil_div(N, kTpBlock), kTpBlock, 0, stream>>>(input1, input2,
                                                                               output, N);
     return (int)hipGetLastError();
@@ -883,6 +963,9 @@ extern "C" int batteries_tensor_product_simple_backward_l3(const float* input1,
                                                            int64_t N, hipStream_t stream) {
     if (N < 0) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
+    if (!aligned16(input1) || !aligned16(input2) || !aligned16(grad_output) ||
+        !aligned16(grad_input1) || !aligned16(grad_input2))
+        return BM_ERR_ARG;
     tp_simple_backward_kernel<<<(unsigned)ceil_div(N, kTpBlock), kTpBlock, 0, stream>>>(
         input1, input2, grad_output, grad_input1, grad_input2, N);
     return (int)hipGetLastError();

@@ -144,6 +144,20 @@ def other_configs(torch, bm, dev):
     res["cfg0_tp_simple_ms"] = round(t, 5)
     res["cfg0_tp_simple_GBs"] = round(E1 * 192 / (t * 1e-3) / 1e9, 1)
 
+    # bandwidth evidence at E = 2e6 (configs[0]'s size is launch-bound)
+    E2 = 2_000_000
+    v2 = torch.randn(E2, 3, generator=g)
+    v2 = (v2 / v2.norm(dim=1, keepdim=True)).to(dev)
+    x2e = torch.randn(E2, 16, generator=g).to(dev)
+    y2e = bm.spherical_harmonics(v2, 3)
+    t = event_ms(torch, lambda: bm.spherical_harmonics(v2, 3), 50)
+    res["sweep_sh_l3_E2e6_ms"] = round(t, 5)
+    res["sweep_sh_l3_E2e6_hbm_frac"] = round(E2 * 76 / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    t = event_ms(torch, lambda: bm.tensor_product_simple(x2e, y2e), 50)
+    res["sweep_tp_simple_E2e6_ms"] = round(t, 5)
+    res["sweep_tp_simple_E2e6_hbm_frac"] = round(E2 * 192 / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    del v2, x2e, y2e
+
     def weighted_inputs(seed, n, ci, co):
         g = torch.Generator().manual_seed(seed)
         x = torch.randn(n, ci, 16, generator=g)

@@ -73,13 +73,13 @@ int batteries_get_num_paths_l3(void);
  * src/tensor_product/tensor_product.cu:207-214. */
 void batteries_get_path_info_l3(int* path_info);
 
-/* output[N,16] = sum c * input1[N,16]_a * input2[N,16]_b.  Replaces
- * batteries::tensor_product_simple_l3, src/tensor_product/tensor_product.cu:159-176. */
+/* output[N,16] = sum c * input1[N,16]_a * input2[N,16]_b (all three 16-byte aligned).
+ * Replaces batteries::tensor_product_simple_l3, src/tensor_product/tensor_product.cu:159-176. */
 int batteries_tensor_product_simple_l3(const float* input1, const float* input2, float* output,
                                        int64_t N, hipStream_t stream);
 
-/* (grad_input1, grad_input2)[N,16].  Replaces batteries::tensor_product_simple_backward_l3,
- * src/tensor_product/tensor_product_backward.cu:1007-1026. */
+/* (grad_input1, grad_input2)[N,16] (all five arrays 16-byte aligned).  Replaces
+ * batteries::tensor_product_simple_backward_l3, src/tensor_product/tensor_product_backward.cu:1007-1026. */
 int batteries_tensor_product_simple_backward_l3(const float* input1, const float* input2,
                                                 const float* grad_output, float* grad_input1,
                                                 float* grad_input2, int64_t N, hipStream_t stream);
