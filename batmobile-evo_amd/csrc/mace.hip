@@ -604,7 +604,9 @@ struct MaceWs {
 
 static size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static MaceWs mace_ws(void* base, int64_t E, int C, bool backward) {
+// external: the per-edge weights of all edges live in a caller buffer
+// (batteries_mace_edge_weight_rows rows of 34 C), so the workspace holds no R chunk.
+static MaceWs mace_ws(void* base, int64_t E, int C, bool backward, bool external = false) {
     const int64_t chunk = mace_chunk(E, C);
     const int64_t eb = std::min<int64_t>(std::max<int64_t>(E, 1), chunk);
     char* p = static_cast<char*>(base);
@@ -619,7 +621,7 @@ static MaceWs mace_ws(void* base, int64_t E, int C, bool backward) {
     w.rows = reinterpret_cast<int64_t*>(
         take(sizeof(int64_t) * 2 * (size_t)ceil_div(std::max<int64_t>(E, 1), chunk)));
     w.h = take(sizeof(float) * (size_t)eb * kHidden);
-    w.R = take(sizeof(float) * (size_t)eb * C * kNumPaths);
+    w.R = external ? nullptr : take(sizeof(float) * (size_t)eb * C * kNumPaths);
     if (backward) {
         w.gR = take(sizeof(float) * (size_t)eb * C * kNumPaths);
         w.gh = take(sizeof(float) * (size_t)eb * kHidden);
@@ -698,9 +700,18 @@ extern "C" int batteries_gemm_f32(const float* A, const float* B, float* C, int6
     return gemm_launch(A, B, C, M, N, K, trans_b != 0, stream);
 }
 
-extern "C" size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward) {
+extern "C" size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward,
+                                                 int external_weights) {
     if (N_edges < 0 || C <= 0) return 0;
-    return mace_ws(nullptr, N_edges, C, backward != 0).bytes;
+    return mace_ws(nullptr, N_edges, C, backward != 0, external_weights != 0).bytes;
+}
+
+// Rows of a caller buffer for the per-edge weights of all edges: whole chunks
+// (every chunk's GEMM writes a full chunk of rows; rows past N_edges are padding).
+extern "C" int64_t batteries_mace_edge_weight_rows(int64_t N_edges, int C) {
+    if (N_edges <= 0 || C <= 0) return 0;
+    const int64_t chunk = mace_chunk(N_edges, C);
+    return ceil_div(N_edges, chunk) * chunk;
 }
 
 extern "C" int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src,
@@ -734,11 +745,12 @@ extern "C" int batteries_mace_forward(const float* positions, const float* box,
                                       const float* node_features, const float* w1,
                                       const float* b1, const float* w2, const int64_t* src,
                                       const int64_t* dst, const int64_t* row_ptr, float* out,
-                                      int64_t N, int64_t N_edges, int C, float cutoff,
-                                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                      float* edge_weights, int64_t N, int64_t N_edges, int C,
+                                      float cutoff, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
     if (!mace_args_ok(box, N, N_edges, C, cutoff)) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
-    const MaceWs w = mace_ws(workspace, N_edges, C, false);
+    const MaceWs w = mace_ws(workspace, N_edges, C, false, edge_weights != nullptr);
     if (!workspace || workspace_bytes < w.bytes) return BM_ERR_WORKSPACE;
     const int64_t count = N * (int64_t)C * 16;
     mace_fill_zero_kernel<<<(unsigned)ceil_div(count, 256), 256, 0, stream>>>(out, count);
@@ -753,13 +765,15 @@ extern "C" int batteries_mace_forward(const float* positions, const float* box,
         row_ptr, N, N_edges, chunk, n_chunks, w.rows);
     for (int64_t e0 = 0; e0 < N_edges; e0 += chunk) {
         const int64_t e1 = std::min(N_edges, e0 + chunk), eb = e1 - e0;
+        // this chunk's R: the workspace chunk, or rows e0.. of the caller's buffer
+        float* R = edge_weights ? edge_weights + e0 * (int64_t)C * kNumPaths : w.R;
         mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
                                                                              e1, cutoff);
-        int rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
+        int rc = blas_gemm(w.h, w2, R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
                            stream);
         if (rc != BM_OK) return rc;
         dim3 grid(mace_row_blocks(chunk), (unsigned)ceil_div(C, nthr));
-        mace_tp_scatter_kernel<<<grid, nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, w.R,
+        mace_tp_scatter_kernel<<<grid, nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, R,
                                                           w.rows + 2 * (e0 / chunk), e0, e1,
                                                           out, C);
     }
@@ -770,13 +784,13 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
                                        const float* node_features, const float* w1,
                                        const float* b1, const float* w2, const int64_t* src,
                                        const int64_t* dst, const int64_t* row_ptr,
-                                       const int64_t* rev, const float* grad_out, float* grad_pos,
-                                       int64_t N, int64_t N_edges, int C, float cutoff,
-                                       void* workspace, size_t workspace_bytes,
-                                       hipStream_t stream) {
+                                       const int64_t* rev, const float* grad_out,
+                                       const float* edge_weights, float* grad_pos, int64_t N,
+                                       int64_t N_edges, int C, float cutoff, void* workspace,
+                                       size_t workspace_bytes, hipStream_t stream) {
     if (!mace_args_ok(box, N, N_edges, C, cutoff)) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
-    const MaceWs w = mace_ws(workspace, N_edges, C, true);
+    const MaceWs w = mace_ws(workspace, N_edges, C, true, edge_weights != nullptr);
     if (!workspace || workspace_bytes < w.bytes) return BM_ERR_WORKSPACE;
     if (N_edges == 0) {
         mace_fill_zero_kernel<<<(unsigned)ceil_div(N * 3, 256), 256, 0, stream>>>(grad_pos, N * 3);
@@ -792,13 +806,18 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
         row_ptr, N, N_edges, chunk, n_chunks, w.rows);
     for (int64_t e0 = 0; e0 < N_edges; e0 += chunk) {
         const int64_t e1 = std::min(N_edges, e0 + chunk), eb = e1 - e0;
-        mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
-                                                                             e1, cutoff);
-        int rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
-                           stream);
-        if (rc != BM_OK) return rc;
+        // R: the forward's saved weights (rows e0..), or recomputed into the workspace
+        const float* R = edge_weights ? edge_weights + e0 * (int64_t)C * kNumPaths : w.R;
+        int rc = BM_OK;
+        if (!edge_weights) {
+            mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h,
+                                                                                 e0, e1, cutoff);
+            rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden,
+                           false, stream);
+            if (rc != BM_OK) return rc;
+        }
         mace_tp_backward_kernel<<<mace_row_blocks(chunk), nthr, 0, stream>>>(
-            w.vec, node_features, src, row_ptr, w.R, grad_out, w.rows + 2 * (e0 / chunk), e0,
+            w.vec, node_features, src, row_ptr, R, grad_out, w.rows + 2 * (e0 / chunk), e0,
             e1, w.gR, w.gY, C);
         rc = blas_gemm(w.gR, w2, w.gh, gemm_rows(N_edges, eb, chunk), kHidden, C * kNumPaths, true, stream);
         if (rc != BM_OK) return rc;

@@ -35,9 +35,17 @@ class MaceLayerFunction(torch.autograd.Function):
     def forward(ctx, positions, node_features, w1, b1, w2, graph, cutoff):
         pos = positions.detach().contiguous()
         x = node_features.detach().contiguous()
+        # the per-edge weights R (34 C floats per edge) are kept for the backward when
+        # positions need a gradient (the backward then skips the MLP and its GEMM)
+        ew = None
+        if ctx.needs_input_grad[0]:
+            e, c = graph.src.numel(), x.shape[1]
+            ew = torch.empty(_batmobile.mace_edge_weight_rows(e, c), NUM_PATHS * c,
+                             dtype=torch.float32, device=x.device)
         out = _batmobile.mace_forward(pos, graph.cell, x, w1, b1, w2, graph.src, graph.dst,
-                                      graph.row_ptr, float(cutoff))
+                                      graph.row_ptr, float(cutoff), ew)
         ctx.save_for_backward(pos, x, w1, b1, w2)
+        ctx.edge_weights = ew
         ctx.graph = graph
         ctx.cutoff = float(cutoff)
         return out
@@ -53,7 +61,9 @@ class MaceLayerFunction(torch.autograd.Function):
             g = ctx.graph
             grad_pos = _batmobile.mace_backward(pos, g.cell, x, w1, b1, w2, g.src, g.dst,
                                                 g.row_ptr, g.reverse_edges(),
-                                                grad_out.contiguous(), ctx.cutoff)
+                                                grad_out.contiguous(), ctx.cutoff,
+                                                ctx.edge_weights)
+        ctx.edge_weights = None
         return grad_pos, None, None, None, None, None, None
 
 

@@ -211,7 +211,8 @@ def mace_config4(torch, bm, dev, reps=3):
     (uniform periodic box at ~30 neighbours within 5 A, seed 4): GPU neighbor list +
     graph, forward, backward w.r.t. positions.  Flop model per edge: radial MLP
     2 (8 64 + 64 34 C) and channel-wise CG product (1222 + 312) C forward; backward
-    recomputes the MLP and adds its transpose GEMM and twice the CG work."""
+    reads the per-edge weights the forward kept and runs the MLP's transpose GEMM and
+    twice the CG work."""
     n, c = 50000, 128
     g = torch.Generator().manual_seed(4)
     L = (n / RHO) ** (1.0 / 3.0)
@@ -238,8 +239,10 @@ def mace_config4(torch, bm, dev, reps=3):
         bwd.append(t2 - t1)
         p.grad = None
     e = graph.num_edges
+    # the forward keeps the per-edge weights for the backward (positions require grad),
+    # so the backward runs the MLP's transpose GEMM only
     f_fwd = e * (2 * (8 * 64 + 64 * 34 * c) + (1222 + 312) * c)
-    f_bwd = e * (4 * (8 * 64 + 64 * 34 * c) + 2 * (1222 + 312) * c)
+    f_bwd = e * (2 * (8 * 64 + 64 * 34 * c) + 2 * (1222 + 312) * c)
     t_f, t_b = min(fwd[1:]), min(bwd[1:])
     return {
         "cfg4_mace_N": n, "cfg4_mace_C": c, "cfg4_mace_E": e,

@@ -282,23 +282,31 @@ size_t neighbor_list_estimate_memory(int64_t N, float density, float cutoff);
 /* C[M,N] = A[M,K] B on MFMA (fp32); B is [K,N] row-major, or [N,K] row-major when trans_b. */
 int batteries_gemm_f32(const float* A, const float* B, float* C, int64_t M, int N, int K,
                        int trans_b, hipStream_t stream);
-size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward);
+/* Workspace of one forward (backward = 0) or backward (backward = 1) pass; with
+ * external_weights the per-edge weights live in the caller's edge_weights buffer
+ * (batteries_mace_edge_weight_rows(N_edges, C) rows of 34 C floats) instead of a
+ * per-chunk workspace buffer. */
+size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward, int external_weights);
+int64_t batteries_mace_edge_weight_rows(int64_t N_edges, int C);
 /* rev[e] = index of the edge with source and destination swapped (-1 if absent);
  * *d_missing (device int) counts the absent ones. */
 int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src, int64_t* rev,
                                  int* d_missing, int64_t N, int64_t N_edges, hipStream_t stream);
+/* edge_weights (nullable): when given, R of every edge is written there (row e,
+ * path-major [34][C]) and kept for batteries_mace_backward. */
 int batteries_mace_forward(const float* positions, const float* box, const float* node_features,
                            const float* w1, const float* b1, const float* w2, const int64_t* src,
-                           const int64_t* dst, const int64_t* row_ptr, float* out, int64_t N,
-                           int64_t N_edges, int C, float cutoff, void* workspace,
-                           size_t workspace_bytes, hipStream_t stream);
-/* grad_pos[N,3] = d <out, grad_out> / d positions (rev from batteries_mace_reverse_edges). */
+                           const int64_t* dst, const int64_t* row_ptr, float* out,
+                           float* edge_weights, int64_t N, int64_t N_edges, int C, float cutoff,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* grad_pos[N,3] = d <out, grad_out> / d positions (rev from batteries_mace_reverse_edges).
+ * edge_weights (nullable): the forward's saved R; when NULL, R is recomputed per chunk. */
 int batteries_mace_backward(const float* positions, const float* box, const float* node_features,
                             const float* w1, const float* b1, const float* w2, const int64_t* src,
                             const int64_t* dst, const int64_t* row_ptr, const int64_t* rev,
-                            const float* grad_out, float* grad_pos, int64_t N, int64_t N_edges,
-                            int C, float cutoff, void* workspace, size_t workspace_bytes,
-                            hipStream_t stream);
+                            const float* grad_out, const float* edge_weights, float* grad_pos,
+                            int64_t N, int64_t N_edges, int C, float cutoff, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Self test (no reference counterpart): D[16,16] = A[16,4] B[4,16] through one

@@ -87,3 +87,25 @@ def test_mace_layer_is_deterministic(bm, dev):
         outs.append(o.detach().cpu())
         grads.append(p.grad.cpu())
     assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
+
+
+@pytest.mark.parametrize("n,c", [(500, 8), (9500, 2)])
+def test_mace_saved_edge_weights_equal_recomputed(bm, dev, n, c):
+    """The backward reading the forward's saved per-edge weights equals the backward
+    that recomputes them chunk by chunk (same GEMMs on the same inputs)."""
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, n, c, 51)
+    p, xd, god = pos.to(dev), x.to(dev), go.to(dev)
+    args = (p, cell, xd, layer.W1, layer.b1, layer.W2, graph.src, graph.dst, graph.row_ptr)
+    e = graph.num_edges
+    rows = bm.mace_edge_weight_rows(e, c)
+    assert rows >= e
+    ew = torch.empty(rows, 34 * c, device=dev)
+    out_saved = bm.mace_forward(*args, 5.0, ew)
+    out_plain = bm.mace_forward(*args, 5.0)
+    assert torch.equal(out_saved, out_plain)
+    rev = graph.reverse_edges()
+    g_saved = bm.mace_backward(*args, rev, god, 5.0, ew)
+    g_plain = bm.mace_backward(*args, rev, god, 5.0)
+    assert torch.equal(g_saved, g_plain)
+    with pytest.raises(RuntimeError, match="edge_weights"):
+        bm.mace_forward(*args, 5.0, torch.empty(rows - 1, 34 * c, device=dev))
