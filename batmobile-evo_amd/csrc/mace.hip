@@ -283,14 +283,164 @@ __global__ void mace_chunk_rows_kernel(const int64_t* __restrict__ row_ptr, int6
     rows[2 * i + 1] = row_of(e1 - 1) + 1;
 }
 
-// T_p (2 l_out + 1 values) of path p from Y_e and the source row xs.
-template <int P, int LO>
-__device__ __forceinline__ void mace_path_products(const float* Y, const float* xs, float* tq) {
+// One past the last path of the (l1, l2) block that starts at path p0 (the path
+// order is l1 outer, l2, l_out inner, so a block's paths are consecutive).
+constexpr int block_end(int p0) {
+    int p = p0;
+    while (p < kNumPaths && kPathL[p][0] == kPathL[p0][0] && kPathL[p][1] == kPathL[p0][1]) ++p;
+    return p;
+}
+constexpr int path_slot(int p) { return p < kNumPaths ? kPathSlot[p] : kNumSlots; }
+
+// Entry e of path p is the first of its path to write its output slot (when the
+// entries are taken component a ascending, then in table order): the slot's
+// accumulator starts from that term instead of from zero.
+constexpr bool first_slot_write(int p, int e) {
+    const CGEntry& x = kCG[kPathEntry[p] + e];
+    for (int i = kPathEntry[p]; i < kPathEntry[p + 1]; ++i) {
+        const CGEntry& y = kCG[i];
+        if (y.q == x.q && (y.a < x.a || (y.a == x.a && i < kPathEntry[p] + e))) return false;
+    }
+    return true;
+}
+// The same for the input-2 component b (the backward's per-path sums over b).
+constexpr bool first_b_write(int p, int e) {
+    const CGEntry& x = kCG[kPathEntry[p] + e];
+    for (int i = kPathEntry[p]; i < kPathEntry[p + 1]; ++i) {
+        const CGEntry& y = kCG[i];
+        if (y.b == x.b && (y.a < x.a || (y.a == x.a && i < kPathEntry[p] + e))) return false;
+    }
+    return true;
+}
+// every output slot and every component b of every path has an entry (so each
+// accumulator is written before it is read)
+constexpr bool every_slot_and_b_written() {
+    for (int p = 0; p < kNumPaths; ++p) {
+        const int lo = kPathL[p][2], l2 = kPathL[p][1];
+        for (int o = lo * lo; o < (lo + 1) * (lo + 1); ++o) {
+            bool f = false;
+            for (int i = kPathEntry[p]; i < kPathEntry[p + 1]; ++i) f = f || kCG[i].o == o;
+            if (!f) return false;
+        }
+        for (int b = l2 * l2; b < (l2 + 1) * (l2 + 1); ++b) {
+            bool f = false;
+            for (int i = kPathEntry[p]; i < kPathEntry[p + 1]; ++i) f = f || kCG[i].b == b;
+            if (!f) return false;
+        }
+    }
+    return true;
+}
+static_assert(every_slot_and_b_written(), "a path output or input-2 component without entries");
+
+// x * c with c a compile-time coefficient (no multiply for c = 1)
+template <int P, int E>
+__device__ __forceinline__ float cg_times(float x) {
+    constexpr float c = kCG[kPathEntry[P] + E].c;
+    if constexpr (c == 1.0f) return x;
+    else return c * x;
+}
+
+// f(P0, P1) for every (l1, l2) block [P0, P1) of paths, in path order.
+template <int P0, typename F>
+__device__ __forceinline__ void for_blocks(F&& f) {
+    if constexpr (P0 < kNumPaths) {
+        constexpr int P1 = block_end(P0);
+        f(std::integral_constant<int, P0>{}, std::integral_constant<int, P1>{});
+        for_blocks<P1>(f);
+    }
+}
+
+// T_p[o] = sum over the entries (a, b, o) of p of c x[a] Y[b], for the paths of
+// the (l1, l2) block [P0, P1), with each product x[a] Y[b] formed once for the
+// block (256 products per edge and channel over all blocks, against one
+// product c Y[b] per distinct (c, b) when the paths are taken one by one).
+// consume(p, tq) receives T_p (2 l_out + 1 values) of every path of the block.
+template <int P0, int P1, typename F>
+__device__ __forceinline__ void block_products(const float* Y, const float* xs, F&& consume) {
+    constexpr int L1 = kPathL[P0][0], L2 = kPathL[P0][1];
+    constexpr int S0 = kPathSlot[P0], NT = path_slot(P1) - S0;
+    float t[NT];  // each written first by its slot's first term
+    static_for<2 * L1 + 1>([&](auto ia) {
+        constexpr int a = L1 * L1 + decltype(ia)::value;
+        float xy[2 * L2 + 1];
 #pragma unroll
-    for (int q = 0; q < 2 * LO + 1; ++q) tq[q] = 0.0f;
-    static_for<kPathEntry[P + 1] - kPathEntry[P]>([&](auto ee) {
-        constexpr CGEntry en = kCG[kPathEntry[P] + decltype(ee)::value];
-        tq[en.o - LO * LO] = fmaf(en.c * Y[en.b], xs[en.a], tq[en.o - LO * LO]);
+        for (int i = 0; i < 2 * L2 + 1; ++i) xy[i] = xs[a] * Y[L2 * L2 + i];
+        static_for<P1 - P0>([&](auto pp) {
+            constexpr int p = P0 + decltype(pp)::value;
+            static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                constexpr int e = decltype(ee)::value;
+                constexpr CGEntry en = kCG[kPathEntry[p] + e];
+                if constexpr (en.a == a) {
+                    if constexpr (first_slot_write(p, e))
+                        t[en.q - S0] = cg_times<p, e>(xy[en.b - L2 * L2]);
+                    else
+                        t[en.q - S0] = fmaf(en.c, xy[en.b - L2 * L2], t[en.q - S0]);
+                }
+            });
+        });
+    });
+    static_for<P1 - P0>([&](auto pp) {
+        constexpr int p = P0 + decltype(pp)::value;
+        consume(std::integral_constant<int, p>{}, t + (kPathSlot[p] - S0));
+    });
+}
+
+// m[o] += sum_p R_p T_p[o] over all paths (the forward's per-edge message).
+__device__ __forceinline__ void mace_message(const float* Y, const float* xs, const float* rr,
+                                             float* m) {
+    for_blocks<0>([&](auto b0, auto b1) {
+        block_products<decltype(b0)::value, decltype(b1)::value>(Y, xs, [&](auto pp, const float* tq) {
+            constexpr int p = decltype(pp)::value;
+            constexpr int lo = kPathL[p][2];
+#pragma unroll
+            for (int q = 0; q < 2 * lo + 1; ++q) m[lo * lo + q] = fmaf(rr[p], tq[q], m[lo * lo + q]);
+        });
+    });
+}
+
+// gy[b] = sum over the entries (a, b, o) of every path p of c x[a] R_p g[o],
+// by (l1, l_out) blocks: each product x[a] g[o] is formed once (256 per edge
+// and channel), the block's per-path sums U_p[b] = sum c x[a] g[o] (one path
+// per l2 within the block, so U is indexed by b) are scaled by R_p once.
+__device__ __forceinline__ void mace_grad_y(const float* xs, const float* g, const float* rr,
+                                            float* gy) {
+    static_for<4>([&](auto l1c) {
+        constexpr int L1 = decltype(l1c)::value;
+        static_for<4>([&](auto loc) {
+            constexpr int LO = decltype(loc)::value;
+            float U[16];  // U[b] written first by its first term (b of the block's paths only)
+            static_for<2 * L1 + 1>([&](auto ia) {
+                constexpr int a = L1 * L1 + decltype(ia)::value;
+                float xg[2 * LO + 1];
+#pragma unroll
+                for (int i = 0; i < 2 * LO + 1; ++i) xg[i] = xs[a] * g[LO * LO + i];
+                static_for<kNumPaths>([&](auto pp) {
+                    constexpr int p = decltype(pp)::value;
+                    if constexpr (kPathL[p][0] == L1 && kPathL[p][2] == LO)
+                        static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto ee) {
+                            constexpr int e = decltype(ee)::value;
+                            constexpr CGEntry en = kCG[kPathEntry[p] + e];
+                            if constexpr (en.a == a) {
+                                if constexpr (first_b_write(p, e))
+                                    U[en.b] = cg_times<p, e>(xg[en.o - LO * LO]);
+                                else
+                                    U[en.b] = fmaf(en.c, xg[en.o - LO * LO], U[en.b]);
+                            }
+                        });
+                });
+            });
+            static_for<kNumPaths>([&](auto pp) {
+                constexpr int p = decltype(pp)::value;
+                if constexpr (kPathL[p][0] == L1 && kPathL[p][2] == LO) {
+                    constexpr int l2 = kPathL[p][1];
+                    // gy[b] is first written by the l1 = 0 block of l_out = l2
+#pragma unroll
+                    for (int i = 0; i < 2 * l2 + 1; ++i)
+                        gy[l2 * l2 + i] = L1 == 0 ? rr[p] * U[l2 * l2 + i]
+                                                  : fmaf(rr[p], U[l2 * l2 + i], gy[l2 * l2 + i]);
+                }
+            });
+        });
     });
 }
 
@@ -328,24 +478,31 @@ __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
         float m[16];
 #pragma unroll
         for (int o = 0; o < 16; ++o) m[o] = 0.0f;
-        for (int64_t k = s; k < e; ++k) {
-            float rr[kNumPaths];
-            const float* Rr = R + (k - e0) * C * kNumPaths + cc;
+        // operands of edge k: its R row (path offsets in a scalar register, no
+        // per-load address math) and the source row
+        auto load = [&](int64_t k, float* rr, float* xs) {
+            const auto rs = buffer_rsrc(R + (k - e0) * C * kNumPaths, (uint32_t)C * kNumPaths * 4u);
 #pragma unroll
-            for (int p = 0; p < kNumPaths; ++p) rr[p] = Rr[p * C];
+            for (int p = 0; p < kNumPaths; ++p) rr[p] = buffer_ld(rs, cc * 4, p * C * 4);
+            load_row16(x + (src[k] * C + cc) * 16, xs);
+        };
+        auto message = [&](int64_t k, const float* rr, const float* xs) {
             float Y[16];
             mace_edge_sh(vec, k, Y);
-            float xs[16];
-            load_row16(x + (src[k] * C + cc) * 16, xs);
-            static_for<kNumPaths>([&](auto pp) {
-                constexpr int p = decltype(pp)::value;
-                constexpr int lo = kPathL[p][2];
-                float tq[2 * lo + 1];
-                mace_path_products<p, lo>(Y, xs, tq);
-#pragma unroll
-                for (int q = 0; q < 2 * lo + 1; ++q) m[lo * lo + q] = fmaf(rr[p], tq[q], m[lo * lo + q]);
-            });
+            mace_message(Y, xs, rr, m);
+        };
+        // two edges per step, each edge's loads issued one edge ahead (the
+        // loads past the row's last edge re-read that edge: always in bounds)
+        float rA[kNumPaths], xA[16], rB[kNumPaths], xB[16];
+        if (s < e) load(s, rA, xA);
+        int64_t k = s;
+        for (; k + 1 < e; k += 2) {
+            load(k + 1, rB, xB);
+            message(k, rA, xA);
+            load(min(k + 2, e - 1), rA, xA);
+            message(k + 1, rB, xB);
         }
+        if (k < e) message(k, rA, xA);
         if (live) {
             float4* op = reinterpret_cast<float4*>(out + (d * C + c) * 16);
 #pragma unroll
@@ -441,42 +598,31 @@ __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
             for (int j = 0; j < nb; ++j) {
                 const int64_t k = kb + j;
                 float rr[kNumPaths];
-                const float* Rr = R + (k - e0) * C * kNumPaths + cc;
+                const auto rs = buffer_rsrc(R + (k - e0) * C * kNumPaths, (uint32_t)C * kNumPaths * 4u);
 #pragma unroll
-                for (int p = 0; p < kNumPaths; ++p) rr[p] = Rr[p * C];
+                for (int p = 0; p < kNumPaths; ++p) rr[p] = buffer_ld(rs, cc * 4, p * C * 4);
                 float Y[16];
                 mace_edge_sh(vec, k, Y);
                 float xs[16];
                 load_row16(x + (src[k] * C + cc) * 16, xs);
-                float* gRr = gR + (k - e0) * C * kNumPaths + cc;
+                const auto gs = buffer_rsrc(gR + (k - e0) * C * kNumPaths, (uint32_t)C * kNumPaths * 4u);
                 // gR[p] = g . T_p (path-major: lanes write consecutive addresses)
-                static_for<kNumPaths>([&](auto pp) {
-                    constexpr int p = decltype(pp)::value;
-                    constexpr int lo = kPathL[p][2];
-                    float tq[2 * lo + 1];
-                    mace_path_products<p, lo>(Y, xs, tq);
-                    float gr = 0.0f;
+                for_blocks<0>([&](auto b0, auto b1) {
+                    block_products<decltype(b0)::value, decltype(b1)::value>(
+                        Y, xs, [&](auto pp, const float* tq) {
+                            constexpr int p = decltype(pp)::value;
+                            constexpr int lo = kPathL[p][2];
+                            float gr = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < 2 * lo + 1; ++q) gr = fmaf(g[lo * lo + q], tq[q], gr);
-                    if (live) gRr[p * C] = gr;
+                            for (int q = 0; q < 2 * lo + 1; ++q) gr = fmaf(g[lo * lo + q], tq[q], gr);
+                            if (live)
+                                __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(gr), gs, c * 4,
+                                                                      p * C * 4, 0);
+                        });
                 });
-                // gy[b] = sum over (p, o, a) of (c0, c1) x[a] R_p g[o]
+                // gy[b] = sum over the entries (a, b, o) of c x[a] R_p g[o]
                 float gy[16];
-#pragma unroll
-                for (int b = 0; b < 16; ++b) gy[b] = 0.0f;
-                static_for<kNumPaths>([&](auto pp) {
-                    constexpr int p = decltype(pp)::value;
-                    constexpr int lo = kPathL[p][2];
-                    float hq[2 * lo + 1];
-#pragma unroll
-                    for (int q = 0; q < 2 * lo + 1; ++q) hq[q] = rr[p] * g[lo * lo + q];
-                    static_for<kPathOp[p + 1] - kPathOp[p]>([&](auto ii) {
-                        constexpr OpEntry oe = kOp[kPathOp[p] + decltype(ii)::value];
-                        const float prod = xs[oe.a] * hq[oe.o - lo * lo];
-                        gy[oe.b0] = fmaf(oe.c0, prod, gy[oe.b0]);
-                        if constexpr (oe.c1 != 0.0f) gy[oe.b1] = fmaf(oe.c1, prod, gy[oe.b1]);
-                    });
-                });
+                mace_grad_y(xs, g, rr, gy);
                 const float t = wave_sum16(gy);
                 if ((lane & 3) == 0) sRed[wv][j][my_b] = t;
             }
