@@ -14,7 +14,8 @@
 //
 // Work per edge: the MLP's second layer is a GEMM [edges x 64] x [64 x 34C]
 // (557 kflop per edge at C = 128) and runs on MFMA over edge chunks; the CG
-// work (1378 flop per edge and channel) runs on the VALU, thread per
+// work (611 products with a coefficient, 256 bilinear products and 156 path
+// weightings per edge and channel) runs on the VALU, thread per
 // (destination row, channel), so every output row is written by one thread in
 // a fixed edge order (deterministic, no atomics).  Forces are gathered per
 // atom from per-edge gradients through the reverse-edge map of the symmetric

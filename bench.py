@@ -283,6 +283,9 @@ def main():
     ap.add_argument("--weighted-only", action="store_true",
                     help="time only the configs[3] weighted variant and print its figures "
                          "(for counter passes)")
+    ap.add_argument("--mace-only", action="store_true",
+                    help="time only the configs[4] MACE layer (forward + backward) and print "
+                         "its figures (for kernel traces and counter passes)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the workload, run 5 plain device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -303,6 +306,9 @@ def main():
             d.copy_(s)
         torch.cuda.synchronize()
         del s, d
+    if a.mace_only:
+        print(json.dumps(mace_config4(torch, bm, dev, reps=max(min(a.steps, 10), 1))), flush=True)
+        return
     w = make_workload(torch, bm, dev)
     E = int(w["src"].numel())
     if a.weighted_only:
