@@ -283,36 +283,70 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-// exclusive scan: out[0..n] (out[n] = total), one workgroup, chunked, fixed order
+// exclusive scan: out[0..n] (out[n] = total), one workgroup, no workspace.
+// Tiles of kScanBlock * kScanPer elements: each thread sums its kScanPer
+// consecutive elements in registers (all loads issued together), the thread
+// sums are scanned within each wave by shuffles and across the waves through
+// LDS (two barriers per tile), and each thread writes its run of prefixes.
 // ---------------------------------------------------------------------------
 constexpr int kScanBlock = 1024;
+constexpr int kScanPer = 16;
 
 template <typename TI>
 __global__ __launch_bounds__(kScanBlock) void scan_exclusive_kernel(const TI* __restrict__ in,
                                                                     int64_t* __restrict__ out,
                                                                     int64_t n) {
-    __shared__ int64_t buf[kScanBlock];
-    __shared__ int64_t carry;
-    if (threadIdx.x == 0) carry = 0;
-    __syncthreads();
-    for (int64_t base = 0; base < n; base += kScanBlock) {
-        const int64_t i = base + threadIdx.x;
-        const int64_t v = i < n ? (int64_t)in[i] : 0;
-        buf[threadIdx.x] = v;
-        __syncthreads();
-        for (int off = 1; off < kScanBlock; off <<= 1) {
-            const int64_t add = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
-            __syncthreads();
-            buf[threadIdx.x] += add;
-            __syncthreads();
+    constexpr int kWaves = kScanBlock / 64;
+    __shared__ int64_t wsum[kWaves];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    int64_t carry = 0;  // total of the previous tiles (the same in every thread)
+    for (int64_t base = 0; base < n; base += (int64_t)kScanBlock * kScanPer) {
+        const int64_t i0 = base + (int64_t)t * kScanPer;
+        int64_t v[kScanPer];
+        if (i0 + kScanPer <= n) {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) v[j] = (int64_t)in[i0 + j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) v[j] = i0 + j < n ? (int64_t)in[i0 + j] : 0;
         }
-        const int64_t incl = buf[threadIdx.x];
-        if (i < n) out[i] = carry + incl - v;
+        int64_t s = 0;
+#pragma unroll
+        for (int j = 0; j < kScanPer; ++j) s += v[j];
+        // inclusive scan of the thread sums within the wave
+        int64_t x = s;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int64_t y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        if (lane == 63) wsum[w] = x;
         __syncthreads();
-        if (threadIdx.x == kScanBlock - 1) carry += incl;
-        __syncthreads();
+        int64_t before = 0, total = 0;  // sums of the waves before this one, of all waves
+#pragma unroll
+        for (int k = 0; k < kWaves; ++k) {
+            const int64_t ws = wsum[k];
+            before += k < w ? ws : 0;
+            total += ws;
+        }
+        __syncthreads();  // wsum is rewritten by the next tile
+        int64_t run = carry + before + x - s;
+        if (i0 + kScanPer <= n) {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) {
+                out[i0 + j] = run;
+                run += v[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kScanPer; ++j) {
+                if (i0 + j < n) out[i0 + j] = run;
+                run += v[j];
+            }
+        }
+        carry += total;
     }
-    if (threadIdx.x == 0) out[n] = carry;
+    if (t == 0) out[n] = carry;
 }
 
 static int scan_i64(const int64_t* in, int64_t* out, int64_t n, hipStream_t s) {

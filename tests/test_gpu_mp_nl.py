@@ -177,6 +177,28 @@ def test_neighbor_list_small_box_self_loops_and_lattice(bm, dev):
     assert np.bincount(ei[0], minlength=216).tolist() == [6] * 216
 
 
+@pytest.mark.parametrize("n", [0, 1, 5, 16383, 16384, 16385, 50001, 300007])
+def test_exclusive_scan_c_abi(bm, dev, n):
+    """batteries_exclusive_scan_i64: out[i] = sum in[:i], out[n] = total, bit-exact; sizes
+    around the 16384-element tile, values up to 2^40 (sums beyond 32 bits)."""
+    lib = ctypes.CDLL(LIB)
+    lib.batteries_exclusive_scan_i64.restype = ctypes.c_int
+    lib.batteries_exclusive_scan_i64.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                                 ctypes.c_void_p]
+    g = gen(900 + n)
+    v = torch.randint(0, 1000, (n,), generator=g, dtype=torch.int64)
+    if n:
+        v[torch.randint(0, n, (max(1, n // 97),), generator=g)] = 1 << 40
+    vd = v.to(dev)
+    out = torch.full((n + 1,), -7, dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    assert lib.batteries_exclusive_scan_i64(vd.data_ptr() if n else None, out.data_ptr(), n, None) == 0
+    torch.cuda.synchronize()
+    want = np.zeros(n + 1, dtype=np.int64)
+    want[1:] = np.cumsum(v.numpy())
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
 def test_neighbor_list_reference_c_abi(bm, dev):
     """ctypes use as in reference benchmarks/benchmark_neighbor_list.py:18-47."""
 
