@@ -1089,12 +1089,13 @@ extern "C" int batteries_sh_tp_scatter_scheduled(const float* edge_vectors,
 //   T[d, q, ci]    = sum_{(a, b) in slot q} c S[d, ci, a, b]           CG table, VALU
 //   out[d, co, o]  = sum_{q -> o} sum_ci W[p(q), ci, co] T[d, q, ci]   MFMA (tp.hip)
 // Work: 2 * 256 * C_in flops per edge (S), 2 * 611 * C_in + 2 * 156 * C_in * C_out per
-// destination (T, mixing).  T is [chunk][slot][position][16]: 16-channel chunks of
-// C_in (zero past C_in), slots in fwd_slot_pos order, destinations by their position
-// in the processing order (padded to a multiple of 16), so that the mixing kernel's
-// operand loads and the path-sum kernel's stores are contiguous 1 KB / 256 B blocks
-// (whole 128-byte lines: a load that uses half of each line it touches runs at half
-// the rate).
+// destination (T, mixing).  T is [chunk][block][slot][16][16]: 16-channel chunks of
+// C_in (zero past C_in), destinations by their position in the processing order
+// (padded to a multiple of 16) in blocks of 16 positions, slots in fwd_slot_pos
+// order, so that the mixing kernel's operand loads and the path-sum kernel's stores
+// are contiguous 1 KB / 256 B blocks (whole 128-byte lines: a load that uses half of
+// each line it touches runs at half the rate) and slot offsets are compile-time
+// constants.
 // ---------------------------------------------------------------------------
 namespace bmhip {
 
@@ -1139,6 +1140,10 @@ __global__ __launch_bounds__(256) void mp_edge_prep_kernel(
 // kPsStride floats apart.  The MFMA-layout writes (8 lanes = 8 values of b) and
 // the contraction's reads (8 lanes = 8 channels) are then free of bank conflicts.
 constexpr int kPsStride = 260;
+// T is [chunk][16-position block][slot][16 positions][16 channels]: one slot of a
+// block is 1 KB, so slot offsets are compile-time constants.
+constexpr int kTSlotBytes = 16 * 16 * 4;
+constexpr int kTBlockBytes = kNumSlots * kTSlotBytes;
 __host__ __device__ constexpr int ps_swz(int b) { return (b >> 1) & 3; }
 
 // CG blocks (l1, l2) contracted by each wave: 166, 149, 149, 147 CG terms.
@@ -1148,11 +1153,12 @@ constexpr int kPsBlocks[4][5][2] = {{{1, 0}, {3, 1}, {3, 3}, {-1, -1}, {-1, -1}}
                                     {{1, 1}, {2, 0}, {2, 1}, {2, 2}, {-1, -1}}};
 
 // The slots of the paths (L1, L2, *) for this lane's (destination, channel):
-// reads S[a in l1][b in l2], contracts with the CG terms, stores
-// T[tbase + pos(q) * sstride].
+// reads S[a in l1][b in l2], contracts with the CG terms, stores slot q at byte
+// toff + pos(q) * 1 KB of the chunk's T (the slot offset is a compile-time
+// constant in a scalar register).
 template <int L1, int L2>
-__device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__ T, int64_t tbase,
-                                         int64_t sstride, bool store, bool chan_ok) {
+__device__ __forceinline__ void ps_block(const float* sSrow, __amdgpu_buffer_rsrc_t tr, int toff,
+                                         bool store, bool chan_ok) {
     constexpr int a0 = L1 * L1, na = 2 * L1 + 1, b0 = L2 * L2, nb = 2 * L2 + 1;
     constexpr int qa0 = a0 / 4, qa1 = (a0 + na - 1) / 4;
     float s[nb][na];
@@ -1185,7 +1191,8 @@ __device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__
                 static_for<no>([&](auto mm) {
                     constexpr int m = decltype(mm)::value;
                     constexpr int pos = fwd_slot_pos(kPathSlot[p] + m);  // compile time
-                    T[tbase + pos * sstride] = chan_ok ? t[m] : 0.0f;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(chan_ok ? t[m] : 0.0f),
+                                                          tr, toff, pos * kTSlotBytes, 0);
                 });
             }
         }
@@ -1193,14 +1200,12 @@ __device__ __forceinline__ void ps_block(const float* sSrow, float* __restrict__
 }
 
 template <int W>
-__device__ __forceinline__ void ps_contract(const float* sSrow, float* __restrict__ T,
-                                            int64_t tbase, int64_t sstride, bool store,
-                                            bool chan_ok) {
+__device__ __forceinline__ void ps_contract(const float* sSrow, __amdgpu_buffer_rsrc_t tr,
+                                            int toff, bool store, bool chan_ok) {
     static_for<5>([&](auto kk) {
         constexpr int k = decltype(kk)::value;
         if constexpr (kPsBlocks[W][k][0] >= 0)
-            ps_block<kPsBlocks[W][k][0], kPsBlocks[W][k][1]>(sSrow, T, tbase, sstride, store,
-                                                             chan_ok);
+            ps_block<kPsBlocks[W][k][0], kPsBlocks[W][k][1]>(sSrow, tr, toff, store, chan_ok);
     });
 }
 
@@ -1221,9 +1226,9 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 // Lane (g, i) then holds S[c0 + 4t + g][all a][b = i] and writes it to LDS.
 // Contraction phase: lane (dd, ch) = (lane / 16, lane % 16) of every wave takes
 // destination dd and channel c0 + ch; wave w contracts its CG blocks.
-// The k-steps of a wave run through a three-stage load pipeline that continues
-// across chunks: the source index and Y of step i + 2, the source-row gathers of
-// step i + 1, the MFMAs of step i.  The next chunk's first gathers are therefore
+// The k-steps of a wave run through a four-stage load pipeline that continues
+// across chunks: the source index and Y of step i + 3, the source-row gathers of
+// steps i + 2 and i + 1, the MFMAs of step i.  The next chunk's first gathers are therefore
 // in flight during this chunk's contraction.
 __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
     const float* __restrict__ yc, const int* __restrict__ srcc, const float* __restrict__ X,
@@ -1276,18 +1281,26 @@ __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
             s = 0;
         }
     };
-    // pipeline state: stage A (source index, Y) and stage B (gathers)
-    int cA = 0, sA = 0, cB = 0, sB = 0;
+    // pipeline state: stage A (source index, Y of the step three ahead), stage C
+    // (gathers of the step two ahead) and stage B (gathers of the next step)
+    int cA = 0, sA = 0, cC = 0, sC = 0;
     int srcA = 0;
-    float yA = 0.f, yB = 0.f;
-    float4 xB[4];
+    float yA = 0.f, yB = 0.f, yC = 0.f;
+    float4 xB[4], xC[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xB[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = 0; t < 4; ++t) xB[t] = xC[t] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (nst > 0) {
         srcA = srcc[slot(0)];
         yA = 4 * 0 + g < deg ? yc[slot(0) * 16 + i16] : 0.f;
         gather(srcA, 0, xB);
         yB = yA;
+        next(cA, sA);
+        srcA = srcc[slot(sA)];
+        yA = 4 * sA + g < deg ? yc[slot(sA) * 16 + i16] : 0.f;
+        cC = cA;
+        sC = sA;
+        gather(srcA, cC, xC);
+        yC = yA;
         next(cA, sA);
         srcA = srcc[slot(sA)];
         yA = 4 * sA + g < deg ? yc[slot(sA) * 16 + i16] : 0.f;
@@ -1301,12 +1314,16 @@ __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
         for (int s = 0; s < nst; ++s) {
             float4 xa[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xa[t] = xB[t];
+            for (int t = 0; t < 4; ++t) {
+                xa[t] = xB[t];
+                xB[t] = xC[t];
+            }
             const float ya = yB;
-            next(cB, sB);  // stage B: gathers of the following step
-            gather(srcA, cB, xB);
-            yB = yA;
-            next(cA, sA);  // stage A: index and Y two steps ahead
+            yB = yC;
+            next(cC, sC);  // stage C: gathers of the step two ahead
+            gather(srcA, cC, xC);
+            yC = yA;
+            next(cA, sA);  // stage A: index and Y three steps ahead
             srcA = srcc[slot(sA)];
             {
                 const float yv = yc[slot(sA) * 16 + i16];
@@ -1332,21 +1349,22 @@ __global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
         }
         __syncthreads();
         // contraction: lane (dd, ch)
-        // T[chunk][slot][position][16]: the 4 positions x 16 channels of one slot are
-        // 256 contiguous bytes
+        // the 4 positions x 16 channels of one slot are 256 contiguous bytes of T
         const int dd = lane >> 4, ch = lane & 15;
         const int c0 = (ch0 + c) * 16;
         const int64_t pos = quad * 4 + dd;
         const bool store = pos < n_dst;
-        const int64_t sstride = npad * 16;
-        const int64_t tbase = (int64_t)(ch0 + c) * kNumSlots * sstride + pos * 16 + ch;
+        const int64_t tchunk = npad * kNumSlots * 16;  // floats per chunk of T
+        const __amdgpu_buffer_rsrc_t tr =
+            buffer_rsrc(T + (int64_t)(ch0 + c) * tchunk, (uint32_t)(tchunk * 4));
+        const int toff = (int)(pos >> 4) * kTBlockBytes + ((int)(pos & 15) * 16 + ch) * 4;
         const float* sSrow = sS + (dd * 16 + ch) * kPsStride;
         const bool chan_ok = c0 + ch < C;
         switch (w) {
-            case 0: ps_contract<0>(sSrow, T, tbase, sstride, store, chan_ok); break;
-            case 1: ps_contract<1>(sSrow, T, tbase, sstride, store, chan_ok); break;
-            case 2: ps_contract<2>(sSrow, T, tbase, sstride, store, chan_ok); break;
-            default: ps_contract<3>(sSrow, T, tbase, sstride, store, chan_ok); break;
+            case 0: ps_contract<0>(sSrow, tr, toff, store, chan_ok); break;
+            case 1: ps_contract<1>(sSrow, tr, toff, store, chan_ok); break;
+            case 2: ps_contract<2>(sSrow, tr, toff, store, chan_ok); break;
+            default: ps_contract<3>(sSrow, tr, toff, store, chan_ok); break;
         }
     }
 }
@@ -1387,8 +1405,7 @@ __device__ __forceinline__ void mix_component(const float* __restrict__ T,
     const int64_t tchunk = (int64_t)kNumSlots * npad * 16;  // floats per chunk of T
     const uint32_t tchunk_bytes = (uint32_t)(tchunk * sizeof(float));
     const int toff = ((int)min<int64_t>(i16, n - 1 - row0) * 16 + 4 * g4) * 4;
-    const int trow = (int)(row0 * 64);   // bytes of the tile's first position in a slot
-    const int tslot = (int)(npad * 64);  // bytes per slot
+    const int tblock = (int)(row0 >> 4) * kTBlockBytes;  // bytes of the tile's block
     const __amdgpu_buffer_rsrc_t wr =
         buffer_rsrc(wt, (uint32_t)((int64_t)nchunk * kNumPaths * cout * 64));
     const int wpath = cout * 64, wchunk = kNumPaths * cout * 64;
@@ -1404,7 +1421,7 @@ __device__ __forceinline__ void mix_component(const float* __restrict__ T,
         constexpr int pos = fwd_slot_pos(q);
         constexpr int p = kSlotPath[q];
         const __amdgpu_buffer_rsrc_t tr = buffer_rsrc(T + chunk * tchunk, tchunk_bytes);
-        a = buffer_ld4(tr, toff, pos * tslot + trow);
+        a = buffer_ld4(tr, toff, tblock + pos * kTSlotBytes);
 #pragma unroll
         for (int t = 0; t < 4; ++t) b[t] = buffer_ld4(wr, wco[t], chunk * wchunk + p * wpath);
     };
