@@ -732,16 +732,28 @@ MaceArgs mace_check(const torch::Tensor& positions, const torch::Tensor& cell,
     return a;
 }
 
+// Optional processing order of the destination rows: int64 [N] on the inputs' device.
+const int64_t* mace_order(const c10::optional<torch::Tensor>& order, int64_t N,
+                          const torch::Tensor& like) {
+    if (!order.has_value() || !order->defined()) return nullptr;
+    TORCH_CHECK(order->dtype() == torch::kInt64 && order->dim() == 1 && order->numel() == N &&
+                    order->device() == like.device() && order->is_contiguous(),
+                "order must be a contiguous int64 [N] tensor on the device of the inputs");
+    return cptr<int64_t>(*order, "order");
+}
+
 torch::Tensor mace_forward(const torch::Tensor& positions, const torch::Tensor& cell,
                            const torch::Tensor& node_features, const torch::Tensor& w1,
                            const torch::Tensor& b1, const torch::Tensor& w2,
                            const torch::Tensor& src, const torch::Tensor& dst,
                            const torch::Tensor& row_ptr, double cutoff,
-                           const c10::optional<torch::Tensor>& edge_weights) {
+                           const c10::optional<torch::Tensor>& edge_weights,
+                           const c10::optional<torch::Tensor>& order) {
     const MaceArgs a = mace_check(positions, cell, node_features, w1, b1, w2, src, dst, row_ptr);
     torch::Tensor x = aligned16(node_features);
     torch::Tensor out = torch::empty({a.N, a.C, 16}, f32_like(x));
     if (a.N == 0) return out;
+    const int64_t* ord = mace_order(order, a.N, x);
     float* ew = nullptr;
     if (edge_weights.has_value() && edge_weights->defined()) {
         TORCH_CHECK(edge_weights->dtype() == torch::kFloat32 &&
@@ -758,8 +770,9 @@ torch::Tensor mace_forward(const torch::Tensor& positions, const torch::Tensor& 
                                         cptr<float>(x, "node_features"), cptr<float>(w1, "W1"),
                                         cptr<float>(b1, "b1"), cptr<float>(w2, "W2"),
                                         cptr<int64_t>(src, "src"), cptr<int64_t>(dst, "dst"),
-                                        cptr<int64_t>(row_ptr, "row_ptr"), mptr<float>(out, "out"),
-                                        ew, a.N, a.E, (int)a.C, (float)cutoff, ws.data_ptr(), wsb,
+                                        cptr<int64_t>(row_ptr, "row_ptr"), ord,
+                                        mptr<float>(out, "out"), ew, a.N, a.E, (int)a.C,
+                                        (float)cutoff, ws.data_ptr(), wsb,
                                         current_stream(x)),
                  "mace_forward");
     return out;
@@ -776,7 +789,8 @@ torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor&
                             const torch::Tensor& src, const torch::Tensor& dst,
                             const torch::Tensor& row_ptr, const torch::Tensor& rev,
                             const torch::Tensor& grad_out, double cutoff,
-                            const c10::optional<torch::Tensor>& edge_weights) {
+                            const c10::optional<torch::Tensor>& edge_weights,
+                            const c10::optional<torch::Tensor>& order) {
     const MaceArgs a = mace_check(positions, cell, node_features, w1, b1, w2, src, dst, row_ptr);
     TORCH_CHECK(rev.numel() == a.E && rev.dtype() == torch::kInt64, "rev must be int64 [E]");
     TORCH_CHECK(grad_out.dim() == 3 && grad_out.size(0) == a.N && grad_out.size(1) == a.C &&
@@ -786,6 +800,7 @@ torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor&
     torch::Tensor g = aligned16(grad_out.contiguous());
     torch::Tensor gpos = torch::empty({a.N, 3}, f32_like(x));
     if (a.N == 0) return gpos;
+    const int64_t* ord = mace_order(order, a.N, x);
     const float* ew = nullptr;
     if (edge_weights.has_value() && edge_weights->defined()) {
         TORCH_CHECK(edge_weights->dtype() == torch::kFloat32 &&
@@ -801,7 +816,7 @@ torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor&
                                          cptr<float>(x, "node_features"), cptr<float>(w1, "W1"),
                                          cptr<float>(b1, "b1"), cptr<float>(w2, "W2"),
                                          cptr<int64_t>(src, "src"), cptr<int64_t>(dst, "dst"),
-                                         cptr<int64_t>(row_ptr, "row_ptr"),
+                                         cptr<int64_t>(row_ptr, "row_ptr"), ord,
                                          cptr<int64_t>(rev, "rev"), cptr<float>(g, "grad_out"),
                                          ew, mptr<float>(gpos, "grad_pos"), a.N, a.E, (int)a.C,
                                          (float)cutoff, ws.data_ptr(), wsb, current_stream(x)),
@@ -883,17 +898,18 @@ PYBIND11_MODULE(_batmobile, m) {
     m.def("mace_forward", &mace_forward, py::arg("positions"), py::arg("cell"),
           py::arg("node_features"), py::arg("W1"), py::arg("b1"), py::arg("W2"), py::arg("src"),
           py::arg("dst"), py::arg("row_ptr"), py::arg("cutoff"),
-          py::arg("edge_weights") = py::none(),
+          py::arg("edge_weights") = py::none(), py::arg("order") = py::none(),
           "MACE-style layer with per-edge radial weights, forward (extension); edge_weights "
-          "[mace_edge_weight_rows(E, C), 34 C] receives the per-edge weights for the backward");
+          "[mace_edge_weight_rows(E, C), 34 C] receives the per-edge weights for the backward; "
+          "order [N] is the processing order of the destination rows (results do not depend on it)");
     m.def("mace_edge_weight_rows", &mace_edge_weight_rows, py::arg("E"), py::arg("C"),
           "rows of the buffer that keeps the per-edge weights of all E edges (whole chunks)");
     m.def("mace_backward", &mace_backward, py::arg("positions"), py::arg("cell"),
           py::arg("node_features"), py::arg("W1"), py::arg("b1"), py::arg("W2"), py::arg("src"),
           py::arg("dst"), py::arg("row_ptr"), py::arg("rev"), py::arg("grad_out"),
-          py::arg("cutoff"), py::arg("edge_weights") = py::none(),
+          py::arg("cutoff"), py::arg("edge_weights") = py::none(), py::arg("order") = py::none(),
           "gradient of the MACE-style layer w.r.t. positions (extension); with the forward's "
-          "edge_weights the per-edge weights are not recomputed");
+          "edge_weights the per-edge weights are not recomputed; order as for mace_forward");
     m.def("selftest_mfma_16x16x4", &selftest_mfma_16x16x4, py::arg("A"), py::arg("B"),
           "D = A @ B through one v_mfma_f32_16x16x4f32 (lane-layout self test)");
 }

@@ -464,17 +464,41 @@ __device__ __forceinline__ void load_row16(const float* __restrict__ p, float* v
     }
 }
 
+// First row and step of a workgroup's walk over the chunk's destination rows
+// [d_lo, d_hi).  Without `order`: rows d_lo + blockIdx.x, + gridDim.x, ...  With
+// `order` (n_pos positions, e.g. a spatial order): workgroup b takes position
+// (b % 8) * gridDim.x / 8 + b / 8 (consecutive positions on one XCD, whose L2 then
+// holds the source rows that neighbouring destinations share) and its row when that
+// row is in the chunk; gridDim.x is a multiple of 8.
+__device__ __forceinline__ void mace_row_walk(const int64_t* __restrict__ order, int64_t n_pos,
+                                              int64_t d_lo, int64_t d_hi, int64_t& first,
+                                              int64_t& step) {
+    if (!order) {
+        first = d_lo + blockIdx.x;
+        step = gridDim.x;
+        return;
+    }
+    const int64_t per_xcd = gridDim.x >> 3;
+    const int64_t p = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    const int64_t d = p < n_pos ? order[p] : -1;
+    first = (d >= d_lo && d < d_hi) ? d : d_hi;
+    step = d_hi - d_lo + 1;  // one row
+}
+
 // Forward: out[d, c, :] += sum over the chunk's edges of row d of
 // sum_p R[e, p, c] T_p[e, c, :] (R row e - e0 of the chunk, path-major).
 __global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
     const float* __restrict__ vec, const float* __restrict__ x, const int64_t* __restrict__ src,
     const int64_t* __restrict__ row_ptr, const float* __restrict__ R,
-    const int64_t* __restrict__ rows, int64_t e0, int64_t e1, float* __restrict__ out, int C) {
+    const int64_t* __restrict__ rows, const int64_t* __restrict__ order, int64_t n_pos, int64_t e0,
+    int64_t e1, float* __restrict__ out, int C) {
     const int c = blockIdx.y * blockDim.x + threadIdx.x;
     const bool live = c < C;
     const int cc = live ? c : C - 1;
     const int64_t d_lo = rows[0], d_hi = rows[1];
-    for (int64_t d = d_lo + blockIdx.x; d < d_hi; d += gridDim.x) {
+    int64_t d0, dstep;
+    mace_row_walk(order, n_pos, d_lo, d_hi, d0, dstep);
+    for (int64_t d = d0; d < d_hi; d += dstep) {
         const int64_t s = max(row_ptr[d], e0), e = min(row_ptr[d + 1], e1);
         float m[16];
 #pragma unroll
@@ -575,7 +599,8 @@ constexpr int kMaceEB = 8;  // edges per gY reduction batch of the backward
 __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
     const float* __restrict__ vec, const float* __restrict__ x, const int64_t* __restrict__ src,
     const int64_t* __restrict__ row_ptr, const float* __restrict__ R,
-    const float* __restrict__ gout, const int64_t* __restrict__ rows, int64_t e0, int64_t e1,
+    const float* __restrict__ gout, const int64_t* __restrict__ rows,
+    const int64_t* __restrict__ order, int64_t n_pos, int64_t e0, int64_t e1,
     float* __restrict__ gR, float* __restrict__ gY, int C) {
     __shared__ float sRed[4][kMaceEB][16];
     const int c = threadIdx.x;
@@ -585,7 +610,9 @@ __global__ __launch_bounds__(256) void mace_tp_backward_kernel(
     const int my_b = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1) + 2 * ((lane >> 3) & 1) +
                      ((lane >> 2) & 1);
     const int64_t d_lo = rows[0], d_hi = rows[1];
-    for (int64_t d = d_lo + blockIdx.x; d < d_hi; d += gridDim.x) {
+    int64_t d0, dstep;
+    mace_row_walk(order, n_pos, d_lo, d_hi, d0, dstep);
+    for (int64_t d = d0; d < d_hi; d += dstep) {
         const int64_t s = max(row_ptr[d], e0), e = min(row_ptr[d + 1], e1);
         float g[16];
         load_row16(gout + (d * C + cc) * 16, g);
@@ -874,6 +901,7 @@ extern "C" int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_
 
 static bool mace_args_ok(const float* box, int64_t N, int64_t E, int C, float cutoff) {
     if (!box || N < 0 || E < 0 || C <= 0 || C > 256 || !(cutoff > 0.0f)) return false;
+    if (ceil_div(N, 8) * 8 > INT32_MAX) return false;  // one workgroup per position
     for (int k = 0; k < 3; ++k)
         if (!(box[k] > 0.0f)) return false;
     return true;  // chunk offsets are kept within 32 bits by mace_chunk
@@ -891,7 +919,8 @@ static MaceBox mace_box(const float* box) {
 extern "C" int batteries_mace_forward(const float* positions, const float* box,
                                       const float* node_features, const float* w1,
                                       const float* b1, const float* w2, const int64_t* src,
-                                      const int64_t* dst, const int64_t* row_ptr, float* out,
+                                      const int64_t* dst, const int64_t* row_ptr,
+                                      const int64_t* order, float* out,
                                       float* edge_weights, int64_t N, int64_t N_edges, int C,
                                       float cutoff, void* workspace, size_t workspace_bytes,
                                       hipStream_t stream) {
@@ -919,10 +948,11 @@ extern "C" int batteries_mace_forward(const float* positions, const float* box,
         int rc = blas_gemm(w.h, w2, R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
                            stream);
         if (rc != BM_OK) return rc;
-        dim3 grid(mace_row_blocks(chunk), (unsigned)ceil_div(C, nthr));
+        dim3 grid(order ? (unsigned)(ceil_div(N, 8) * 8) : mace_row_blocks(chunk),
+                  (unsigned)ceil_div(C, nthr));
         mace_tp_scatter_kernel<<<grid, nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, R,
-                                                          w.rows + 2 * (e0 / chunk), e0, e1,
-                                                          out, C);
+                                                          w.rows + 2 * (e0 / chunk), order, N,
+                                                          e0, e1, out, C);
     }
     return (int)hipGetLastError();
 }
@@ -931,7 +961,8 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
                                        const float* node_features, const float* w1,
                                        const float* b1, const float* w2, const int64_t* src,
                                        const int64_t* dst, const int64_t* row_ptr,
-                                       const int64_t* rev, const float* grad_out,
+                                       const int64_t* order, const int64_t* rev,
+                                       const float* grad_out,
                                        const float* edge_weights, float* grad_pos, int64_t N,
                                        int64_t N_edges, int C, float cutoff, void* workspace,
                                        size_t workspace_bytes, hipStream_t stream) {
@@ -963,9 +994,10 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
                            false, stream);
             if (rc != BM_OK) return rc;
         }
-        mace_tp_backward_kernel<<<mace_row_blocks(chunk), nthr, 0, stream>>>(
-            w.vec, node_features, src, row_ptr, R, grad_out, w.rows + 2 * (e0 / chunk), e0,
-            e1, w.gR, w.gY, C);
+        mace_tp_backward_kernel<<<order ? (unsigned)(ceil_div(N, 8) * 8) : mace_row_blocks(chunk),
+                                  nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, R,
+                                                     grad_out, w.rows + 2 * (e0 / chunk), order,
+                                                     N, e0, e1, w.gR, w.gY, C);
         rc = blas_gemm(w.gR, w2, w.gh, gemm_rows(N_edges, eb, chunk), kHidden, C * kNumPaths, true, stream);
         if (rc != BM_OK) return rc;
         mace_radial_backward_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(

@@ -293,18 +293,22 @@ int64_t batteries_mace_edge_weight_rows(int64_t N_edges, int C);
 int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src, int64_t* rev,
                                  int* d_missing, int64_t N, int64_t N_edges, hipStream_t stream);
 /* edge_weights (nullable): when given, R of every edge is written there (row e,
- * path-major [34][C]) and kept for batteries_mace_backward. */
+ * path-major [34][C]) and kept for batteries_mace_backward.  order (nullable, [N]): the
+ * order in which destination rows are processed (a spatial order keeps the source rows
+ * that neighbouring destinations share in cache); the results do not depend on it. */
 int batteries_mace_forward(const float* positions, const float* box, const float* node_features,
                            const float* w1, const float* b1, const float* w2, const int64_t* src,
-                           const int64_t* dst, const int64_t* row_ptr, float* out,
-                           float* edge_weights, int64_t N, int64_t N_edges, int C, float cutoff,
-                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+                           const int64_t* dst, const int64_t* row_ptr, const int64_t* order,
+                           float* out, float* edge_weights, int64_t N, int64_t N_edges, int C,
+                           float cutoff, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
 /* grad_pos[N,3] = d <out, grad_out> / d positions (rev from batteries_mace_reverse_edges).
  * edge_weights (nullable): the forward's saved R; when NULL, R is recomputed per chunk. */
 int batteries_mace_backward(const float* positions, const float* box, const float* node_features,
                             const float* w1, const float* b1, const float* w2, const int64_t* src,
-                            const int64_t* dst, const int64_t* row_ptr, const int64_t* rev,
-                            const float* grad_out, const float* edge_weights, float* grad_pos,
+                            const int64_t* dst, const int64_t* row_ptr, const int64_t* order,
+                            const int64_t* rev, const float* grad_out, const float* edge_weights,
+                            float* grad_pos,
                             int64_t N, int64_t N_edges, int C, float cutoff, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 

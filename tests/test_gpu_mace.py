@@ -109,3 +109,25 @@ def test_mace_saved_edge_weights_equal_recomputed(bm, dev, n, c):
     assert torch.equal(g_saved, g_plain)
     with pytest.raises(RuntimeError, match="edge_weights"):
         bm.mace_forward(*args, 5.0, torch.empty(rows - 1, 34 * c, device=dev))
+
+
+def test_mace_row_order_does_not_change_results(bm, dev):
+    """Rows in the graph's spatial order (as MACEInteraction runs them) and in index
+    order give bit-identical outputs and forces: each row is summed by one workgroup in
+    ascending edge order either way.  A malformed order is refused."""
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, 9500, 2, 61)  # two edge chunks
+    p, xd, god = pos.to(dev), x.to(dev), go.to(dev)
+    args = (p, cell, xd, layer.W1, layer.b1, layer.W2, graph.src, graph.dst, graph.row_ptr)
+    out_idx = bm.mace_forward(*args, 5.0)
+    out_sp = bm.mace_forward(*args, 5.0, None, graph.order)
+    assert torch.equal(out_idx, out_sp)
+    rev = graph.reverse_edges()
+    g_idx = bm.mace_backward(*args, rev, god, 5.0)
+    g_sp = bm.mace_backward(*args, rev, god, 5.0, None, graph.order)
+    assert torch.equal(g_idx, g_sp)
+    # a reversed order as well (any permutation)
+    assert torch.equal(bm.mace_forward(*args, 5.0, None, graph.order.flip(0).contiguous()), out_idx)
+    with pytest.raises(RuntimeError, match="order"):
+        bm.mace_forward(*args, 5.0, None, graph.order[:-1].contiguous())
+    with pytest.raises(RuntimeError, match="order"):
+        bm.mace_forward(*args, 5.0, None, graph.order.to(torch.int32))
