@@ -901,7 +901,8 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("edge_weights") = py::none(), py::arg("order") = py::none(),
           "MACE-style layer with per-edge radial weights, forward (extension); edge_weights "
           "[mace_edge_weight_rows(E, C), 34 C] receives the per-edge weights for the backward; "
-          "order [N] is the processing order of the destination rows (results do not depend on it)");
+          "order [N], a permutation of 0..N-1, is the processing order of the destination rows "
+          "(results do not depend on it)");
     m.def("mace_edge_weight_rows", &mace_edge_weight_rows, py::arg("E"), py::arg("C"),
           "rows of the buffer that keeps the per-edge weights of all E edges (whole chunks)");
     m.def("mace_backward", &mace_backward, py::arg("positions"), py::arg("cell"),

@@ -294,8 +294,10 @@ int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src, int
                                  int* d_missing, int64_t N, int64_t N_edges, hipStream_t stream);
 /* edge_weights (nullable): when given, R of every edge is written there (row e,
  * path-major [34][C]) and kept for batteries_mace_backward.  order (nullable, [N]): the
- * order in which destination rows are processed (a spatial order keeps the source rows
- * that neighbouring destinations share in cache); the results do not depend on it. */
+ * order in which destination rows are processed, a permutation of 0..N-1 (a spatial
+ * order keeps the source rows that neighbouring destinations share in cache); the
+ * results do not depend on it.  A row that order names twice is summed twice and a row
+ * it does not name is left out, so order must be a permutation. */
 int batteries_mace_forward(const float* positions, const float* box, const float* node_features,
                            const float* w1, const float* b1, const float* w2, const int64_t* src,
                            const int64_t* dst, const int64_t* row_ptr, const int64_t* order,
