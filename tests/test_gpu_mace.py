@@ -39,7 +39,7 @@ def _oracle(pos, cell, graph, layer, x, go):
                                       go.numpy())
 
 
-@pytest.mark.parametrize("n,c", [(80, 16), (300, 5), (80, 64), (60, 128)])
+@pytest.mark.parametrize("n,c", [(80, 16), (300, 5), (80, 64), (60, 128), (40, 256)])
 def test_mace_layer_forward_and_forces(bm, dev, n, c):
     pos, cell, graph, layer, x, go = _layer_inputs(dev, n, c, 11)
     p = pos.to(dev).requires_grad_(True)

@@ -34,6 +34,7 @@ def _weights(ci, co, seed):
     (64, 900, 5, 3, True),      # channels below one 16-channel chunk
     (50, 700, 20, 70, True),    # a partial input chunk, two output-channel groups
     (33, 400, 48, 8, False),    # an odd number of input chunks
+    (70, 1200, 128, 128, True),  # eight input chunks in four groups, two output-channel tiles
 ])
 def test_weighted_scatter_random_graph(bm, dev, n, e, ci, co, normalize):
     vec = unit_vectors(e, 40 + ci)
