@@ -253,6 +253,30 @@ def mace_config4(torch, bm, dev, reps=3):
     }
 
 
+def scatter_sweep(torch, bm, dev, sizes=(5000, 20000, 50000), reps=200):
+    """The headline kernel (Graph.sh_tp_scatter, C = 64, ~30 neighbours within 5 A) at
+    several system sizes, same density and seed scheme: HIP-event time per launch after a
+    clock settle, edges/s and the fraction of the fp32 MFMA peak on E (512 C + 1222) flops."""
+    res = {}
+    for n in sizes:
+        g = torch.Generator().manual_seed(SEED)
+        L = (n / RHO) ** (1.0 / 3.0)
+        pos = torch.rand(n, 3, generator=g) * L
+        cell = torch.diag(torch.tensor([L, L, L]))
+        x = torch.randn(n, CHANNELS, 16, generator=g).to(dev)
+        graph = bm.Graph(pos.to(dev), cell, CUTOFF, CHANNELS)
+        e = graph.num_edges
+        for _ in range(SETTLE_STEPS):
+            graph.sh_tp_scatter(x)
+        t = event_ms(torch, lambda: graph.sh_tp_scatter(x), reps)
+        f = e * (2 * 256 * CHANNELS + 2 * 611)
+        res[f"N{n}"] = {"E": e, "kernel_us": round(t * 1e3, 2),
+                        "edges_per_s": round(e / (t * 1e-3), 1),
+                        "mfma_frac": round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)}
+        del graph, x
+    return res
+
+
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     passes recorded in profiles/hbm_traffic.txt (scaled by the copy calibration)."""
@@ -286,6 +310,9 @@ def main():
     ap.add_argument("--mace-only", action="store_true",
                     help="time only the configs[4] MACE layer (forward + backward) and print "
                          "its figures (for kernel traces and counter passes)")
+    ap.add_argument("--scatter-sweep", action="store_true",
+                    help="time only the headline kernel at N = 5000, 20000, 50000 (C = 64) and "
+                         "print the figures")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the workload, run 5 plain device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -306,6 +333,9 @@ def main():
             d.copy_(s)
         torch.cuda.synchronize()
         del s, d
+    if a.scatter_sweep:
+        print(json.dumps(scatter_sweep(torch, bm, dev, reps=max(a.steps, 1))), flush=True)
+        return
     if a.mace_only:
         print(json.dumps(mace_config4(torch, bm, dev, reps=max(min(a.steps, 10), 1))), flush=True)
         return
