@@ -100,30 +100,32 @@ __device__ __forceinline__ void tp_simple_backward_rows(const float* x, const fl
 __global__ __launch_bounds__(kTpBlock) void tp_simple_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ y,
                                                              float* __restrict__ out, int64_t n) {
-    __shared__ float sx[kTpBlock * kRowStride];
-    __shared__ float sy[kTpBlock * kRowStride];
+    // one staging buffer, used in turn for x, y and the output (half the LDS of
+    // separate buffers, so registers, not LDS, bound the waves per SIMD)
+    __shared__ float sb[kTpBlock * kRowStride];
     const int64_t base = (int64_t)blockIdx.x * kTpBlock;
     const int rows = (int)min<int64_t>(kTpBlock, n - base);
     float4 vx[4], vy[4];
     load_rows16(x, base, rows, vx);
     load_rows16(y, base, rows, vy);
-    put_rows16(sx, rows, vx);
-    put_rows16(sy, rows, vy);
-    __syncthreads();
     const int t = threadIdx.x;
-    if (t < rows) {
-        float a[16], b[16], o[16];
+    float a[16], b[16], o[16];
+    put_rows16(sb, rows, vx);
+    __syncthreads();
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            a[k] = sx[t * kRowStride + k];
-            b[k] = sy[t * kRowStride + k];
-        }
+    for (int k = 0; k < 16; ++k) a[k] = sb[t * kRowStride + k];
+    __syncthreads();
+    put_rows16(sb, rows, vy);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) b[k] = sb[t * kRowStride + k];
+    if (t < rows) {
         tp_simple_rows(a, b, o);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) sx[t * kRowStride + k] = o[k];
+        for (int k = 0; k < 16; ++k) sb[t * kRowStride + k] = o[k];  // own row: read above
     }
     __syncthreads();
-    store_rows16(sx, out, base, rows);
+    store_rows16(sb, out, base, rows);
 }
 
 __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
