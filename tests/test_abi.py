@@ -94,3 +94,28 @@ def test_extension_module_names(bm):
 def test_argument_errors_raise_runtime_error(bm, call):
     with pytest.raises(RuntimeError):
         call(bm)
+
+
+def test_package_fails_loudly_without_the_extension(tmp_path):
+    """No CPU fallback: the package copied without its compiled extension refuses to import."""
+    import shutil
+    import subprocess
+    import sys
+    pkg = os.path.join(REPO, "batmobile-evo_amd", "python", "batmobile")
+    shutil.copytree(pkg, tmp_path / "batmobile", ignore=shutil.ignore_patterns("__pycache__"))
+    code = f"import sys; sys.path.insert(0, {str(tmp_path)!r}); import batmobile"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0
+    assert "ImportError" in r.stderr and "not built" in r.stderr
+
+
+def test_extension_refuses_host_tensors():
+    """Host (CPU) tensors are refused with an error, never computed on the CPU."""
+    import sys
+    import torch
+    sys.path.insert(0, os.path.join(REPO, "batmobile-evo_amd", "python"))
+    import _batmobile
+    with pytest.raises(RuntimeError):
+        _batmobile.spherical_harmonics(torch.zeros(4, 3), 3)
+    with pytest.raises(RuntimeError):
+        _batmobile.tensor_product_simple(torch.zeros(4, 16), torch.zeros(4, 16))
