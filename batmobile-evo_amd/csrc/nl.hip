@@ -123,6 +123,44 @@ __global__ void nl_sort_bins_kernel(const int64_t* __restrict__ bin_start, int* 
     }
 }
 
+// The same with one wave per bin (bins of a few atoms each, as many bins as a few
+// workgroups per compute unit): the bin's atom indices are staged in LDS and each
+// goes to its rank (indices in a bin are distinct).  A bin of more than
+// kBinSortCap atoms is sorted by one lane as above.
+constexpr int kBinSortCap = 1024;
+__global__ __launch_bounds__(64) void nl_sort_bins_wave_kernel(const int64_t* __restrict__ bin_start,
+                                                               int* __restrict__ order, int total) {
+    __shared__ int sv[kBinSortCap];
+    const int k = blockIdx.x;
+    if (k >= total) return;
+    const int64_t s = bin_start[k];
+    const int n = (int)(bin_start[k + 1] - s);
+    const int lane = threadIdx.x;
+    if (n <= 1) return;
+    if (n > kBinSortCap) {
+        if (lane == 0) {
+            for (int64_t i = s + 1; i < s + n; ++i) {
+                const int v = order[i];
+                int64_t j = i - 1;
+                while (j >= s && order[j] > v) {
+                    order[j + 1] = order[j];
+                    --j;
+                }
+                order[j + 1] = v;
+            }
+        }
+        return;
+    }
+    for (int i = lane; i < n; i += 64) sv[i] = order[s + i];
+    __syncthreads();
+    for (int i = lane; i < n; i += 64) {
+        const int v = sv[i];
+        int r = 0;
+        for (int u = 0; u < n; ++u) r += sv[u] < v ? 1 : 0;
+        order[s + r] = v;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Stencil passes (count, then write): one wave per home cell.  The atoms of the
 // 27 cells around it (reference order: dz, dy, dx from -1 to 1, atoms of a cell
@@ -429,8 +467,8 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
     if (N > 0) {
         nl_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(bin_of, bin_start, bin_count,
                                                                     order, N);
-        nl_sort_bins_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_start, order,
-                                                                              c.total);
+        nl_sort_bins_wave_kernel<<<(unsigned)c.total, 64, 0, stream>>>(bin_start, order,
+                                                                         c.total);
         nl_cell_kernel<false><<<(unsigned)c.total, 64, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
             nullptr, nullptr);
