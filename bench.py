@@ -319,7 +319,8 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
-              "(every box here has one MI355X; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(every box here has one MI355X; the path would shard by destination ownership with a "
+              "halo exchange of source rows, which this build does not implement)", file=sys.stderr)
         sys.exit(2)
 
     import torch
