@@ -310,6 +310,9 @@ def main():
     ap.add_argument("--mace-only", action="store_true",
                     help="time only the configs[4] MACE layer (forward + backward) and print "
                          "its figures (for kernel traces and counter passes)")
+    ap.add_argument("--tp-only", action="store_true",
+                    help="time only configs[0..2] (SH, simple and weighted tensor products) and "
+                         "print their figures (for counter passes)")
     ap.add_argument("--scatter-sweep", action="store_true",
                     help="time only the headline kernel at N = 5000, 20000, 50000 (C = 64) and "
                          "print the figures")
@@ -334,6 +337,9 @@ def main():
             d.copy_(s)
         torch.cuda.synchronize()
         del s, d
+    if a.tp_only:
+        print(json.dumps(other_configs(torch, bm, dev)), flush=True)
+        return
     if a.scatter_sweep:
         print(json.dumps(scatter_sweep(torch, bm, dev, reps=max(a.steps, 1))), flush=True)
         return
