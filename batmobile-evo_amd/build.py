@@ -3,6 +3,10 @@
 
   lib/libbatmobile_hip.so         HIP kernels + C ABI (include/batmobile_hip.h),
                                   hipcc --offload-arch=gfx950
+  lib/libbatteries_neighbor.so    the neighbor list alone (the reference's ctypes
+                                  library name: neighbor_list_cuda / _free /
+                                  _estimate_memory and the batteries_neighbor_list_*
+                                  entry points), from the same object
   python/_batmobile.so            torch extension (host code only) over the C ABI
 
 Usage:  python build.py [--force]
@@ -22,6 +26,7 @@ BUILD = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 PYDIR = os.path.join(HERE, "python")
 LIB = os.path.join(LIBDIR, "libbatmobile_hip.so")
+NL_LIB = os.path.join(LIBDIR, "libbatteries_neighbor.so")
 EXT = os.path.join(PYDIR, "_batmobile" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 HIP_SOURCES = ["sh.hip", "tp.hip", "mp.hip", "nl.hip", "mace.hip"]
@@ -74,6 +79,9 @@ def build_lib(force=False, jobs=4):
     if force or todo or _stale(LIB, objs):
         _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", LIB] + objs
              + ["-L" + os.path.join(ROCM, "lib"), "-lrocblas"])
+    nl_obj = os.path.join(BUILD, "nl.o")
+    if force or todo or _stale(NL_LIB, [nl_obj]):
+        _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", NL_LIB, nl_obj])
     return LIB
 
 
@@ -103,7 +111,7 @@ def build_ext(force=False):
 def build(force=False):
     build_lib(force=force)
     build_ext(force=force)
-    return LIB, EXT
+    return LIB, NL_LIB, EXT
 
 
 if __name__ == "__main__":

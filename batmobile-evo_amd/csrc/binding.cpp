@@ -253,7 +253,8 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> tensor_product_backward(
     TORCH_CHECK(input1.dtype() == torch::kFloat32 && input2.dtype() == torch::kFloat32 &&
                     weights.dtype() == torch::kFloat32 && grad_output.dtype() == torch::kFloat32,
                 "inputs must be float32");
-    TORCH_CHECK(C_out <= 256, "C_out must be <= 256");
+    TORCH_CHECK(C_in <= 1023 || C_out <= 128,
+                "tensor_product_backward: C_in must be <= 1023 when C_out > 128");
     auto opt = f32_like(input1);
     torch::Tensor g1, g2, gW;
     if (needs_input1_grad) g1 = torch::empty({N, C_in, 16}, opt);

@@ -809,19 +809,25 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_bwd_w_mfma_kernel(
 // h[n,ci,q] = sum_co W[path(q),ci,co] g[n,co,out(q)], gx = CG^T(h, y),
 // gy = sum_ci CG^T(h, x).  One thread per (row, ci); per-ci gy partials are
 // reduced in a fixed order.
+// STAGE_G: the rows' g is staged in LDS (kBRows rows per workgroup); otherwise
+// (C_out too large for that) one row per workgroup reads g from memory, where
+// the row's C_out x 64 bytes stay in cache for the workgroup's threads.
 constexpr int kBRows = 2;
+template <bool STAGE_G>
 __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ w,
     const float* __restrict__ g, float* __restrict__ gx, float* __restrict__ gy, int64_t n, int cin,
     int cout) {
+    constexpr int kRows = STAGE_G ? kBRows : 1;
     extern __shared__ float smem[];
-    float* sg = smem;                          // [kBRows][cout][16]
-    float* sgy = sg + kBRows * cout * 16;      // [kBRows][cin][16]
-    float* sy = sgy + kBRows * cin * 16;       // [kBRows][16]
-    const int64_t row0 = (int64_t)blockIdx.x * kBRows;
-    const int rows = (int)min<int64_t>(kBRows, n - row0);
+    float* sgy = smem;                         // [kRows][cin][16]
+    float* sy = sgy + kRows * cin * 16;        // [kRows][16]
+    float* sg = sy + kRows * 16;               // [kRows][cout][16] when STAGE_G
+    const int64_t row0 = (int64_t)blockIdx.x * kRows;
+    const int rows = (int)min<int64_t>(kRows, n - row0);
     const int tid = threadIdx.x;
-    for (int i = tid; i < rows * cout * 16; i += kTpBlock) sg[i] = g[row0 * cout * 16 + i];
+    if constexpr (STAGE_G)
+        for (int i = tid; i < rows * cout * 16; i += kTpBlock) sg[i] = g[row0 * cout * 16 + i];
     for (int i = tid; i < rows * 16; i += kTpBlock) sy[i] = y[row0 * 16 + i];
     __syncthreads();
     for (int it = tid; it < rows * cin; it += kTpBlock) {
@@ -830,7 +836,7 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
 #pragma unroll
         for (int q = 0; q < kNumSlots; ++q) h[q] = 0.0f;
         const float* wci = w + (int64_t)ci * cout;
-        const float* gr = sg + r * cout * 16;
+        const float* gr = STAGE_G ? sg + r * cout * 16 : g + (row0 + r) * cout * 16;
         for (int co = 0; co < cout; ++co) {
             float gv[16];
 #pragma unroll
@@ -998,26 +1004,12 @@ extern "C" size_t batteries_tensor_product_backward_workspace_bytes(int64_t N, i
            sizeof(float);
 }
 
-extern "C" int batteries_tensor_product_backward_l3(
-    const float* input1, const float* input2, const float* weights, const float* grad_output,
-    float* grad_input1, float* grad_input2, float* grad_weights, int64_t N, int C_in, int C_out,
-    void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (N < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
-    if (N == 0) {
-        if (grad_weights) {
-            const int64_t count = (int64_t)kNumPaths * C_in * C_out;
-            fill_zero_kernel<<<(unsigned)ceil_div(count, kTpBlock), kTpBlock, 0, stream>>>(
-                grad_weights, count);
-            return (int)hipGetLastError();
-        }
-        return BM_OK;
-    }
-    if (ceil_div(N, kTile) > INT32_MAX) return BM_ERR_ARG;
-    if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(grad_output)) & 15)
-        return BM_ERR_ARG;
-    const size_t need = batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out);
-    if (grad_weights && (!workspace || workspace_bytes < need)) return BM_ERR_WORKSPACE;
-    float* gw_part = static_cast<float*>(workspace);
+// The weighted backward on a given workspace (gw_part: the grad_W partials, at least
+// batteries_tensor_product_backward_workspace_bytes when grad_weights is computed).
+static int tp_backward_run(const float* input1, const float* input2, const float* weights,
+                           const float* grad_output, float* grad_input1, float* grad_input2,
+                           float* grad_weights, int64_t N, int C_in, int C_out, float* gw_part,
+                           hipStream_t stream) {
     if (grad_input1 || grad_input2) {
         if (C_out <= 128 && (int64_t)kNumPaths * C_in * C_out * 4 <= INT32_MAX) {
             // one wave per (path group, 16-channel tile), at most 8 per workgroup;
@@ -1047,11 +1039,21 @@ extern "C" int batteries_tensor_product_backward_l3(
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return (int)e;
         } else {
-            const size_t smem = sizeof(float) *
-                                ((size_t)kBRows * C_out * 16 + (size_t)kBRows * C_in * 16 + kBRows * 16);
-            if (smem > 64 * 1024) return BM_ERR_ARG;
-            tp_weighted_backward_xy_kernel<<<(unsigned)ceil_div(N, kBRows), kTpBlock, smem, stream>>>(
-                input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+            // g staged in LDS while two rows of it fit in 64 KB beside the gy partials;
+            // above that one row per workgroup with g read from memory (no bound on C_out)
+            const size_t staged = sizeof(float) * ((size_t)kBRows * C_out * 16 +
+                                                   (size_t)kBRows * C_in * 16 + kBRows * 16);
+            const size_t unstaged = sizeof(float) * ((size_t)C_in * 16 + 16);
+            if (staged <= 64 * 1024) {
+                tp_weighted_backward_xy_kernel<true>
+                    <<<(unsigned)ceil_div(N, kBRows), kTpBlock, staged, stream>>>(
+                        input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in,
+                        C_out);
+            } else {
+                if (unstaged > 64 * 1024 || N > INT32_MAX) return BM_ERR_ARG;  // C_in > 1023
+                tp_weighted_backward_xy_kernel<false><<<(unsigned)N, kTpBlock, unstaged, stream>>>(
+                    input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
+            }
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return (int)e;
         }
@@ -1073,4 +1075,37 @@ extern "C" int batteries_tensor_product_backward_l3(
         if (e != hipSuccess) return (int)e;
     }
     return BM_OK;
+}
+
+// Argument checks shared by both entry points; N = 0 fills grad_weights with zeros.
+// Returns 1 when the call is complete (nothing more to launch).
+static int tp_backward_check(const float* input1, const float* grad_output, float* grad_weights,
+                             int64_t N, int C_in, int C_out, hipStream_t stream) {
+    if (N < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
+    if (N == 0) {
+        if (grad_weights) {
+            const int64_t count = (int64_t)kNumPaths * C_in * C_out;
+            fill_zero_kernel<<<(unsigned)ceil_div(count, kTpBlock), kTpBlock, 0, stream>>>(
+                grad_weights, count);
+            const hipError_t e = hipGetLastError();
+            return e != hipSuccess ? (int)e : 1;
+        }
+        return 1;
+    }
+    if (ceil_div(N, kTile) > INT32_MAX) return BM_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(grad_output)) & 15)
+        return BM_ERR_ARG;
+    return BM_OK;
+}
+
+extern "C" int batteries_tensor_product_backward_l3(
+    const float* input1, const float* input2, const float* weights, const float* grad_output,
+    float* grad_input1, float* grad_input2, float* grad_weights, int64_t N, int C_in, int C_out,
+    void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const int rc = tp_backward_check(input1, grad_output, grad_weights, N, C_in, C_out, stream);
+    if (rc != BM_OK) return rc == 1 ? BM_OK : rc;
+    const size_t need = batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out);
+    if (grad_weights && (!workspace || workspace_bytes < need)) return BM_ERR_WORKSPACE;
+    return tp_backward_run(input1, input2, weights, grad_output, grad_input1, grad_input2,
+                           grad_weights, N, C_in, C_out, static_cast<float*>(workspace), stream);
 }

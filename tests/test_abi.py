@@ -33,6 +33,18 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_reference_named_neighbor_library():
+    """libbatteries_neighbor.so, the name the reference's ctypes callers load
+    (benchmarks/benchmark_neighbor_list.py:18-22, benchmark_e2e_mace.py:38), exports the
+    reference's three neighbor-list symbols."""
+    nl = ctypes.CDLL(os.path.join(REPO, "batmobile-evo_amd", "lib", "libbatteries_neighbor.so"))
+    for n in ("neighbor_list_cuda", "neighbor_list_free", "neighbor_list_estimate_memory"):
+        assert hasattr(nl, n)
+    nl.neighbor_list_estimate_memory.restype = ctypes.c_size_t
+    nl.neighbor_list_estimate_memory.argtypes = [ctypes.c_int64, ctypes.c_float, ctypes.c_float]
+    assert nl.neighbor_list_estimate_memory(1000, 0.05, 5.0) > 0
+
+
 def test_host_only_entry_points():
     lib = ctypes.CDLL(LIB)
     assert lib.batteries_get_num_paths_l3() == 34

@@ -19,6 +19,7 @@ pytestmark = pytest.mark.gpu
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(REPO, "batmobile-evo_amd", "lib", "libbatmobile_hip.so")
+NL_LIB = os.path.join(REPO, "batmobile-evo_amd", "lib", "libbatteries_neighbor.so")
 
 
 def _random_graph(n, e, c, seed):
@@ -87,6 +88,13 @@ def test_sh_tp_scatter_empty_rows_and_edges(bm, dev):
     # no edges at all -> zeros
     z = bm.sh_tp_scatter(vec[:0].to(dev), x, src[:0].to(dev), torch.zeros(n + 1, dtype=torch.int64, device=dev))
     assert torch.count_nonzero(z).item() == 0 and tuple(z.shape) == (n, c, 16)
+    # no source rows and no edges -> zeros for every destination (simple and weighted)
+    rp0 = torch.zeros(n + 1, dtype=torch.int64, device=dev)
+    z = bm.sh_tp_scatter(vec[:0].to(dev), x[:0], src[:0].to(dev), rp0)
+    assert torch.count_nonzero(z).item() == 0 and tuple(z.shape) == (n, c, 16)
+    w = torch.randn(34, c, 8, generator=gen(6)).to(dev)
+    z = bm.sh_tp_scatter_weighted(vec[:0].to(dev), x[:0], w, src[:0].to(dev), rp0)
+    assert torch.count_nonzero(z).item() == 0 and tuple(z.shape) == (n, 8, 16)
 
 
 def test_edge_index_to_csr(bm, dev):
@@ -150,6 +158,24 @@ def test_neighbor_list_bit_exact(bm, dev, n):
         np.testing.assert_array_equal(vec, bv)
 
 
+def test_neighbor_list_reference_cases(bm, dev):
+    """The reference's correctness cases (tests/test_neighbor_list.cu:264-266: N = 100, 500,
+    1000, density 0.05, cutoff 5, std::mt19937(42) positions from tests/golden/): bit-exact
+    against the C restatement and against brute force."""
+    from test_oracle_nl_mp import reference_nl_cases
+    cases, cutoff = reference_nl_cases()
+    for n, box, pos in cases:
+        print(f"reference NL case N={n}", flush=True)
+        cell = torch.diag(torch.tensor([box, box, box], dtype=torch.float32))
+        ei, vec, off = _nl_gpu(bm, dev, torch.from_numpy(pos), cell, cutoff)
+        s, d, v = onl.cell_list(pos, cell.numpy(), cutoff)
+        np.testing.assert_array_equal(ei, np.stack([s, d]))
+        np.testing.assert_array_equal(vec, v)
+        bs, bd, bv = onl.brute_force(pos, cell.numpy(), cutoff)
+        np.testing.assert_array_equal(ei, np.stack([bs, bd]))
+        np.testing.assert_array_equal(vec, bv)
+
+
 def test_neighbor_list_dense_long_rows_and_chunked_cells(bm, dev):
     """3000 atoms in a 12 A box with r_c = 4 A: 3 bins per axis, so every cell's
     27-cell candidate list is the whole system (> 2048 staged per chunk), and
@@ -199,15 +225,17 @@ def test_exclusive_scan_c_abi(bm, dev, n):
     np.testing.assert_array_equal(out.cpu().numpy(), want)
 
 
-def test_neighbor_list_reference_c_abi(bm, dev):
-    """ctypes use as in reference benchmarks/benchmark_neighbor_list.py:18-47."""
+@pytest.mark.parametrize("libpath", [NL_LIB, LIB])
+def test_neighbor_list_reference_c_abi(bm, dev, libpath):
+    """ctypes use as in reference benchmarks/benchmark_neighbor_list.py:18-47, through the
+    reference's library name (libbatteries_neighbor.so) and the full library."""
 
     class Result(ctypes.Structure):
         _fields_ = [("edge_index", ctypes.c_void_p), ("edge_vectors", ctypes.c_void_p),
                     ("num_edges", ctypes.c_int64), ("d_edge_index", ctypes.c_void_p),
                     ("d_edge_vectors", ctypes.c_void_p)]
 
-    lib = ctypes.CDLL(LIB)
+    lib = ctypes.CDLL(libpath)
     lib.neighbor_list_cuda.restype = ctypes.c_int
     lib.neighbor_list_cuda.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
                                        ctypes.c_bool, ctypes.POINTER(Result), ctypes.c_void_p]

@@ -136,6 +136,8 @@ def _tp_backward_oracle_chunked(x, y, w, g, chunk=2000):
     (1, 16, 16),
     (40, 20, 100),     # C_out in (64, 128]: the 128-channel grad_output tile
     (20, 8, 160),      # C_out > 128: the per-(row, channel) grad_x / grad_y kernel
+    (9, 24, 320),      # C_out above the reference binding's sizes, g staged in LDS
+    (5, 12, 1100),     # g of two rows over 64 KB: one row per workgroup, g read from memory
     (33, 80, 24),      # 15 (group, channel-tile) units on 8 waves: waves loop over units
     (45, 32, 48),      # single-tile workgroups of the two-tile kernel, the last tile partly past N
     (35, 64, 20),      # the same with C_in = 64 and C_out not a multiple of 16

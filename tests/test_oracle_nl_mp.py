@@ -22,6 +22,34 @@ def test_cell_list_equals_brute_force(n):
         np.testing.assert_array_equal(u, v)
 
 
+def reference_nl_cases():
+    """Positions of the reference's correctness cases (tests/test_neighbor_list.cu:18-27,
+    264-266: std::mt19937(42), density 0.05, N = 100, 500, 1000), written by
+    tests/golden/make_nl_fixtures.py."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "nl_mt19937_positions.json")
+    d = json.load(open(path))
+    return [(c["N"], np.float32(c["box"]), np.asarray(c["positions"], dtype=np.float32))
+            for c in d["cases"]], float(d["cutoff"])
+
+
+def test_reference_cases_cell_list_equals_brute_force():
+    """The reference's own cases: cell list == brute force (its check, :30-68), bit-exact."""
+    cases, cutoff = reference_nl_cases()
+    for n, box, pos in cases:
+        assert pos.shape == (n, 3) and pos.min() >= 0 and pos.max() < box
+        cell = np.diag([box, box, box]).astype(np.float32)
+        a = nl.cell_list(pos, cell, cutoff)
+        b = nl.brute_force(pos, cell, cutoff)
+        for u, v in zip(a, b):
+            np.testing.assert_array_equal(u, v)
+        # ~ density * 4/3 pi r^3 = 26 neighbours per atom, symmetric
+        assert 20 * n < a[0].size < 32 * n
+        assert a[0].size == np.sum(a[0] != a[1])
+
+
 def test_self_loops_and_symmetry():
     pos, cell = _box(300, 1)
     s, d, v = nl.cell_list(pos, cell, 5.0, self_loops=True)
