@@ -48,6 +48,7 @@ void check_status(int rc, const char* what) {
     if (rc == BATMOBILE_HIP_ERR_ARG) TORCH_CHECK(false, what, ": invalid argument");
     if (rc == BATMOBILE_HIP_ERR_WORKSPACE) TORCH_CHECK(false, what, ": workspace too small");
     if (rc == BATMOBILE_HIP_ERR_BLAS) TORCH_CHECK(false, what, ": rocBLAS call failed");
+    if (rc == BATMOBILE_HIP_ERR_SCRATCH) TORCH_CHECK(false, what, ": larger than the static scratch");
     TORCH_CHECK(false, "HIP error in ", what, ": ", hipGetErrorString(static_cast<hipError_t>(rc)));
 }
 

@@ -8,6 +8,8 @@
 #include "common.h"
 #include "batmobile_hip.h"
 
+#include <mutex>
+
 namespace bmhip {
 
 constexpr int kTpBlock = 256;
@@ -1108,4 +1110,59 @@ extern "C" int batteries_tensor_product_backward_l3(
     if (grad_weights && (!workspace || workspace_bytes < need)) return BM_ERR_WORKSPACE;
     return tp_backward_run(input1, input2, weights, grad_output, grad_input1, grad_input2,
                            grad_weights, N, C_in, C_out, static_cast<float*>(workspace), stream);
+}
+
+// ---------------------------------------------------------------------------
+// The same backward without any allocation: the grad_W partials live in
+// `scratch`, a file-scope device array of BATMOBILE_HIP_NOALLOC_SCRATCH_BYTES that
+// each GPU holds (its own copy) from the library's load until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory: the
+// device address comes from hipGetSymbolAddress, resolved once per device (with
+// that device current) on the first call there and kept in scratch_dev[].  Every
+// call on one GPU shares that GPU's array; each call writes every partial it
+// reads, so nothing needs clearing, and calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[BATMOBILE_HIP_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices];
+
+int scratch_address(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return BM_ERR_ARG;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return (int)hipErrorInvalidSymbol;
+        scratch_dev[dev] = p;
+    }
+    *out = static_cast<float*>(scratch_dev[dev]);
+    return BM_OK;
+}
+}  // namespace
+
+extern "C" int batteries_tensor_product_backward_l3_noalloc(
+    const float* input1, const float* input2, const float* weights, const float* grad_output,
+    float* grad_input1, float* grad_input2, float* grad_weights, int64_t N, int C_in, int C_out,
+    hipStream_t stream) {
+    // size limit first: a rejected call touches no device state
+    if (N > 0 && C_in > 0 && C_out > 0 && grad_weights &&
+        batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out) >
+            (size_t)BATMOBILE_HIP_NOALLOC_SCRATCH_BYTES)
+        return BATMOBILE_HIP_ERR_SCRATCH;
+    const int rc = tp_backward_check(input1, grad_output, grad_weights, N, C_in, C_out, stream);
+    if (rc != BM_OK) return rc == 1 ? BM_OK : rc;
+    float* part = nullptr;
+    if (grad_weights) {
+        const int e = scratch_address(&part);
+        if (e != BM_OK) return e;
+    }
+    return tp_backward_run(input1, input2, weights, grad_output, grad_input1, grad_input2,
+                           grad_weights, N, C_in, C_out, part, stream);
 }

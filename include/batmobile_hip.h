@@ -8,10 +8,14 @@
  *   - Work is enqueued on `stream` and is asynchronous unless stated.
  *   - Return value: 0 on success, a hipError_t value (> 0) on a launch/runtime
  *     error, BATMOBILE_HIP_ERR_ARG (-1) for invalid arguments, BATMOBILE_HIP_ERR_WORKSPACE (-2) for a
- *     missing or too small workspace, BATMOBILE_HIP_ERR_BLAS (-3) for a rocBLAS failure.
+ *     missing or too small workspace, BATMOBILE_HIP_ERR_BLAS (-3) for a rocBLAS failure,
+ *     BATMOBILE_HIP_ERR_SCRATCH (-4) for a call too large for the static scratch of
+ *     the no-allocation entry point.
  *   - No function allocates device memory except the reference-compatible
  *     neighbor_list_cuda(); where scratch is needed the caller passes a
- *     workspace whose size is given by the matching *_workspace_bytes().  The
+ *     workspace whose size is given by the matching *_workspace_bytes(), except
+ *     batteries_tensor_product_backward_l3_noalloc(), whose scratch is a static
+ *     device array.  The
  *     MACE layer's plain GEMMs run on rocBLAS: its first call on a device
  *     creates that device's rocBLAS handle (rocBLAS allocates its own
  *     workspace then).
@@ -37,6 +41,11 @@ extern "C" {
 #define BATMOBILE_HIP_ERR_ARG -1
 #define BATMOBILE_HIP_ERR_WORKSPACE -2
 #define BATMOBILE_HIP_ERR_BLAS -3
+#define BATMOBILE_HIP_ERR_SCRATCH -4 /* the call needs more than the static scratch holds */
+
+/* Size of the static device scratch of batteries_tensor_product_backward_l3_noalloc
+ * (24 MiB per GPU, held from the library's load until the process ends). */
+#define BATMOBILE_HIP_NOALLOC_SCRATCH_BYTES (24u << 20)
 
 /* ---------------------------------------------------------------------------
  * Spherical harmonics, L_max in [0, 6]
@@ -104,6 +113,24 @@ int batteries_tensor_product_backward_l3(const float* input1, const float* input
                                          float* grad_weights, int64_t N, int C_in, int C_out,
                                          void* workspace, size_t workspace_bytes,
                                          hipStream_t stream);
+
+/* The backward above without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments and results
+ * as batteries_tensor_product_backward_l3 minus the workspace: the grad_W partials
+ * live in a static device array of BATMOBILE_HIP_NOALLOC_SCRATCH_BYTES per GPU.
+ * Returns BATMOBILE_HIP_ERR_SCRATCH (and touches nothing) when grad_weights is
+ * requested and batteries_tensor_product_backward_workspace_bytes(N, C_in, C_out)
+ * exceeds it.  The partials fit for every N when 3 ceil(C_in/16) ceil(C_out/64)
+ * <= 512 (e.g. C_in = C_out = 256).  The first call on a device
+ * resolves the array's device address (hipGetSymbolAddress, no allocation by this
+ * library); make it outside graph capture.  All calls on one GPU share the array,
+ * so calls that overlap on one GPU (concurrent streams, threads) race. */
+int batteries_tensor_product_backward_l3_noalloc(const float* input1, const float* input2,
+                                                 const float* weights, const float* grad_output,
+                                                 float* grad_input1, float* grad_input2,
+                                                 float* grad_weights, int64_t N, int C_in,
+                                                 int C_out, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Fused SH + TP, scatter-add, CSR

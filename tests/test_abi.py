@@ -45,6 +45,18 @@ def test_reference_named_neighbor_library():
     assert nl.neighbor_list_estimate_memory(1000, 0.05, 5.0) > 0
 
 
+def test_noalloc_backward_rejects_oversize_before_any_device_call():
+    """The no-allocation backward refuses a call whose grad_W partials exceed its static
+    scratch (24 MiB) with BATMOBILE_HIP_ERR_SCRATCH, before touching the device."""
+    lib = ctypes.CDLL(LIB)
+    f = lib.batteries_tensor_product_backward_l3_noalloc
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_void_p]
+    one = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    assert f(one, one, one, one, None, None, one, 100000, 1024, 1024, None) == -4
+
+
 def test_host_only_entry_points():
     lib = ctypes.CDLL(LIB)
     assert lib.batteries_get_num_paths_l3() == 34
