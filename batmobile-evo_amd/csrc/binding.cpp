@@ -664,6 +664,18 @@ torch::Tensor selftest_mfma_16x16x4(const torch::Tensor& A, const torch::Tensor&
     return D;
 }
 
+torch::Tensor selftest_mfma_4x4x1_bcast(const torch::Tensor& A, const torch::Tensor& B) {
+    TORCH_CHECK(A.numel() == 64 && B.numel() == 64 && A.dtype() == torch::kFloat32 &&
+                    B.dtype() == torch::kFloat32,
+                "A [64] and B [64] float32");
+    torch::Tensor D = torch::empty({16, 64, 4}, f32_like(A));
+    const c10::DeviceGuard guard(A.device());
+    check_status(batteries_selftest_mfma_4x4x1_bcast(cptr<float>(A, "A"), cptr<float>(B, "B"),
+                                                     mptr<float>(D, "D"), current_stream(A)),
+                 "selftest_mfma_4x4x1_bcast");
+    return D;
+}
+
 // ---------------------------------------------------------------------------
 // MACE-style interaction layer with per-edge radial weights (no single
 // reference function: benchmarks/benchmark_e2e_mace.py:281-434 composes the
@@ -915,4 +927,6 @@ PYBIND11_MODULE(_batmobile, m) {
           "edge_weights the per-edge weights are not recomputed; order as for mace_forward");
     m.def("selftest_mfma_16x16x4", &selftest_mfma_16x16x4, py::arg("A"), py::arg("B"),
           "D = A @ B through one v_mfma_f32_16x16x4f32 (lane-layout self test)");
+    m.def("selftest_mfma_4x4x1_bcast", &selftest_mfma_4x4x1_bcast, py::arg("A"), py::arg("B"),
+          "D[k, l, r]: one v_mfma_f32_4x4x1_16b_f32 with A of block k broadcast (layout check)");
 }

@@ -42,6 +42,18 @@ __device__ __forceinline__ v4f mfma1(float a, float b, v4f acc) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// v_mfma_f32_4x4x1_16b_f32 with the A operand of one block broadcast to all 16
+// blocks (CBSZ = 4, ABID = the source block): block b (lanes 4b .. 4b + 3)
+// accumulates the 4x4 outer product D_b[i][j] += A[i] B_b[j], with A[i] read from
+// lane 4 ABID + i and B_b[j] from lane 4b + j; lane 4b + j holds D_b[r][j] in
+// element r of the accumulator.
+// ---------------------------------------------------------------------------
+template <int ABID>
+__device__ __forceinline__ v4f mfma_4x4_bcast(float a, float b, v4f acc) {
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, acc, 4, ABID, 0);
+}
+
 // Raw buffer loads: 32-bit lane offset (VGPR) + uniform offset (SGPR) from a
 // base address, reads past num_records bytes return 0.
 constexpr int kBufferDword3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3

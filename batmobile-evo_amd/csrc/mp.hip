@@ -599,9 +599,29 @@ __global__ void selftest_mfma_kernel(const float* __restrict__ A, const float* _
     for (int r = 0; r < 4; ++r) D[(4 * (l >> 4) + r) * 16 + (l & 15)] = acc[r];
 }
 
+// D[abid][l][r] = the accumulator of mfma_4x4_bcast<abid>(A[l], B[l], 0) in lane l
+__global__ void selftest_mfma_4x4_bcast_kernel(const float* __restrict__ A,
+                                               const float* __restrict__ B, float* __restrict__ D) {
+    const int l = threadIdx.x;
+    const float a = A[l], b = B[l];
+    static_for<16>([&](auto kk) {
+        constexpr int k = decltype(kk)::value;
+        const v4f d = mfma_4x4_bcast<k>(a, b, v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int r = 0; r < 4; ++r) D[(k * 64 + l) * 4 + r] = d[r];
+    });
+}
+
 }  // namespace bmhip
 
 using namespace bmhip;
+
+extern "C" int batteries_selftest_mfma_4x4x1_bcast(const float* A, const float* B, float* D,
+                                                   hipStream_t stream) {
+    if (!A || !B || !D) return BM_ERR_ARG;
+    selftest_mfma_4x4_bcast_kernel<<<1, 64, 0, stream>>>(A, B, D);
+    return (int)hipGetLastError();
+}
 
 extern "C" int batteries_selftest_mfma_16x16x4(const float* A, const float* B, float* D,
                                                hipStream_t stream) {
@@ -1085,129 +1105,33 @@ extern "C" int batteries_sh_tp_scatter_scheduled(const float* edge_vectors,
 //   out[d, co, o] = sum_{e -> d} TP_W(X[src_e], Y(v_e))[co, o].
 // Because W is shared, the sum over the edges of d moves in front of both the
 // CG contraction and the channel mixing:
-//   S[d, ci, a, b] = sum_{e -> d} X[src_e, ci, a] Y_e[b]              MFMA over edges
+//   S[d, ci, a, b] = sum_{e -> d} X[src_e, ci, a] Y_e[b]              MFMA 16x16x4 over edges
 //   T[d, q, ci]    = sum_{(a, b) in slot q} c S[d, ci, a, b]           CG table, VALU
-//   out[d, co, o]  = sum_{q -> o} sum_ci W[p(q), ci, co] T[d, q, ci]   MFMA (tp.hip)
+//   out[d, co, o]  = sum_{q -> o} sum_ci W[p(q), ci, co] T[d, q, ci]   MFMA 4x4x1 (16 blocks)
 // Work: 2 * 256 * C_in flops per edge (S), 2 * 611 * C_in + 2 * 156 * C_in * C_out per
-// destination (T, mixing).  T is [chunk][block][slot][16][16]: 16-channel chunks of
-// C_in (zero past C_in), destinations by their position in the processing order
-// (padded to a multiple of 16) in blocks of 16 positions, slots in fwd_slot_pos
-// order, so that the mixing kernel's operand loads and the path-sum kernel's stores
-// are contiguous 1 KB / 256 B blocks (whole 128-byte lines: a load that uses half of
-// each line it touches runs at half the rate) and slot offsets are compile-time
-// constants.
+// destination (T, mixing).
+//
+// One workgroup (4 waves) owns 4 destinations at consecutive positions of the
+// processing order and 64 output channels, and walks C_in in 16-channel chunks.
+// Per chunk:
+//   S phase: wave w sums channels c0 + 4w .. c0 + 4w + 3 of all four destinations
+//     (every wave does the same work), four edges per k-step:  MFMA j takes
+//     A[i][g] = X[src of edge g][c0 + 4w + i / 4][4 (i % 4) + j] (one float4 gather per
+//     lane) and B[g][i] = Y[edge g][i], so lane (g, i) ends with S[ch = 4w + g][a = 4r + j]
+//     [b = i] in element r of acc[j]; each destination's S goes to LDS row (ch, dd).
+//   contraction + mixing: lane l = 4 ch + dd reads row (ch, dd), contracts the CG blocks
+//     (l1, l2) of its wave and, for each slot q of a path p, issues 16 MFMAs
+//     acc[out(q)] += T[q][dd'][c0 + k] (x) W[p][c0 + k][co0 + lane'], k = 0..15, where the
+//     T operand of block k (lanes 4k .. 4k + 3: channel k, destinations 0..3) is broadcast
+//     to all 16 blocks (CBSZ = 4, ABID = k) and block b's B operand is W for output
+//     channels co0 + 4b .. 4b + 3.  T never leaves registers.
+// The waves' CG blocks carry 39 slots each (624 MFMAs per chunk); each path's W rows
+// (16 x 256 contiguous bytes) are loaded one path ahead.  At the end the four waves'
+// accumulators (lane l: destination r, output channel co0 + l, output component o) are
+// summed in LDS in a fixed order, and wave r stores destination r: deterministic, no
+// atomics.
 // ---------------------------------------------------------------------------
 namespace bmhip {
-
-// Blocks [0, edge_blocks): Y and the source row of CSR slot k (edge perm[k] when
-// perm is given), so that the path-sum kernel reads both without indirection.
-// Blocks past them: wt[chunk][p][co][16] = W[p][16 chunk + i][co], zero past cin (the
-// mixing kernel's B operand: 16 output channels x 16 input channels = 1 KB contiguous).
-__global__ __launch_bounds__(256) void mp_edge_prep_kernel(
-    const float* __restrict__ vec, const int64_t* __restrict__ src_idx,
-    const int64_t* __restrict__ perm, int64_t n_edges, int normalize, float* __restrict__ yc,
-    int* __restrict__ srcc, int64_t edge_blocks, const float* __restrict__ w,
-    float* __restrict__ wt, int cin, int cout, int cp) {
-    if ((int64_t)blockIdx.x >= edge_blocks) {
-        const int64_t i = ((int64_t)blockIdx.x - edge_blocks) * 256 + threadIdx.x;
-        if (i >= (int64_t)kNumPaths * cout * cp) return;
-        const int cl = (int)(i & 15);
-        const int64_t r = i >> 4;  // (chunk * 34 + p) * cout + co
-        const int co = (int)(r % cout);
-        const int64_t cpp = r / cout;
-        const int p = (int)(cpp % kNumPaths);
-        const int ci = (int)(cpp / kNumPaths) * 16 + cl;
-        wt[i] = ci < cin ? w[((int64_t)p * cin + ci) * cout + co] : 0.0f;
-        return;
-    }
-    const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (k >= n_edges) return;
-    const int64_t e = perm ? perm[k] : k;
-    float x = vec[e * 3 + 0], y = vec[e * 3 + 1], z = vec[e * 3 + 2];
-    if (normalize) normalize3(x, y, z);
-    float Y[16];
-    sh_forward<3>(x, y, z, Y);
-    float4* o = reinterpret_cast<float4*>(yc + k * 16);
-    o[0] = make_float4(Y[0], Y[1], Y[2], Y[3]);
-    o[1] = make_float4(Y[4], Y[5], Y[6], Y[7]);
-    o[2] = make_float4(Y[8], Y[9], Y[10], Y[11]);
-    o[3] = make_float4(Y[12], Y[13], Y[14], Y[15]);
-    srcc[k] = (int)src_idx[e];
-}
-
-// S of one (destination, channel) in LDS: 16 rows b of 16 a, the four 16-byte
-// quads of row b at positions quad ^ ps_swz(b), rows of successive channels
-// kPsStride floats apart.  The MFMA-layout writes (8 lanes = 8 values of b) and
-// the contraction's reads (8 lanes = 8 channels) are then free of bank conflicts.
-constexpr int kPsStride = 260;
-// T is [chunk][16-position block][slot][16 positions][16 channels]: one slot of a
-// block is 1 KB, so slot offsets are compile-time constants.
-constexpr int kTSlotBytes = 16 * 16 * 4;
-constexpr int kTBlockBytes = kNumSlots * kTSlotBytes;
-__host__ __device__ constexpr int ps_swz(int b) { return (b >> 1) & 3; }
-
-// CG blocks (l1, l2) contracted by each wave: 166, 149, 149, 147 CG terms.
-constexpr int kPsBlocks[4][5][2] = {{{1, 0}, {3, 1}, {3, 3}, {-1, -1}, {-1, -1}},
-                                    {{0, 2}, {1, 3}, {2, 3}, {3, 0}, {-1, -1}},
-                                    {{0, 0}, {0, 1}, {0, 3}, {1, 2}, {3, 2}},
-                                    {{1, 1}, {2, 0}, {2, 1}, {2, 2}, {-1, -1}}};
-
-// The slots of the paths (L1, L2, *) for this lane's (destination, channel):
-// reads S[a in l1][b in l2], contracts with the CG terms, stores slot q at byte
-// toff + pos(q) * 1 KB of the chunk's T (the slot offset is a compile-time
-// constant in a scalar register).
-template <int L1, int L2>
-__device__ __forceinline__ void ps_block(const float* sSrow, __amdgpu_buffer_rsrc_t tr, int toff,
-                                         bool store, bool chan_ok) {
-    constexpr int a0 = L1 * L1, na = 2 * L1 + 1, b0 = L2 * L2, nb = 2 * L2 + 1;
-    constexpr int qa0 = a0 / 4, qa1 = (a0 + na - 1) / 4;
-    float s[nb][na];
-    static_for<nb>([&](auto bb) {
-        constexpr int b = b0 + decltype(bb)::value;
-        static_for<qa1 - qa0 + 1>([&](auto qq) {
-            constexpr int qa = qa0 + decltype(qq)::value;
-            const float4 v =
-                *reinterpret_cast<const float4*>(sSrow + b * 16 + (qa ^ ps_swz(b)) * 4);
-            const float vv[4] = {v.x, v.y, v.z, v.w};
-            static_for<4>([&](auto ii) {
-                constexpr int i = decltype(ii)::value;
-                constexpr int a = 4 * qa + i;
-                if constexpr (a >= a0 && a < a0 + na) s[b - b0][a - a0] = vv[i];
-            });
-        });
-    });
-    static_for<kNumPaths>([&](auto pp) {
-        constexpr int p = decltype(pp)::value;
-        if constexpr (kPathL[p][0] == L1 && kPathL[p][1] == L2) {
-            constexpr int no = 2 * kPathL[p][2] + 1;
-            float t[no];
-            static_for<no>([&](auto m) { t[decltype(m)::value] = 0.0f; });
-            static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto kk) {
-                constexpr CGEntry e = kCG[kPathEntry[p] + decltype(kk)::value];
-                constexpr int m = e.q - kPathSlot[p];
-                t[m] = fmaf(e.c, s[e.b - b0][e.a - a0], t[m]);
-            });
-            if (store) {
-                static_for<no>([&](auto mm) {
-                    constexpr int m = decltype(mm)::value;
-                    constexpr int pos = fwd_slot_pos(kPathSlot[p] + m);  // compile time
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(chan_ok ? t[m] : 0.0f),
-                                                          tr, toff, pos * kTSlotBytes, 0);
-                });
-            }
-        }
-    });
-}
-
-template <int W>
-__device__ __forceinline__ void ps_contract(const float* sSrow, __amdgpu_buffer_rsrc_t tr,
-                                            int toff, bool store, bool chan_ok) {
-    static_for<5>([&](auto kk) {
-        constexpr int k = decltype(kk)::value;
-        if constexpr (kPsBlocks[W][k][0] >= 0)
-            ps_block<kPsBlocks[W][k][0], kPsBlocks[W][k][1]>(sSrow, tr, toff, store, chan_ok);
-    });
-}
 
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
     const uint64_t u = (uint64_t)v;
@@ -1216,286 +1140,411 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// One workgroup per unit: 4 destinations at consecutive positions of `order`
-// and `cpw` consecutive 16-channel chunks.  Per chunk:
-// S phase: wave w sums the edges of destination w, four edges per k-step: lane
-// (g = lane / 16, i = lane % 16) supplies
-//   A[i][g] = X[src of edge g][c0 + 4t + i / 4][4 (i % 4) + j]   (MFMA (t, j), float4 over j)
-//   B[g][i] = Y[edge g][b = i]
-// so that MFMA (t, j) accumulates S[c0 + 4t + m / 4][a = 4 (m % 4) + j][b] in row m.
-// Lane (g, i) then holds S[c0 + 4t + g][all a][b = i] and writes it to LDS.
-// Contraction phase: lane (dd, ch) = (lane / 16, lane % 16) of every wave takes
-// destination dd and channel c0 + ch; wave w contracts its CG blocks.
-// The k-steps of a wave run through a four-stage load pipeline that continues
-// across chunks: the source index and Y of step i + 3, the source-row gathers of
-// steps i + 2 and i + 1, the MFMAs of step i.  The next chunk's first gathers are therefore
-// in flight during this chunk's contraction.
-__global__ __launch_bounds__(256, 2) void mp_path_sums_kernel(
-    const float* __restrict__ yc, const int* __restrict__ srcc, const float* __restrict__ X,
-    const int64_t* __restrict__ row_ptr, const int64_t* __restrict__ order, float* __restrict__ T,
-    int64_t n_dst, int64_t npad, int C, int cpw, int64_t n_units) {
-    __shared__ __attribute__((aligned(16))) float sS[4 * 16 * kPsStride];
-    const int64_t per_xcd = (n_units + 7) / 8;
-    const int64_t logical = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (logical >= n_units) return;
-    const int64_t nquad = (n_dst + 3) >> 2;
-    const int nchunk = (C + 15) >> 4;
-    const int cgrp = (int)(logical / nquad);  // chunk-group major: an XCD works on a
-    const int64_t quad = logical - cgrp * nquad;  // compact range of destinations
-    const int ch0 = cgrp * cpw;                   // first chunk of this unit
-    const int nch = min(cpw, nchunk - ch0);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i16 = lane & 15;
+// S of one (channel, destination) in LDS: 16 rows b of 16 a, the four 16-byte quads of
+// row b at positions quad ^ ps_swz(b), rows (ch, dd) at ch * 4 + dd, kPsStride floats
+// apart.  The S-phase writes (8 lanes = 8 values of b) and the contraction's reads
+// (8 lanes = 8 consecutive rows) are then free of bank conflicts.
+constexpr int kPsStride = 260;
+__host__ __device__ constexpr int ps_swz(int b) { return (b >> 1) & 3; }
 
-    int64_t r0 = 0, r1 = 0;
-    {
-        const int64_t pos = quad * 4 + w;
-        if (pos < n_dst) {
-            const int64_t d = order ? order[pos] : pos;
-            if (d >= 0 && d < n_dst) {  // an order entry out of range sums no edges
-                r0 = row_ptr[d];
-                r1 = row_ptr[d + 1];
-            }
-        }
-        r0 = uniform64(r0);
-        r1 = uniform64(r1);
-    }
-    const int deg = (int)(r1 - r0);
-    const int nst = (deg + 3) >> 2;  // k-steps per chunk
-    const int64_t rowf = (int64_t)C * 16;  // floats per source row
-    // CSR slot of this lane's edge in step s (past the row: its last edge, Y masked to 0)
-    auto slot = [&](int s) { return r0 + min(4 * s + g, deg - 1); };
-    auto gather = [&](int src, int chunk, float4(&xv)[4]) {
-        const float* rowp = X + (int64_t)src * rowf;
-        const int c0 = (ch0 + chunk) * 16;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            xv[t] = *reinterpret_cast<const float4*>(
-                rowp + min(c0 + 4 * t + (i16 >> 2), C - 1) * 16 + (i16 & 3) * 4);
-    };
-    // the step after (c, s), or (c, s) itself past the last step
-    auto next = [&](int& c, int& s) {
-        if (s + 1 < nst) {
-            ++s;
-        } else if (c + 1 < nch) {
-            ++c;
-            s = 0;
-        }
-    };
-    // pipeline state: stage A (source index, Y of the step three ahead), stage C
-    // (gathers of the step two ahead) and stage B (gathers of the next step)
-    int cA = 0, sA = 0, cC = 0, sC = 0;
-    int srcA = 0;
-    float yA = 0.f, yB = 0.f, yC = 0.f;
-    float4 xB[4], xC[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) xB[t] = xC[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (nst > 0) {
-        srcA = srcc[slot(0)];
-        yA = 4 * 0 + g < deg ? yc[slot(0) * 16 + i16] : 0.f;
-        gather(srcA, 0, xB);
-        yB = yA;
-        next(cA, sA);
-        srcA = srcc[slot(sA)];
-        yA = 4 * sA + g < deg ? yc[slot(sA) * 16 + i16] : 0.f;
-        cC = cA;
-        sC = sA;
-        gather(srcA, cC, xC);
-        yC = yA;
-        next(cA, sA);
-        srcA = srcc[slot(sA)];
-        yA = 4 * sA + g < deg ? yc[slot(sA) * 16 + i16] : 0.f;
-    }
-    v4f acc[4][4];
-    for (int c = 0; c < nch; ++c) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < nst; ++s) {
-            float4 xa[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                xa[t] = xB[t];
-                xB[t] = xC[t];
-            }
-            const float ya = yB;
-            yB = yC;
-            next(cC, sC);  // stage C: gathers of the step two ahead
-            gather(srcA, cC, xC);
-            yC = yA;
-            next(cA, sA);  // stage A: index and Y three steps ahead
-            srcA = srcc[slot(sA)];
-            {
-                const float yv = yc[slot(sA) * 16 + i16];
-                yA = 4 * sA + g < deg ? yv : 0.f;
-            }
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                acc[t][0] = mfma1(xa[t].x, ya, acc[t][0]);
-                acc[t][1] = mfma1(xa[t].y, ya, acc[t][1]);
-                acc[t][2] = mfma1(xa[t].z, ya, acc[t][2]);
-                acc[t][3] = mfma1(xa[t].w, ya, acc[t][3]);
-            }
-        }
-        if (c > 0) __syncthreads();  // the previous chunk's contraction reads are done
-        // S[c0 + 4t + g][a = 4r + j][b = i16] -> LDS block (w, 4t + g), row b, quad r
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            float* blk = sS + (w * 16 + 4 * t + g) * kPsStride + i16 * 16;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                *reinterpret_cast<float4*>(blk + ((r ^ ps_swz(i16)) * 4)) =
-                    make_float4(acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]);
-        }
-        __syncthreads();
-        // contraction: lane (dd, ch)
-        // the 4 positions x 16 channels of one slot are 256 contiguous bytes of T
-        const int dd = lane >> 4, ch = lane & 15;
-        const int c0 = (ch0 + c) * 16;
-        const int64_t pos = quad * 4 + dd;
-        const bool store = pos < n_dst;
-        const int64_t tchunk = npad * kNumSlots * 16;  // floats per chunk of T
-        const __amdgpu_buffer_rsrc_t tr =
-            buffer_rsrc(T + (int64_t)(ch0 + c) * tchunk, (uint32_t)(tchunk * 4));
-        const int toff = (int)(pos >> 4) * kTBlockBytes + ((int)(pos & 15) * 16 + ch) * 4;
-        const float* sSrow = sS + (dd * 16 + ch) * kPsStride;
-        const bool chan_ok = c0 + ch < C;
-        switch (w) {
-            case 0: ps_contract<0>(sSrow, tr, toff, store, chan_ok); break;
-            case 1: ps_contract<1>(sSrow, tr, toff, store, chan_ok); break;
-            case 2: ps_contract<2>(sSrow, tr, toff, store, chan_ok); break;
-            default: ps_contract<3>(sSrow, tr, toff, store, chan_ok); break;
-        }
-    }
-}
+// CG blocks (l1, l2) of each wave, 39 slots each (16 + 15 + 5 + 3, 16 + 15 + 7 + 1,
+// 15 + 15 + 9, 12 + 12 + 7 + 5 + 3); CG terms 130, 172, 200, 109.
+constexpr int kWfBlocks[4][5][2] = {{{2, 2}, {1, 2}, {0, 2}, {0, 1}, {-1, -1}},
+                                    {{3, 3}, {2, 1}, {0, 3}, {0, 0}, {-1, -1}},
+                                    {{2, 3}, {3, 2}, {1, 1}, {-1, -1}, {-1, -1}},
+                                    {{1, 3}, {3, 1}, {3, 0}, {2, 0}, {1, 0}}};
 
-// Mixing stage: out[order[r], co, o] = sum_{q: out(q) = o} sum_ci W[p(q), ci, co] T[., q, r, ci]
-// over positions r.  One wave per (16 positions, output component o, 64 output
-// channels), no LDS until the output: per slot q of o and 16-channel chunk, four
-// k-steps of
-//   D[r][co] += A[r][ci] B[ci][co],  A = T (lane (r = l % 16, k = l / 16): float4
-//   over ci = 4k .. 4k + 3),  B = wt (lane (k, co = l % 16), the same four ci)
-// for the four 16-channel tiles of co.  Each operand load is 1 KB contiguous.  A path
-// reaches o through one slot only, so every slot brings its own W.  Operands are
-// loaded kMixAhead slots ahead, across chunk boundaries.
-constexpr int kMixAhead = 2;
-constexpr int n_slots_out(int o) {
-    int c = 0;
-    for (int q = 0; q < kNumSlots; ++q) c += kSlotOut[q] == o ? 1 : 0;
-    return c;
+// The paths of wave W in processing order (blocks in kWfBlocks order, paths in path order).
+constexpr int wf_num_paths(int W) {
+    int n = 0;
+    for (int k = 0; k < 5; ++k)
+        for (int p = 0; p < kNumPaths; ++p)
+            if (kWfBlocks[W][k][0] >= 0 && kPathL[p][0] == kWfBlocks[W][k][0] &&
+                kPathL[p][1] == kWfBlocks[W][k][1])
+                ++n;
+    return n;
 }
-constexpr int slot_of_out(int o, int k) {
-    for (int q = 0; q < kNumSlots; ++q)
-        if (kSlotOut[q] == o) {
-            if (k == 0) return q;
-            --k;
-        }
+constexpr int wf_path(int W, int i) {
+    for (int k = 0; k < 5; ++k)
+        for (int p = 0; p < kNumPaths; ++p)
+            if (kWfBlocks[W][k][0] >= 0 && kPathL[p][0] == kWfBlocks[W][k][0] &&
+                kPathL[p][1] == kWfBlocks[W][k][1]) {
+                if (i == 0) return p;
+                --i;
+            }
     return -1;
 }
-
-template <int O>
-__device__ __forceinline__ void mix_component(const float* __restrict__ T,
-                                              const float* __restrict__ wt, float* sOut, int64_t n,
-                                              int64_t npad, int nchunk, int cout, int64_t row0,
-                                              int co0) {
-    constexpr int NS = n_slots_out(O);
-    static_assert(NS >= kMixAhead, "ring deeper than the slot list");
-    const int lane = threadIdx.x & 63, g4 = lane >> 4, i16 = lane & 15;
-    // buffer loads: lane offsets in VGPRs, (chunk, slot, path) offsets in SGPRs
-    const int64_t tchunk = (int64_t)kNumSlots * npad * 16;  // floats per chunk of T
-    const uint32_t tchunk_bytes = (uint32_t)(tchunk * sizeof(float));
-    const int toff = ((int)min<int64_t>(i16, n - 1 - row0) * 16 + 4 * g4) * 4;
-    const int tblock = (int)(row0 >> 4) * kTBlockBytes;  // bytes of the tile's block
-    const __amdgpu_buffer_rsrc_t wr =
-        buffer_rsrc(wt, (uint32_t)((int64_t)nchunk * kNumPaths * cout * 64));
-    const int wpath = cout * 64, wchunk = kNumPaths * cout * 64;
-    int wco[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) wco[t] = (min(co0 + 16 * t + i16, cout - 1) * 16 + 4 * g4) * 4;
-    v4f acc[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-    auto load = [&](int chunk, auto kk, float4& a, float4 (&b)[4]) {
-        constexpr int k = decltype(kk)::value;
-        constexpr int q = slot_of_out(O, k);
-        constexpr int pos = fwd_slot_pos(q);
-        constexpr int p = kSlotPath[q];
-        const __amdgpu_buffer_rsrc_t tr = buffer_rsrc(T + chunk * tchunk, tchunk_bytes);
-        a = buffer_ld4(tr, toff, tblock + pos * kTSlotBytes);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) b[t] = buffer_ld4(wr, wco[t], chunk * wchunk + p * wpath);
-    };
-    float4 hA[kMixAhead], hB[kMixAhead][4];  // first slots of the current chunk
-    static_for<kMixAhead>([&](auto jj) {
-        constexpr int j = decltype(jj)::value;
-        load(0, jj, hA[j], hB[j]);
-    });
-    for (int c = 0; c < nchunk; ++c) {
-        float4 oA[NS], oB[NS][4];
-        static_for<kMixAhead>([&](auto jj) {
-            constexpr int j = decltype(jj)::value;
-            oA[j] = hA[j];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) oB[j][t] = hB[j][t];
-        });
-        static_for<NS>([&](auto kk) {
-            constexpr int k = decltype(kk)::value;
-            constexpr int kn = k + kMixAhead;
-            if constexpr (kn < NS)
-                load(c, std::integral_constant<int, kn>{}, oA[kn], oB[kn]);
-            else
-                load(min(c + 1, nchunk - 1), std::integral_constant<int, kn - NS>{}, hA[kn - NS],
-                     hB[kn - NS]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[t] = mfma4(oA[k], oB[k][t], acc[t]);
-            // keep the ring: no load moves ahead of the slot it belongs to
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    }
-    // D[4 g4 + r][i16]: position 4 g4 + r of the tile, channel 16 t + i16 of the 64; the
-    // workgroup's four components of one (position, channel) meet in LDS
-    const int w = threadIdx.x >> 6;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sOut[((4 * g4 + r) * 64 + 16 * t + i16) * 4 + w] = acc[t][r];
+// does path i of wave W start a new CG block (l1, l2)?
+constexpr bool wf_new_block(int W, int i) {
+    if (i == 0) return true;
+    const int p = wf_path(W, i), q = wf_path(W, i - 1);
+    return kPathL[p][0] != kPathL[q][0] || kPathL[p][1] != kPathL[q][1];
 }
 
-// grid (4 x 16-position tiles, 64-channel tiles of C_out): block x is group G = x % 4 of
-// tile x / 4 (a tile's four blocks are dispatched together), wave w takes o = 4 G + w,
-// and the block stores float4 (o = 4 G .. 4 G + 3) per (destination, channel).
-__global__ __launch_bounds__(256) void mp_weighted_mix_kernel(const float* __restrict__ T,
-                                                              const float* __restrict__ wt,
-                                                              const int64_t* __restrict__ order,
-                                                              float* __restrict__ out, int64_t n,
-                                                              int64_t npad, int nchunk, int cout) {
-    __shared__ __attribute__((aligned(16))) float sOut[16 * 64 * 4];
-    const int G = blockIdx.x & 3;
-    const int64_t row0 = (int64_t)(blockIdx.x >> 2) * 16;
-    const int co0 = blockIdx.y * 64;
-    switch (G * 4 + (threadIdx.x >> 6)) {
-#define BM_MIX_CASE(o) \
-    case o: mix_component<o>(T, wt, sOut, n, npad, nchunk, cout, row0, co0); break;
-        BM_MIX_CASE(0) BM_MIX_CASE(1) BM_MIX_CASE(2) BM_MIX_CASE(3)
-        BM_MIX_CASE(4) BM_MIX_CASE(5) BM_MIX_CASE(6) BM_MIX_CASE(7)
-        BM_MIX_CASE(8) BM_MIX_CASE(9) BM_MIX_CASE(10) BM_MIX_CASE(11)
-        BM_MIX_CASE(12) BM_MIX_CASE(13) BM_MIX_CASE(14)
-#undef BM_MIX_CASE
-        default: mix_component<15>(T, wt, sOut, n, npad, nchunk, cout, row0, co0); break;
-    }
-    __syncthreads();
-    // 16 positions x 64 channels of float4: four per thread
+// W rows of path p for the 16 channels of chunk c0: w[k] = W[p][min(c0 + k, cin - 1)][co]
+// (lane offset woff = the lane's output channel, clamped, in bytes).
+__device__ __forceinline__ void wf_load_w(__amdgpu_buffer_rsrc_t wr, int woff, int p, int c0,
+                                          int cin, int cout, float (&w)[16]) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = threadIdx.x + 256 * k;  // position i / 64, channel i % 64
-        const int64_t r = row0 + (i >> 6);
-        const int co = co0 + (i & 63);
-        if (r < n && co < cout) {
-            const int64_t d = order ? order[r] : r;
-            if (d >= 0 && d < n)  // an order entry out of range is not written
-                *reinterpret_cast<float4*>(out + (d * cout + co) * 16 + 4 * G) =
-                    *reinterpret_cast<const float4*>(sOut + i * 4);
+    for (int k = 0; k < 16; ++k)
+        w[k] = buffer_ld(wr, woff, (p * cin + min(c0 + k, cin - 1)) * cout * 4);
+}
+
+// Contraction of wave W's CG blocks for the lane's (channel, destination) row and the
+// mixing MFMAs of every slot.  wbuf[i & 1] holds path i's W; path i + 1's is loaded
+// before path i's products.
+template <int W>
+__device__ __forceinline__ void wf_contract_mix(const float* sSrow, __amdgpu_buffer_rsrc_t wr,
+                                                int woff, int c0, int cin, int cout,
+                                                float (&wbuf)[2][16], v4f (&acc)[16]) {
+    constexpr int NP = wf_num_paths(W);
+    float s[7][7];  // S[a in l1][b in l2] of the current block
+    static_for<NP>([&](auto ii) {
+        constexpr int i = decltype(ii)::value;
+        constexpr int p = wf_path(W, i);
+        constexpr int L1 = kPathL[p][0], L2 = kPathL[p][1], LO = kPathL[p][2];
+        constexpr int a0 = L1 * L1, na = 2 * L1 + 1, b0 = L2 * L2, nb = 2 * L2 + 1;
+        if constexpr (wf_new_block(W, i)) {
+            constexpr int qa0 = a0 / 4, qa1 = (a0 + na - 1) / 4;
+            static_for<nb>([&](auto bb) {
+                constexpr int b = b0 + decltype(bb)::value;
+                static_for<qa1 - qa0 + 1>([&](auto qq) {
+                    constexpr int qa = qa0 + decltype(qq)::value;
+                    const float4 v =
+                        *reinterpret_cast<const float4*>(sSrow + b * 16 + (qa ^ ps_swz(b)) * 4);
+                    const float vv[4] = {v.x, v.y, v.z, v.w};
+                    static_for<4>([&](auto jj) {
+                        constexpr int j = decltype(jj)::value;
+                        constexpr int a = 4 * qa + j;
+                        if constexpr (a >= a0 && a < a0 + na) s[a - a0][b - b0] = vv[j];
+                    });
+                });
+            });
         }
+        if constexpr (i + 1 < NP) {
+            constexpr int pn = wf_path(W, i + 1);
+            wf_load_w(wr, woff, pn, c0, cin, cout, wbuf[(i + 1) & 1]);
+            // keep the next path's loads here: sunk to their uses, each would wait on
+            // its own round trip
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        constexpr int no = 2 * LO + 1;
+        float t[no];
+        static_for<no>([&](auto m) { t[decltype(m)::value] = 0.0f; });
+        static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto kk) {
+            constexpr CGEntry e = kCG[kPathEntry[p] + decltype(kk)::value];
+            constexpr int m = e.q - kPathSlot[p];
+            t[m] = fmaf(e.c, s[e.a - a0][e.b - b0], t[m]);
+        });
+        static_for<16>([&](auto kk) {
+            constexpr int k = decltype(kk)::value;
+            static_for<no>([&](auto mm) {
+                constexpr int m = decltype(mm)::value;
+                acc[LO * LO + m] = mfma_4x4_bcast<k>(t[m], wbuf[i & 1][k], acc[LO * LO + m]);
+            });
+        });
+    });
+}
+
+// Step t < T of a tile: the CSR slot of its first edge (returned) and its number of
+// edges left from it (cnt; lane g takes edge g when g < cnt).  Destinations
+// 0..3 hold dg0..dg3 edges from slots r00..r03; steps cum1, cum2, cum3 onward belong to
+// destinations 1, 2, 3.  Values by argument, not through captured references: a select
+// between variables in memory becomes a load through a selected pointer.
+__device__ __forceinline__ int64_t wf_step_rows(int t, int cum1, int cum2, int cum3, int64_t r00,
+                                                int64_t r01, int64_t r02, int64_t r03, int dg0,
+                                                int dg1, int dg2, int dg3, int& cnt) {
+    const bool b1 = t >= cum1, b2 = t >= cum2, b3 = t >= cum3;
+    const int64_t r = b3 ? r03 : b2 ? r02 : b1 ? r01 : r00;
+    const int c = b3 ? cum3 : b2 ? cum2 : b1 ? cum1 : 0;
+    const int d = b3 ? dg3 : b2 ? dg2 : b1 ? dg1 : dg0;
+    cnt = d - 4 * (t - c);
+    return r + 4 * (t - c);
+}
+
+template <int W>
+__device__ __forceinline__ void wf_load_first(__amdgpu_buffer_rsrc_t wr, int woff, int c0, int cin,
+                                              int cout, float (&w)[16]) {
+    constexpr int p = wf_path(W, 0);
+    wf_load_w(wr, woff, p, c0, cin, cout, w);
+}
+
+// Edges of the tile staged in LDS at a time, in k-steps of 4 (160 edges): the Y and
+// source row of each step's four edges, computed once per tile and read by every chunk.
+constexpr int kWfSegSteps = 40;
+
+// BUF: source-row gathers as raw buffer loads with 32-bit offsets (X under 2 GiB).
+template <bool BUF>
+__global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
+    const float* __restrict__ vec, const int64_t* __restrict__ src_idx,
+    const int64_t* __restrict__ perm, const float* __restrict__ X, const float* __restrict__ Wt,
+    const int64_t* __restrict__ row_ptr, const int64_t* __restrict__ order, float* __restrict__ out,
+    int64_t n_dst, int cin, int cout, int64_t n_tiles, int normalize, uint32_t x_bytes) {
+    __shared__ __attribute__((aligned(16))) float sS[64 * kPsStride];
+    __shared__ __attribute__((aligned(16))) float sY[kWfSegSteps * 4 * 16];
+    __shared__ int sSrc[kWfSegSteps * 4];
+    const int64_t per_xcd = (n_tiles + 7) / 8;
+    const int64_t tile = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= n_tiles) return;
+    const int lane = threadIdx.x & 63, g = lane >> 4, i16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int co0 = blockIdx.y * 64;
+    const int nchunk = (cin + 15) >> 4;
+
+    // the tile's destinations: rows [r0, r0 + deg) of the CSR, k-steps per chunk.  Plain
+    // wave-uniform scalars (no arrays or structs, which the compiler may keep in memory
+    // and reach through pointers when a step selects among them).
+    auto dest_rows = [&](int k, int64_t& d, int64_t& r0, int& deg) {
+        const int64_t pos = tile * 4 + k;
+        int64_t dd = -1, a = 0, b = 0;
+        if (pos < n_dst) {
+            dd = order ? order[pos] : pos;
+            if (dd >= 0 && dd < n_dst) {  // an order entry out of range sums no edges
+                a = row_ptr[dd];
+                b = row_ptr[dd + 1];
+            } else {
+                dd = -1;
+            }
+        }
+        d = uniform64(dd);
+        r0 = uniform64(a);
+        deg = __builtin_amdgcn_readfirstlane((int)(b - a));
+    };
+    int64_t d0, d1, d2, d3, r00, r01, r02, r03;
+    int dg0, dg1, dg2, dg3;
+    dest_rows(0, d0, r00, dg0);
+    dest_rows(1, d1, r01, dg1);
+    dest_rows(2, d2, r02, dg2);
+    dest_rows(3, d3, r03, dg3);
+    const int cum1 = (dg0 + 3) >> 2, cum2 = cum1 + ((dg1 + 3) >> 2),
+              cum3 = cum2 + ((dg2 + 3) >> 2);
+    const int T = cum3 + ((dg3 + 3) >> 2);  // k-steps per chunk, the same in every chunk
+    // Steps are padded to T4, a multiple of the ring below, and staged in segments of at
+    // most kWfSegSteps; padding steps and lanes past a destination's last edge have Y = 0
+    // and source row 0 (a valid row).
+    const int T4 = (T + 3) & ~3;
+    const int nseg = (T4 + kWfSegSteps - 1) / kWfSegSteps;  // 0: the tile has no edges
+
+    // S rows of destinations without edges are zero for every chunk
+    auto zero_rows = [&](int k, int deg) {
+        if (deg == 0) {
+            float* row = sS + ((4 * w + g) * 4 + k) * kPsStride + i16 * 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<float4*>(row + r * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    zero_rows(0, dg0);
+    zero_rows(1, dg1);
+    zero_rows(2, dg2);
+    zero_rows(3, dg3);
+
+    // steps [s0, s0 + len) into LDS: thread k takes edge k % 4 of step s0 + k / 4
+    auto stage = [&](int s0, int len) {
+        for (int k = threadIdx.x; k < len * 4; k += 256) {
+            const int t = s0 + (k >> 2), ge = k & 3;
+            int64_t e = -1;
+            if (t < T) {
+                int cnt;
+                const int64_t base =
+                    wf_step_rows(t, cum1, cum2, cum3, r00, r01, r02, r03, dg0, dg1, dg2, dg3, cnt);
+                if (ge < cnt) e = perm ? perm[base + ge] : base + ge;
+            }
+            float Y[16];
+            int src = 0;
+            if (e >= 0) {
+                float x = vec[e * 3 + 0], y = vec[e * 3 + 1], z = vec[e * 3 + 2];
+                if (normalize) normalize3(x, y, z);
+                sh_forward<3>(x, y, z, Y);
+                src = (int)src_idx[e];
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) Y[q] = 0.f;
+            }
+            float4* yd = reinterpret_cast<float4*>(sY + k * 16);
+            yd[0] = make_float4(Y[0], Y[1], Y[2], Y[3]);
+            yd[1] = make_float4(Y[4], Y[5], Y[6], Y[7]);
+            yd[2] = make_float4(Y[8], Y[9], Y[10], Y[11]);
+            yd[3] = make_float4(Y[12], Y[13], Y[14], Y[15]);
+            sSrc[k] = src;
+        }
+    };
+    const uint32_t row_bytes = (uint32_t)cin * 64u;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), (short)0, BUF ? (int)x_bytes : 0, kBufferDword3);
+    // lane (g, i16) of a gather: channel 4 w + i16 / 4 of the chunk (clamped to the last
+    // channel), components 4 (i16 % 4) ..; goff is that byte offset inside a source row
+    auto chunk_off = [&](int chunk) {
+        return min(min(chunk, nchunk - 1) * 16 + 4 * w + (i16 >> 2), cin - 1) * 64 + (i16 & 3) * 16;
+    };
+    auto gather_at = [&](int goff, int src) {
+        if constexpr (BUF) {
+            return buffer_ld4(xr, (int)((uint32_t)src * row_bytes) + goff, 0);
+        } else {
+            return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(X) +
+                                                    (int64_t)src * row_bytes + goff);
+        }
+    };
+    auto gather = [&](int chunk, int src) { return gather_at(chunk_off(chunk), src); };
+    // the first destination boundary (end of a destination's steps) after step index b
+    auto next_boundary = [&](int b) {
+        return b < cum1 ? cum1 : b < cum2 ? cum2 : b < cum3 ? cum3 : b < T ? T : -1;
+    };
+
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wt, (uint32_t)((int64_t)kNumPaths * cin * cout * 4));
+    const int woff = min(co0 + lane, cout - 1) * 4;
+    const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+    v4f macc[16];
+#pragma unroll
+    for (int o = 0; o < 16; ++o) macc[o] = zero4;
+    float wbuf[2][16];
+
+    // A ring of 4 steps with static register names (the step loop is unrolled by 4):
+    // slot j holds, for the step t = j (mod 4) being consumed, its gather and Y (issued 4
+    // steps earlier); scur the source row of the next step to gather (read one step ahead).
+    float4 xring[4];
+    float yring[4];
+    int scur = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        xring[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        yring[j] = 0.f;
+    }
+    // ring refill target for local step u (< len + 5) of a segment of len (>= 4) steps in
+    // chunk c: past the segment, the matching step of a following chunk when the whole
+    // tile is one segment (its LDS data stays; with len = 4 that can be two chunks on),
+    // otherwise -1, a load that is never consumed (row 0, Y index 0).  Every index it
+    // returns lies inside the staged segment.
+    auto target = [&](int u, int len, int c, int& cn) {
+        cn = c;
+        if (u < len) return u;
+        if (nseg != 1) return -1;
+        while (u >= len) {
+            u -= len;
+            ++cn;
+        }
+        return cn < nchunk ? u : -1;
+    };
+    // slots 0..3: steps 0..3 of a segment of len (>= 4) steps in chunk c; scur: the step after
+    auto prime = [&](int c, int len) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xring[j] = gather(c, sSrc[j * 4 + g]);
+            yring[j] = sY[(j * 4 + g) * 16 + i16];
+        }
+        int cn;
+        const int u = target(4, len, c, cn);
+        scur = sSrc[(u >= 0 ? u : 0) * 4 + g];
+    };
+    if (nseg == 1) {
+        stage(0, T4);
+        __syncthreads();
+        prime(0, T4);
+    }
+
+    for (int c = 0; c < nchunk; ++c) {
+        const int c0 = c * 16;
+        const int goff_c = chunk_off(c), goff_next = chunk_off(c + 1);
+        int next_end = next_boundary(0);
+        v4f acc[4] = {zero4, zero4, zero4, zero4};
+        // the first path's W of this chunk, in flight during the S phase
+        switch (w) {
+            case 0: wf_load_first<0>(wr, woff, c0, cin, cout, wbuf[0]); break;
+            case 1: wf_load_first<1>(wr, woff, c0, cin, cout, wbuf[0]); break;
+            case 2: wf_load_first<2>(wr, woff, c0, cin, cout, wbuf[0]); break;
+            default: wf_load_first<3>(wr, woff, c0, cin, cout, wbuf[0]); break;
+        }
+        for (int sg = 0; sg < nseg; ++sg) {
+            const int s0 = sg * kWfSegSteps;
+            const int len = min(kWfSegSteps, T4 - s0);
+            if (nseg > 1) {
+                __syncthreads();  // every wave is done with the previous segment
+                stage(s0, len);
+                __syncthreads();
+                prime(c, len);
+            }
+            // one k-step: MFMAs of slot j, refill of slot j with step t + 4 (of chunk c4, or
+            // never consumed when u4 < 0), the source row of step t + 5, and S to LDS when
+            // the step ends a destination
+            auto step = [&](auto jj, int t0, int u4, int c4, int u5) {
+                constexpr int j = decltype(jj)::value;
+                const int t = t0 + j;
+                const float4 xa = xring[j];
+                const float ya = yring[j];
+                acc[0] = mfma1(xa.x, ya, acc[0]);
+                acc[1] = mfma1(xa.y, ya, acc[1]);
+                acc[2] = mfma1(xa.z, ya, acc[2]);
+                acc[3] = mfma1(xa.w, ya, acc[3]);
+                xring[j] = gather_at(c4 == c ? goff_c : goff_next, u4 >= 0 ? scur : 0);
+                yring[j] = sY[((u4 >= 0 ? u4 : 0) * 4 + g) * 16 + i16];
+                scur = sSrc[(u5 >= 0 ? u5 : 0) * 4 + g];
+                const int tg = s0 + t;
+                if (tg + 1 == next_end) {  // last step of destination kd: S to LDS row (ch, kd)
+                    const int kd = (int)(((uint32_t)(cum1 - 1 - tg) >> 31) +
+                                         ((uint32_t)(cum2 - 1 - tg) >> 31) +
+                                         ((uint32_t)(cum3 - 1 - tg) >> 31));
+                    const bool cok = c0 + 4 * w + g < cin;  // channels past C_in contribute zero
+                    float* row = sS + ((4 * w + g) * 4 + kd) * kPsStride + i16 * 16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        *reinterpret_cast<float4*>(row + ((r ^ ps_swz(i16)) * 4)) =
+                            cok ? make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r])
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[q] = zero4;
+                    next_end = next_boundary(tg + 1);
+                }
+            };
+            for (int t0 = 0; t0 < len; t0 += 4) {
+                if (t0 + 8 < len) {  // every refill target inside the segment, this chunk
+                    static_for<4>([&](auto jj) {
+                        constexpr int j = decltype(jj)::value;
+                        step(jj, t0, t0 + j + 4, c, t0 + j + 5);
+                    });
+                } else {
+                    static_for<4>([&](auto jj) {
+                        constexpr int j = decltype(jj)::value;
+                        int c4, c5;
+                        const int u4 = target(t0 + j + 4, len, c, c4);
+                        const int u5 = target(t0 + j + 5, len, c, c5);
+                        step(jj, t0, u4, c4, u5);
+                    });
+                }
+            }
+        }
+        __syncthreads();  // S of all four destinations is in LDS
+        const float* sSrow = sS + lane * kPsStride;
+        switch (w) {
+            case 0: wf_contract_mix<0>(sSrow, wr, woff, c0, cin, cout, wbuf, macc); break;
+            case 1: wf_contract_mix<1>(sSrow, wr, woff, c0, cin, cout, wbuf, macc); break;
+            case 2: wf_contract_mix<2>(sSrow, wr, woff, c0, cin, cout, wbuf, macc); break;
+            default: wf_contract_mix<3>(sSrow, wr, woff, c0, cin, cout, wbuf, macc); break;
+        }
+        __syncthreads();  // S is rewritten by the next chunk
+    }
+
+    // lane l of wave w holds, for output component o, macc[o][r] = partial out[dest r]
+    // [co0 + l][o]; the waves' partials meet in LDS and wave r sums them in wave order
+    float* sR = sS;  // [wave][r][o][lane]
+#pragma unroll
+    for (int o = 0; o < 16; ++o)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sR[((w * 4 + r) * 16 + o) * 64 + lane] = macc[o][r];
+    __syncthreads();
+    const int64_t d = w == 0 ? d0 : w == 1 ? d1 : w == 2 ? d2 : d3;
+    const int co = co0 + lane;
+    if (d >= 0 && co < cout) {
+        float v[16];
+#pragma unroll
+        for (int o = 0; o < 16; ++o) {
+            float sum = sR[((0 * 4 + w) * 16 + o) * 64 + lane];
+#pragma unroll
+            for (int ww = 1; ww < 4; ++ww) sum += sR[((ww * 4 + w) * 16 + o) * 64 + lane];
+            v[o] = sum;
+        }
+        float4* dstp = reinterpret_cast<float4*>(out + (d * cout + co) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dstp[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
     }
 }
 
@@ -1505,12 +1554,11 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 extern "C" size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges,
                                                                    int C_in, int C_out) {
-    if (N_dst < 0 || N_edges < 0 || C_in <= 0 || C_out <= 0) return 0;
-    const size_t cp = (size_t)((C_in + 15) / 16) * 16;
-    const size_t npad = (size_t)((N_dst + 15) / 16) * 16;
-    return align256((size_t)N_edges * 16 * sizeof(float)) + align256((size_t)N_edges * sizeof(int)) +
-           align256(npad * kNumSlots * cp * sizeof(float)) +
-           align256((size_t)kNumPaths * C_out * cp * sizeof(float));
+    (void)N_dst;
+    (void)N_edges;
+    (void)C_in;
+    (void)C_out;
+    return 0;  // the fused kernel keeps everything on chip
 }
 
 extern "C" int batteries_sh_tp_scatter_weighted(
@@ -1518,48 +1566,29 @@ extern "C" int batteries_sh_tp_scatter_weighted(
     const int64_t* source_idx, const int64_t* perm, const int64_t* row_ptr, const int64_t* order,
     float* node_output, int64_t N_src, int64_t N_dst, int64_t N_edges, int C_in, int C_out,
     int normalize, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
     if (N_src < 0 || N_dst < 0 || N_edges < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
     if (N_edges > 0 && N_src == 0) return BM_ERR_ARG;
     if (N_dst == 0) return BM_OK;
-    if (N_edges > INT32_MAX || N_src > INT32_MAX) return BM_ERR_ARG;  // int32 source rows in workspace
+    if (N_src > INT32_MAX) return BM_ERR_ARG;  // int32 source rows in LDS
     if ((int64_t)kNumPaths * C_in * C_out * 4 > INT32_MAX) return BM_ERR_ARG;  // W via 32-bit offsets
-    if (ceil_div(N_dst, 16) > INT32_MAX || ceil_div(C_out, 64) > 65535) return BM_ERR_ARG;
-    if ((reinterpret_cast<uintptr_t>(node_features) | reinterpret_cast<uintptr_t>(node_output) |
-         reinterpret_cast<uintptr_t>(workspace)) & 15)
+    if (ceil_div(C_out, 64) > 65535) return BM_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(node_features) | reinterpret_cast<uintptr_t>(node_output)) & 15)
         return BM_ERR_ARG;
-    const size_t need =
-        batteries_sh_tp_scatter_weighted_workspace_bytes(N_dst, N_edges, C_in, C_out);
-    if (!workspace || workspace_bytes < need) return BM_ERR_WORKSPACE;
-    const int cp = (C_in + 15) / 16 * 16;
-    const int64_t npad = ceil_div(N_dst, 16) * 16;
-    // 32-bit byte offsets inside one chunk of T and inside wt
-    if ((int64_t)kNumSlots * npad * 64 > INT32_MAX) return BM_ERR_ARG;
-    if ((int64_t)kNumPaths * C_out * cp * 4 > INT32_MAX) return BM_ERR_ARG;
-    char* ws = static_cast<char*>(workspace);
-    float* yc = reinterpret_cast<float*>(ws);
-    ws += align256((size_t)N_edges * 16 * sizeof(float));
-    int* srcc = reinterpret_cast<int*>(ws);
-    ws += align256((size_t)N_edges * sizeof(int));
-    float* tsum = reinterpret_cast<float*>(ws);
-    ws += align256((size_t)npad * kNumSlots * cp * sizeof(float));
-    float* wt = reinterpret_cast<float*>(ws);
-    const int64_t edge_blocks = ceil_div(N_edges, 256);
-    const int64_t wt_blocks = ceil_div((int64_t)kNumPaths * C_out * cp, 256);
-    if (edge_blocks + wt_blocks > INT32_MAX) return BM_ERR_ARG;
-    mp_edge_prep_kernel<<<(unsigned)(edge_blocks + wt_blocks), 256, 0, stream>>>(
-        edge_vectors, source_idx, perm, N_edges, normalize, yc, srcc, edge_blocks, weights, wt,
-        C_in, C_out, cp);
-    const int64_t nquad = ceil_div(N_dst, 4);
-    const int nchunk = (C_in + 15) / 16;
-    const int cpw = std::min(nchunk, 2);  // 16-channel chunks per workgroup
-    const int64_t n_units = nquad * ceil_div(nchunk, cpw);
-    const int64_t grid = ceil_div(n_units, 8) * 8;
+    const int64_t n_tiles = ceil_div(N_dst, 4);
+    const int64_t grid = ceil_div(n_tiles, 8) * 8;
     if (grid > INT32_MAX) return BM_ERR_ARG;
-    mp_path_sums_kernel<<<(unsigned)grid, 256, 0, stream>>>(
-        yc, srcc, node_features, row_ptr, order, tsum, N_dst, npad, C_in, cpw, n_units);
-    if (ceil_div(N_dst, 16) * 4 > INT32_MAX) return BM_ERR_ARG;
-    dim3 mgrid((unsigned)(ceil_div(N_dst, 16) * 4), (unsigned)ceil_div(C_out, 64), 1);
-    mp_weighted_mix_kernel<<<mgrid, 256, 0, stream>>>(tsum, wt, order, node_output, N_dst, npad,
-                                                      nchunk, C_out);
+    const int64_t xb = std::max<int64_t>(N_src, 1) * (int64_t)C_in * 64;
+    const bool buf = xb <= (int64_t)INT32_MAX;
+    dim3 g((unsigned)grid, (unsigned)ceil_div(C_out, 64), 1);
+    if (buf)
+        mp_weighted_fused_kernel<true><<<g, 256, 0, stream>>>(
+            edge_vectors, source_idx, perm, node_features, weights, row_ptr, order, node_output,
+            N_dst, C_in, C_out, n_tiles, normalize, (uint32_t)xb);
+    else
+        mp_weighted_fused_kernel<false><<<g, 256, 0, stream>>>(
+            edge_vectors, source_idx, perm, node_features, weights, row_ptr, order, node_output,
+            N_dst, C_in, C_out, n_tiles, normalize, 0u);
     return (int)hipGetLastError();
 }

@@ -346,6 +346,11 @@ int batteries_mace_backward(const float* positions, const float* box, const floa
  * v_mfma_f32_16x16x4f32 with the lane layout the kernels above assume.
  * ------------------------------------------------------------------------- */
 int batteries_selftest_mfma_16x16x4(const float* A, const float* B, float* D, hipStream_t stream);
+/* D[16][64][4]: for every ABID k in 0..15, lane l's accumulator (4 values) after one
+ * v_mfma_f32_4x4x1_16b_f32 with CBSZ = 4, ABID = k, A[l] and B[l] from lane l and a zero
+ * accumulator.  The weighted scatter assumes D[k][4b + j][r] = A[4k + r] * B[4b + j]. */
+int batteries_selftest_mfma_4x4x1_bcast(const float* A, const float* B, float* D,
+                                        hipStream_t stream);
 
 #ifdef __cplusplus
 }

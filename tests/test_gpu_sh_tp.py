@@ -27,6 +27,20 @@ def test_mfma_lane_layout(bm, dev):
     torch.testing.assert_close(d, a @ b, rtol=1e-5, atol=1e-5)
 
 
+def test_mfma_4x4_broadcast_lane_layout(bm, dev):
+    """The weighted scatter's mixing step: v_mfma_f32_4x4x1_16b_f32 with CBSZ = 4 and
+    ABID = k gives lane 4b + j the products A[4k + r] * B[4b + j], r = 0..3."""
+    a = torch.randn(64, generator=gen(2))
+    b = torch.randn(64, generator=gen(3))
+    d = bm.selftest_mfma_4x4x1_bcast(a.to(dev), b.to(dev)).cpu()
+    want = torch.empty(16, 64, 4)
+    for k in range(16):
+        for lane in range(64):
+            for r in range(4):
+                want[k, lane, r] = a[4 * k + r] * b[lane]
+    torch.testing.assert_close(d, want, rtol=1e-6, atol=0)
+
+
 @pytest.mark.parametrize("lmax", range(7))
 @pytest.mark.parametrize("n", [1, 10, 100, 1000, 100000])
 def test_sh_forward_random(bm, dev, lmax, n):
