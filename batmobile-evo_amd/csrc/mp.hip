@@ -1190,13 +1190,21 @@ __device__ __forceinline__ void wf_load_w(__amdgpu_buffer_rsrc_t wr, int woff, i
         w[k] = buffer_ld(wr, woff, (p * cin + min(c0 + k, cin - 1)) * cout * 4);
 }
 
-// Contraction of wave W's CG blocks for the lane's (channel, destination) row and the
-// mixing MFMAs of every slot.  wbuf[i & 1] holds path i's W; path i + 1's is loaded
-// before path i's products.
+// Slots of wave W's paths before path i (its T values sit in tq[wf_slot_base(W, i) ..]).
+constexpr int wf_slot_base(int W, int i) {
+    int n = 0;
+    for (int k = 0; k < i; ++k) n += 2 * kPathL[wf_path(W, k)][2] + 1;
+    return n;
+}
+// Depth of the W ring of the mixing step: path i + kWfAhead - 1's rows are loaded when
+// path i's products start.
+constexpr int kWfAhead = 2;
+
+// Contraction of wave W's CG blocks for the lane's (channel, destination) row: T of every
+// slot of the wave's paths into tq, in path order.
 template <int W>
-__device__ __forceinline__ void wf_contract_mix(const float* sSrow, __amdgpu_buffer_rsrc_t wr,
-                                                int woff, int c0, int cin, int cout,
-                                                float (&wbuf)[2][16], v4f (&acc)[16]) {
+__device__ __forceinline__ void wf_contract(const float* sSrow,
+                                            float (&tq)[wf_slot_base(W, wf_num_paths(W))]) {
     constexpr int NP = wf_num_paths(W);
     float s[7][7];  // S[a in l1][b in l2] of the current block
     static_for<NP>([&](auto ii) {
@@ -1205,6 +1213,8 @@ __device__ __forceinline__ void wf_contract_mix(const float* sSrow, __amdgpu_buf
         constexpr int L1 = kPathL[p][0], L2 = kPathL[p][1], LO = kPathL[p][2];
         constexpr int a0 = L1 * L1, na = 2 * L1 + 1, b0 = L2 * L2, nb = 2 * L2 + 1;
         if constexpr (wf_new_block(W, i)) {
+            // one block's S values live at a time: no reads hoisted from the next block
+            __builtin_amdgcn_sched_barrier(0);
             constexpr int qa0 = a0 / 4, qa1 = (a0 + na - 1) / 4;
             static_for<nb>([&](auto bb) {
                 constexpr int b = b0 + decltype(bb)::value;
@@ -1221,34 +1231,49 @@ __device__ __forceinline__ void wf_contract_mix(const float* sSrow, __amdgpu_buf
                 });
             });
         }
-        if constexpr (i + 1 < NP) {
-            constexpr int pn = wf_path(W, i + 1);
-            wf_load_w(wr, woff, pn, c0, cin, cout, wbuf[(i + 1) & 1]);
-            // keep the next path's loads here: sunk to their uses, each would wait on
-            // its own round trip
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        constexpr int no = 2 * LO + 1;
-        float t[no];
-        static_for<no>([&](auto m) { t[decltype(m)::value] = 0.0f; });
+        constexpr int base = wf_slot_base(W, i);
+        static_for<2 * LO + 1>([&](auto m) { tq[base + decltype(m)::value] = 0.0f; });
         static_for<kPathEntry[p + 1] - kPathEntry[p]>([&](auto kk) {
             constexpr CGEntry e = kCG[kPathEntry[p] + decltype(kk)::value];
             constexpr int m = e.q - kPathSlot[p];
-            t[m] = fmaf(e.c, s[e.a - a0][e.b - b0], t[m]);
+            tq[base + m] = fmaf(e.c, s[e.a - a0][e.b - b0], tq[base + m]);
         });
+    });
+}
+
+// Mixing MFMAs of every slot of wave W's paths.  wbuf[i % kWfAhead] holds path i's W rows;
+// paths 0 .. kWfAhead - 2 were loaded before the call, path i + kWfAhead - 1's rows are
+// loaded when path i's products start.
+template <int W>
+__device__ __forceinline__ void wf_mix(__amdgpu_buffer_rsrc_t wr, int woff, int c0, int cin,
+                                       int cout, const float (&tq)[wf_slot_base(W, wf_num_paths(W))],
+                                       float (&wbuf)[kWfAhead][16], v4f (&acc)[16]) {
+    constexpr int NP = wf_num_paths(W);
+    static_for<NP>([&](auto ii) {
+        constexpr int i = decltype(ii)::value;
+        constexpr int p = wf_path(W, i);
+        constexpr int LO = kPathL[p][2];
+        if constexpr (i + kWfAhead - 1 < NP) {
+            constexpr int pn = wf_path(W, i + kWfAhead - 1);
+            wf_load_w(wr, woff, pn, c0, cin, cout, wbuf[(i + kWfAhead - 1) % kWfAhead]);
+            // keep the loads here: sunk to their uses, each would wait on its own round trip
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        constexpr int base = wf_slot_base(W, i);
         static_for<16>([&](auto kk) {
             constexpr int k = decltype(kk)::value;
-            static_for<no>([&](auto mm) {
+            static_for<2 * LO + 1>([&](auto mm) {
                 constexpr int m = decltype(mm)::value;
-                acc[LO * LO + m] = mfma_4x4_bcast<k>(t[m], wbuf[i & 1][k], acc[LO * LO + m]);
+                acc[LO * LO + m] =
+                    mfma_4x4_bcast<k>(tq[base + m], wbuf[i % kWfAhead][k], acc[LO * LO + m]);
             });
         });
     });
 }
 
-// Step t < T of a tile: the CSR slot of its first edge (returned) and its number of
-// edges left from it (cnt; lane g takes edge g when g < cnt).  Destinations
-// 0..3 hold dg0..dg3 edges from slots r00..r03; steps cum1, cum2, cum3 onward belong to
+// Step t < T of a tile: the CSR slot of its first edge (returned) and the number of
+// edges left from it (cnt; lane g takes edge g when g < cnt).  Destinations 0..3 hold
+// dg0..dg3 edges from slots r00..r03; steps cum1, cum2, cum3 onward belong to
 // destinations 1, 2, 3.  Values by argument, not through captured references: a select
 // between variables in memory becomes a load through a selected pointer.
 __device__ __forceinline__ int64_t wf_step_rows(int t, int cum1, int cum2, int cum3, int64_t r00,
@@ -1262,18 +1287,36 @@ __device__ __forceinline__ int64_t wf_step_rows(int t, int cum1, int cum2, int c
     return r + 4 * (t - c);
 }
 
+// W rows of wave W's first kWfAhead - 1 paths (the ones wf_mix expects in flight)
 template <int W>
 __device__ __forceinline__ void wf_load_first(__amdgpu_buffer_rsrc_t wr, int woff, int c0, int cin,
-                                              int cout, float (&w)[16]) {
-    constexpr int p = wf_path(W, 0);
-    wf_load_w(wr, woff, p, c0, cin, cout, w);
+                                              int cout, float (&wbuf)[kWfAhead][16]) {
+    static_for<kWfAhead - 1>([&](auto ii) {
+        constexpr int i = decltype(ii)::value;
+        constexpr int p = wf_path(W, i);
+        wf_load_w(wr, woff, p, c0, cin, cout, wbuf[i]);
+    });
 }
 
-// Edges of the tile staged in LDS at a time, in k-steps of 4 (160 edges): the Y and
-// source row of each step's four edges, computed once per tile and read by every chunk.
-constexpr int kWfSegSteps = 40;
+// Contraction then mixing of wave W (T of its 39 slots in registers in between)
+template <int W>
+__device__ __forceinline__ void wf_contract_mix(const float* sSrow, __amdgpu_buffer_rsrc_t wr,
+                                                int woff, int c0, int cin, int cout,
+                                                float (&wbuf)[kWfAhead][16], v4f (&acc)[16]) {
+    float tq[wf_slot_base(W, wf_num_paths(W))];
+    wf_contract<W>(sSrow, tq);
+    __builtin_amdgcn_sched_barrier(0);
+    wf_mix<W>(wr, woff, c0, cin, cout, tq, wbuf, acc);
+}
 
-// BUF: source-row gathers as raw buffer loads with 32-bit offsets (X under 2 GiB).
+// Edges of one destination staged in LDS at a time (per wave): kWfSegSteps k-steps of 4
+// edges, the Y and source-row value of each edge, transposed as [edge g][component b]
+// [step] (and [edge g][step]) so that one 16-byte read gives a lane four steps' values;
+// rows of 12 floats put the 16 lanes of a read pass in distinct banks.
+constexpr int kWfSegSteps = 12;
+
+// BUF: source-row gathers as raw buffer loads with 32-bit offsets (X under 2 GiB); the
+// staged source values are then byte offsets of the rows, otherwise row indices.
 template <bool BUF>
 __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
     const float* __restrict__ vec, const int64_t* __restrict__ src_idx,
@@ -1281,8 +1324,8 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
     const int64_t* __restrict__ row_ptr, const int64_t* __restrict__ order, float* __restrict__ out,
     int64_t n_dst, int cin, int cout, int64_t n_tiles, int normalize, uint32_t x_bytes) {
     __shared__ __attribute__((aligned(16))) float sS[64 * kPsStride];
-    __shared__ __attribute__((aligned(16))) float sY[kWfSegSteps * 4 * 16];
-    __shared__ int sSrc[kWfSegSteps * 4];
+    __shared__ __attribute__((aligned(16))) float sYall[4][4 * 16 * kWfSegSteps];
+    __shared__ __attribute__((aligned(16))) int sSrcAll[4][4 * kWfSegSteps];
     const int64_t per_xcd = (n_tiles + 7) / 8;
     const int64_t tile = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (tile >= n_tiles) return;
@@ -1290,69 +1333,47 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int co0 = blockIdx.y * 64;
     const int nchunk = (cin + 15) >> 4;
+    float* sY = sYall[w];
+    int* sSrc = sSrcAll[w];
 
-    // the tile's destinations: rows [r0, r0 + deg) of the CSR, k-steps per chunk.  Plain
-    // wave-uniform scalars (no arrays or structs, which the compiler may keep in memory
-    // and reach through pointers when a step selects among them).
-    auto dest_rows = [&](int k, int64_t& d, int64_t& r0, int& deg) {
-        const int64_t pos = tile * 4 + k;
-        int64_t dd = -1, a = 0, b = 0;
+    // destination w of the tile (position 4 tile + w of the processing order): CSR rows
+    // [r0, r0 + deg); the output is written by wave w, so every wave keeps its own
+    int64_t dst = -1, r0 = 0;
+    int deg = 0;
+    {
+        const int64_t pos = tile * 4 + w;
+        int64_t a = 0, b = 0;
         if (pos < n_dst) {
-            dd = order ? order[pos] : pos;
-            if (dd >= 0 && dd < n_dst) {  // an order entry out of range sums no edges
-                a = row_ptr[dd];
-                b = row_ptr[dd + 1];
+            dst = order ? order[pos] : pos;
+            if (dst >= 0 && dst < n_dst) {  // an order entry out of range sums no edges
+                a = row_ptr[dst];
+                b = row_ptr[dst + 1];
             } else {
-                dd = -1;
+                dst = -1;
             }
         }
-        d = uniform64(dd);
+        dst = uniform64(dst);
         r0 = uniform64(a);
         deg = __builtin_amdgcn_readfirstlane((int)(b - a));
-    };
-    int64_t d0, d1, d2, d3, r00, r01, r02, r03;
-    int dg0, dg1, dg2, dg3;
-    dest_rows(0, d0, r00, dg0);
-    dest_rows(1, d1, r01, dg1);
-    dest_rows(2, d2, r02, dg2);
-    dest_rows(3, d3, r03, dg3);
-    const int cum1 = (dg0 + 3) >> 2, cum2 = cum1 + ((dg1 + 3) >> 2),
-              cum3 = cum2 + ((dg2 + 3) >> 2);
-    const int T = cum3 + ((dg3 + 3) >> 2);  // k-steps per chunk, the same in every chunk
-    // Steps are padded to T4, a multiple of the ring below, and staged in segments of at
-    // most kWfSegSteps; padding steps and lanes past a destination's last edge have Y = 0
-    // and source row 0 (a valid row).
-    const int T4 = (T + 3) & ~3;
-    const int nseg = (T4 + kWfSegSteps - 1) / kWfSegSteps;  // 0: the tile has no edges
+    }
+    // k-steps of 4 edges, padded to a multiple of 2 (the unroll of the pipeline below);
+    // padding steps and lanes past the last edge have Y = 0 and source 0 (a valid row)
+    const int nst = (deg + 3) >> 2;
+    const int nst2 = (nst + 1) & ~1;
+    const int nseg = (nst2 + kWfSegSteps - 1) / kWfSegSteps;  // 0: no edges
 
-    // S rows of destinations without edges are zero for every chunk
-    auto zero_rows = [&](int k, int deg) {
-        if (deg == 0) {
-            float* row = sS + ((4 * w + g) * 4 + k) * kPsStride + i16 * 16;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                *reinterpret_cast<float4*>(row + r * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    zero_rows(0, dg0);
-    zero_rows(1, dg1);
-    zero_rows(2, dg2);
-    zero_rows(3, dg3);
-
-    // steps [s0, s0 + len) into LDS: thread k takes edge k % 4 of step s0 + k / 4
+    const uint32_t row_bytes = (uint32_t)cin * 64u;
+    // steps [s0, s0 + len) of this wave's destination into its LDS area: lane l takes edge
+    // 4 s0 + l (len <= kWfSegSteps = 12, so 48 lanes); read back by the same wave only
     auto stage = [&](int s0, int len) {
-        for (int k = threadIdx.x; k < len * 4; k += 256) {
-            const int t = s0 + (k >> 2), ge = k & 3;
-            int64_t e = -1;
-            if (t < T) {
-                int cnt;
-                const int64_t base =
-                    wf_step_rows(t, cum1, cum2, cum3, r00, r01, r02, r03, dg0, dg1, dg2, dg3, cnt);
-                if (ge < cnt) e = perm ? perm[base + ge] : base + ge;
-            }
+        if (lane < 4 * len) {
+            const int sl = lane >> 2, ge = lane & 3;
+            const int k = 4 * s0 + lane;  // edge index within the destination
             float Y[16];
             int src = 0;
-            if (e >= 0) {
+            if (k < deg) {
+                const int64_t slot = r0 + k;
+                const int64_t e = perm ? perm[slot] : slot;
                 float x = vec[e * 3 + 0], y = vec[e * 3 + 1], z = vec[e * 3 + 2];
                 if (normalize) normalize3(x, y, z);
                 sh_forward<3>(x, y, z, Y);
@@ -1361,35 +1382,47 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
 #pragma unroll
                 for (int q = 0; q < 16; ++q) Y[q] = 0.f;
             }
-            float4* yd = reinterpret_cast<float4*>(sY + k * 16);
-            yd[0] = make_float4(Y[0], Y[1], Y[2], Y[3]);
-            yd[1] = make_float4(Y[4], Y[5], Y[6], Y[7]);
-            yd[2] = make_float4(Y[8], Y[9], Y[10], Y[11]);
-            yd[3] = make_float4(Y[12], Y[13], Y[14], Y[15]);
-            sSrc[k] = src;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) sY[(ge * 16 + q) * kWfSegSteps + sl] = Y[q];
+            sSrc[ge * kWfSegSteps + sl] = BUF ? (int)((uint32_t)src * row_bytes) : src;
         }
+        // the wave's own LDS writes are complete before its reads below
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
     };
-    const uint32_t row_bytes = (uint32_t)cin * 64u;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(X), (short)0, BUF ? (int)x_bytes : 0, kBufferDword3);
-    // lane (g, i16) of a gather: channel 4 w + i16 / 4 of the chunk (clamped to the last
-    // channel), components 4 (i16 % 4) ..; goff is that byte offset inside a source row
-    auto chunk_off = [&](int chunk) {
-        return min(min(chunk, nchunk - 1) * 16 + 4 * w + (i16 >> 2), cin - 1) * 64 + (i16 & 3) * 16;
-    };
-    auto gather_at = [&](int goff, int src) {
-        if constexpr (BUF) {
-            return buffer_ld4(xr, (int)((uint32_t)src * row_bytes) + goff, 0);
-        } else {
-            return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(X) +
-                                                    (int64_t)src * row_bytes + goff);
+    // lane (g, i16) gathers channels c0 + 4t + i16 / 4 (t = 0..3, clamped to the last channel),
+    // components 4 (i16 % 4) .. 4 (i16 % 4) + 3 of the source row of its edge g
+    auto gather4 = [&](int c0, int sv, float4 (&x)[4]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int off = min(c0 + 4 * t + (i16 >> 2), cin - 1) * 64 + (i16 & 3) * 16;
+            if constexpr (BUF) {
+                x[t] = buffer_ld4(xr, sv + off, 0);
+            } else {
+                x[t] = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(X) +
+                                                        (int64_t)sv * row_bytes + off);
+            }
         }
     };
-    auto gather = [&](int chunk, int src) { return gather_at(chunk_off(chunk), src); };
-    // the first destination boundary (end of a destination's steps) after step index b
-    auto next_boundary = [&](int b) {
-        return b < cum1 ? cum1 : b < cum2 ? cum2 : b < cum3 ? cum3 : b < T ? T : -1;
+    auto ld_y = [&](int col) {  // Y[edge g][b = i16] of steps col .. col + 3
+        return *reinterpret_cast<const float4*>(sY + (g * 16 + i16) * kWfSegSteps + col);
     };
+    auto ld_s = [&](int col) {  // source values of edge g of steps col .. col + 3
+        return *reinterpret_cast<const int4*>(sSrc + g * kWfSegSteps + col);
+    };
+
+    // S rows of a destination without edges are zero for every chunk
+    if (deg == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float* row = sS + ((4 * t + g) * 4 + w) * kPsStride + i16 * 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<float4*>(row + r * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
 
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wt, (uint32_t)((int64_t)kNumPaths * cin * cout * 4));
     const int woff = min(co0 + lane, cout - 1) * 4;
@@ -1397,120 +1430,78 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
     v4f macc[16];
 #pragma unroll
     for (int o = 0; o < 16; ++o) macc[o] = zero4;
-    float wbuf[2][16];
+    float wbuf[kWfAhead][16];
 
-    // A ring of 4 steps with static register names (the step loop is unrolled by 4):
-    // slot j holds, for the step t = j (mod 4) being consumed, its gather and Y (issued 4
-    // steps earlier); scur the source row of the next step to gather (read one step ahead).
-    float4 xring[4];
-    float yring[4];
-    int scur = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        xring[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        yring[j] = 0.f;
-    }
-    // ring refill target for local step u (< len + 5) of a segment of len (>= 4) steps in
-    // chunk c: past the segment, the matching step of a following chunk when the whole
-    // tile is one segment (its LDS data stays; with len = 4 that can be two chunks on),
-    // otherwise -1, a load that is never consumed (row 0, Y index 0).  Every index it
-    // returns lies inside the staged segment.
-    auto target = [&](int u, int len, int c, int& cn) {
-        cn = c;
-        if (u < len) return u;
-        if (nseg != 1) return -1;
-        while (u >= len) {
-            u -= len;
-            ++cn;
-        }
-        return cn < nchunk ? u : -1;
-    };
-    // slots 0..3: steps 0..3 of a segment of len (>= 4) steps in chunk c; scur: the step after
-    auto prime = [&](int c, int len) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            xring[j] = gather(c, sSrc[j * 4 + g]);
-            yring[j] = sY[(j * 4 + g) * 16 + i16];
-        }
-        int cn;
-        const int u = target(4, len, c, cn);
-        scur = sSrc[(u >= 0 ? u : 0) * 4 + g];
-    };
-    if (nseg == 1) {
-        stage(0, T4);
-        __syncthreads();
-        prime(0, T4);
-    }
+    if (nseg == 1) stage(0, nst2);
 
     for (int c = 0; c < nchunk; ++c) {
         const int c0 = c * 16;
-        const int goff_c = chunk_off(c), goff_next = chunk_off(c + 1);
-        int next_end = next_boundary(0);
-        v4f acc[4] = {zero4, zero4, zero4, zero4};
-        // the first path's W of this chunk, in flight during the S phase
-        switch (w) {
-            case 0: wf_load_first<0>(wr, woff, c0, cin, cout, wbuf[0]); break;
-            case 1: wf_load_first<1>(wr, woff, c0, cin, cout, wbuf[0]); break;
-            case 2: wf_load_first<2>(wr, woff, c0, cin, cout, wbuf[0]); break;
-            default: wf_load_first<3>(wr, woff, c0, cin, cout, wbuf[0]); break;
+        if (nseg > 0) {
+            // S phase: acc[t][j] accumulates S[ch = 4t + g][a = 4r + j][b = i16] (element r)
+            // of destination w over its edges, four per k-step (16 MFMAs).  Steps run in
+            // pairs through two pipeline stages with static register names: entering step
+            // s, stage s % 2 holds its gathers (issued two steps earlier); y4/s4 hold the
+            // Y and source values of the current block of four steps.
+            v4f acc[4][4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][j] = zero4;
+            for (int sg = 0; sg < nseg; ++sg) {
+                const int s0 = sg * kWfSegSteps;
+                const int len = min(kWfSegSteps, nst2 - s0);  // even
+                if (nseg > 1) stage(s0, len);
+                float4 xa[4], xb[4];
+                int4 sv = ld_s(0);
+                float4 yv = ld_y(0);
+                gather4(c0, sv.x, xa);
+                gather4(c0, len > 1 ? sv.y : 0, xb);
+                // one step from stage x, whose refill is step s + 2 (source value snext)
+                auto step = [&](float4 (&x)[4], float y, int snext, bool refill) {
+                    float4 xs[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) xs[t] = x[t];
+                    gather4(c0, refill ? snext : 0, x);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        acc[t][0] = mfma1(xs[t].x, y, acc[t][0]);
+                        acc[t][1] = mfma1(xs[t].y, y, acc[t][1]);
+                        acc[t][2] = mfma1(xs[t].z, y, acc[t][2]);
+                        acc[t][3] = mfma1(xs[t].w, y, acc[t][3]);
+                    }
+                };
+                for (int s = 0; s < len; s += 4) {
+                    // steps s .. s + 3 (the last block may hold only s, s + 1)
+                    const int4 svn = s + 4 < len ? ld_s(s + 4) : make_int4(0, 0, 0, 0);
+                    const float4 yn = s + 4 < len ? ld_y(s + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    step(xa, yv.x, sv.z, s + 2 < len);
+                    step(xb, yv.y, sv.w, s + 3 < len);
+                    if (s + 2 < len) {
+                        step(xa, yv.z, svn.x, s + 4 < len);
+                        step(xb, yv.w, svn.y, s + 5 < len);
+                    }
+                    sv = svn;
+                    yv = yn;
+                }
+            }
+            // S of destination w to LDS rows (ch, w); channels past C_in are zero
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bool cok = c0 + 4 * t + g < cin;
+                float* row = sS + ((4 * t + g) * 4 + w) * kPsStride + i16 * 16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    *reinterpret_cast<float4*>(row + ((r ^ ps_swz(i16)) * 4)) =
+                        cok ? make_float4(acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r])
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
-        for (int sg = 0; sg < nseg; ++sg) {
-            const int s0 = sg * kWfSegSteps;
-            const int len = min(kWfSegSteps, T4 - s0);
-            if (nseg > 1) {
-                __syncthreads();  // every wave is done with the previous segment
-                stage(s0, len);
-                __syncthreads();
-                prime(c, len);
-            }
-            // one k-step: MFMAs of slot j, refill of slot j with step t + 4 (of chunk c4, or
-            // never consumed when u4 < 0), the source row of step t + 5, and S to LDS when
-            // the step ends a destination
-            auto step = [&](auto jj, int t0, int u4, int c4, int u5) {
-                constexpr int j = decltype(jj)::value;
-                const int t = t0 + j;
-                const float4 xa = xring[j];
-                const float ya = yring[j];
-                acc[0] = mfma1(xa.x, ya, acc[0]);
-                acc[1] = mfma1(xa.y, ya, acc[1]);
-                acc[2] = mfma1(xa.z, ya, acc[2]);
-                acc[3] = mfma1(xa.w, ya, acc[3]);
-                xring[j] = gather_at(c4 == c ? goff_c : goff_next, u4 >= 0 ? scur : 0);
-                yring[j] = sY[((u4 >= 0 ? u4 : 0) * 4 + g) * 16 + i16];
-                scur = sSrc[(u5 >= 0 ? u5 : 0) * 4 + g];
-                const int tg = s0 + t;
-                if (tg + 1 == next_end) {  // last step of destination kd: S to LDS row (ch, kd)
-                    const int kd = (int)(((uint32_t)(cum1 - 1 - tg) >> 31) +
-                                         ((uint32_t)(cum2 - 1 - tg) >> 31) +
-                                         ((uint32_t)(cum3 - 1 - tg) >> 31));
-                    const bool cok = c0 + 4 * w + g < cin;  // channels past C_in contribute zero
-                    float* row = sS + ((4 * w + g) * 4 + kd) * kPsStride + i16 * 16;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        *reinterpret_cast<float4*>(row + ((r ^ ps_swz(i16)) * 4)) =
-                            cok ? make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r])
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[q] = zero4;
-                    next_end = next_boundary(tg + 1);
-                }
-            };
-            for (int t0 = 0; t0 < len; t0 += 4) {
-                if (t0 + 8 < len) {  // every refill target inside the segment, this chunk
-                    static_for<4>([&](auto jj) {
-                        constexpr int j = decltype(jj)::value;
-                        step(jj, t0, t0 + j + 4, c, t0 + j + 5);
-                    });
-                } else {
-                    static_for<4>([&](auto jj) {
-                        constexpr int j = decltype(jj)::value;
-                        int c4, c5;
-                        const int u4 = target(t0 + j + 4, len, c, c4);
-                        const int u5 = target(t0 + j + 5, len, c, c5);
-                        step(jj, t0, u4, c4, u5);
-                    });
-                }
-            }
+        // the first paths' W rows of this chunk, in flight during the barrier wait
+        switch (w) {
+            case 0: wf_load_first<0>(wr, woff, c0, cin, cout, wbuf); break;
+            case 1: wf_load_first<1>(wr, woff, c0, cin, cout, wbuf); break;
+            case 2: wf_load_first<2>(wr, woff, c0, cin, cout, wbuf); break;
+            default: wf_load_first<3>(wr, woff, c0, cin, cout, wbuf); break;
         }
         __syncthreads();  // S of all four destinations is in LDS
         const float* sSrow = sS + lane * kPsStride;
@@ -1531,7 +1522,7 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) sR[((w * 4 + r) * 16 + o) * 64 + lane] = macc[o][r];
     __syncthreads();
-    const int64_t d = w == 0 ? d0 : w == 1 ? d1 : w == 2 ? d2 : d3;
+    const int64_t d = dst;
     const int co = co0 + lane;
     if (d >= 0 && co < cout) {
         float v[16];
