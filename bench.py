@@ -20,6 +20,10 @@ kernel's flop count E * (2 * 256 * C + 2 * 611) (16x16 edge operator applied to
 C channels, plus building it from the 611 CG entries).
 `cpu_baseline` times the reference's float32 PyTorch composition on the host
 cores (oracle/cpu_path.py) on the same workload.
+`weighted` is the same configs[3] workload with W [34, 64, 64] as BASELINE.json
+states it (Graph.sh_tp_scatter(x, weights=W), one kernel), with its own value,
+roofline (fp32 MFMA on the flops the kernel executes, measured traffic beside it)
+and cpu_baseline (the reference's weighted composition, float32 torch on the host).
 """
 import argparse
 import json
@@ -184,26 +188,98 @@ def other_configs(torch, bm, dev):
     return res
 
 
-def weighted_config3(torch, bm, dev, w, reps=100):
-    """configs[3], weighted variant: the same graph and X with W [34, 64, 64] ~ N(0, 1/64)
-    (seed 3 continued), out[d] = sum_{e -> d} tensor_product(X[src_e], Y(v_e), W).
-    Flop models: the survey's minimal exact count E (1222 C) + N (312 C^2) (per-edge CG
-    products, mixing once per destination), and the count this build executes,
-    E (512 C) + N (1222 C + 312 C^2) (edge sums of X Y^T on MFMA, CG and mixing per
-    destination)."""
+WEIGHTED_KERNEL = "mp_weighted_fused_kernel<true>"
+WEIGHTED_WORKLOAD = "configs[3] weighted"
+
+
+def weighted_inputs3(torch, dev):
+    """W [34, 64, 64] ~ N(0, 1/64) for configs[3]'s weighted variant (seed 103)."""
     g = torch.Generator().manual_seed(SEED + 100)
-    wt = (torch.randn(34, CHANNELS, CHANNELS, generator=g) / math.sqrt(CHANNELS)).to(dev)
+    return (torch.randn(34, CHANNELS, CHANNELS, generator=g) / math.sqrt(CHANNELS)).to(dev)
+
+
+def weighted_config3(torch, bm, dev, w, wt, reps=200, settle=SETTLE_STEPS // 2):
+    """configs[3], weighted variant, as BASELINE.json states it: the same graph and X with
+    W [34, 64, 64], out[d] = sum_{e -> d} tensor_product(X[src_e], Y(v_e), W)
+    (the reference's interaction block, benchmarks/benchmark_e2e_mace.py:308-349), one
+    kernel (mp_weighted_fused_kernel), HIP events on the launch stream.
+    Flop models: the one this kernel executes, E (512 C) + N (1222 C + 312 C^2) (edge sums
+    of X Y^T on MFMA, CG contraction and per-path mixing once per destination), which the
+    roofline uses; and the survey's E (1222 C) + N (312 C^2), reported beside it.
+    Compulsory bytes: edge vector, source index, X row once, W, output row, row pointer."""
     graph, x = w["graph"], w["x"]
+    for _ in range(settle):     # clock settle under this kernel's own load
+        out = graph.sh_tp_scatter(x, weights=wt)
     t = event_ms(torch, lambda: graph.sh_tp_scatter(x, weights=wt), reps)
     e, n, c = graph.num_edges, N_ATOMS, CHANNELS
     f_survey = e * 1222 * c + n * 312 * c * c
     f_exec = e * 512 * c + n * (1222 * c + 312 * c * c)
+    b_comp = e * (12 + 8) + n * (64 * c + 64 * c + 8) + 34 * c * c * 4
+    tf = f_exec / (t * 1e-3) / 1e12
+    traffic, note = measured_traffic(WEIGHTED_KERNEL, WEIGHTED_WORKLOAD)
+    res = {
+        "metric": "fused SH+TP(weighted W[34,64,64])+scatter edges/s (N=5k,C=64,~30 nbr)",
+        "value": e / (t * 1e-3),
+        "unit": "edges/s",
+        "kernel_ms": t,
+        "higher_is_better": True,
+        "dtype": "f32",
+        "config": {
+            "workload": "configs[3] weighted variant: N=5000 atoms, C_in=C_out=64, "
+                        "W [34,64,64] ~ N(0,1/64) (seed 103), same graph and X as the headline",
+            "E": e, "kernel": WEIGHTED_KERNEL + " (batmobile.Graph.sh_tp_scatter(x, weights=W))",
+        },
+        "roofline": {
+            "bound": "mfma", "achieved": tf, "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tf / MFMA_FP32_PEAK_TFLOPS, "traffic": traffic,
+            "flop_model": "executed: E*512*C + N*(1222*C + 312*C^2)",
+            "flops_per_launch": f_exec,
+            "survey_model_flops_per_launch": f_survey,
+            "survey_model_TFLOPs": f_survey / (t * 1e-3) / 1e12,
+            "traffic_source": note,
+        },
+        "roofline_hbm": {
+            "bound": "hbm",
+            "achieved": (traffic / (t * 1e-3) / 1e9) if traffic else None,
+            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": (traffic / (t * 1e-3) / 1e9 / HBM_PEAK_GBS) if traffic else None,
+            "traffic": traffic, "compulsory_bytes_per_launch": b_comp,
+        },
+    }
+    return res, out
+
+
+def cpu_baseline_weighted(torch, w, wt, gpu_out):
+    """The reference's weighted composition in float32 torch on the host cores
+    (oracle/cpu_path.weighted_sh_tp_scatter: SH -> per-path CG product and W mixing per
+    edge -> index_add_) on the full configs[3] workload: one warm-up on 8192 edges, then
+    the median of up to 3 full passes within about 20 s."""
+    from oracle import cpu_path
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    vec, x, wc = w["vec"].cpu(), w["x"].cpu(), wt.cpu()
+    src, dst = w["src"].cpu(), w["dst"].cpu()
+    e = vec.shape[0]
+    cpu_path.weighted_sh_tp_scatter(vec[:8192], x, wc, src[:8192], dst[:8192], N_ATOMS)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 and (len(times) < 1 or time.perf_counter() - t_start < 20.0):
+        t0 = time.perf_counter()
+        out = cpu_path.weighted_sh_tp_scatter(vec, x, wc, src, dst, N_ATOMS)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    err = float((out - gpu_out.cpu()).norm() / gpu_out.cpu().norm())
     return {
-        "cfg3_weighted_ms": round(t, 5),
-        "cfg3_weighted_edges_per_s": round(e / (t * 1e-3), 1),
-        "cfg3_weighted_TFLOPs_survey_model": round(f_survey / (t * 1e-3) / 1e12, 2),
-        "cfg3_weighted_mfma_frac_survey_model": round(f_survey / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4),
-        "cfg3_weighted_TFLOPs_executed": round(f_exec / (t * 1e-3) / 1e12, 2),
+        "value": e / med,
+        "unit": "edges/s",
+        "cores": cores,
+        "cpu_count": os.cpu_count(),
+        "kind": "port",
+        "sample": f"full configs[3] weighted workload (E={e}, C=64, W [34,64,64]), float32 "
+                  f"torch on CPU (SH polynomials -> per-path CG einsum and W mixing per edge, "
+                  f"8192-edge chunks -> index_add_), median of {len(times)} after a warm-up "
+                  f"on 8192 edges, {med * 1e3:.1f} ms/step",
+        "cpu_vs_gpu_normwise_err": err,
     }
 
 
@@ -349,9 +425,10 @@ def main():
         return
     w = make_workload(torch, bm, dev)
     E = int(w["src"].numel())
+    wt = weighted_inputs3(torch, dev)
     if a.weighted_only:
-        weighted_config3(torch, bm, dev, w, reps=SETTLE_STEPS // 2)  # clock settle
-        print(json.dumps(weighted_config3(torch, bm, dev, w, reps=max(a.steps, 1))), flush=True)
+        print(json.dumps(weighted_config3(torch, bm, dev, w, wt, reps=max(a.steps, 1))[0]),
+              flush=True)
         return
 
     graph = w["graph"]
@@ -396,7 +473,7 @@ def main():
         extra["graph_build_ms"] = round(time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS)), 4)
         extra["index_order_kernel_ms"] = round(time_call(torch, lambda: graph.sh_tp_scatter_index_order(w["x"]), 20), 4)
         extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
-        extra.update(weighted_config3(torch, bm, dev, w))
+        weighted, w_out = weighted_config3(torch, bm, dev, w, wt)
         extra.update(other_configs(torch, bm, dev))
         extra.update(mace_config4(torch, bm, dev))
 
@@ -446,8 +523,12 @@ def main():
         },
         "also": extra,
     }
+    if not a.headline_only:
+        res["weighted"] = weighted
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(torch, w, out)
+        if not a.headline_only:
+            res["weighted"]["cpu_baseline"] = cpu_baseline_weighted(torch, w, wt, w_out)
     print(json.dumps(res), flush=True)
 
 

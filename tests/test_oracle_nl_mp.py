@@ -134,3 +134,29 @@ def test_weighted_message_passing_matches_per_edge_loop():
     for k in range(e):
         want[dst[k]] += tp.tensor_product(x[src[k]][None], sh.spherical_harmonics(u[k:k + 1], 3), w)[0]
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_cpu_baseline_compositions_match_the_oracle(normalize):
+    """The float32 torch compositions bench.py times as its CPU baselines
+    (oracle/cpu_path.py) agree with the float64 message-passing oracle, the weighted one
+    with chunks smaller than the edge list so that the chunked scatter is exercised."""
+    import torch
+
+    from oracle import cpu_path
+    g = torch.Generator().manual_seed(11)
+    n, e, c, co = 40, 700, 6, 10
+    vec = torch.randn(e, 3, generator=g) * 2.0
+    x = torch.randn(n, c, 16, generator=g)
+    w = torch.randn(34, c, co, generator=g) / 3.0
+    src = torch.randint(0, n, (e,), generator=g)
+    dst = torch.randint(0, n, (e,), generator=g)
+    got = cpu_path.weighted_sh_tp_scatter(vec, x, w, src, dst, n, normalize=normalize, chunk=128)
+    want = mp.weighted_message_passing(vec.double().numpy(), x.double().numpy(),
+                                       w.double().numpy(), src.numpy(), dst.numpy(), n,
+                                       normalize=normalize)
+    assert np.abs(got.numpy() - want).max() <= 1e-5 * np.abs(want).max()
+    got = cpu_path.sh_tp_scatter(vec, x, src, dst, n, normalize=normalize)
+    want = mp.sh_tp_scatter(vec.double().numpy(), x.double().numpy(), src.numpy(), dst.numpy(),
+                            n, normalize=normalize)
+    assert np.abs(got.numpy() - want).max() <= 1e-5 * np.abs(want).max()
