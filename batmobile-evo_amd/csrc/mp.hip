@@ -78,6 +78,30 @@ __device__ __forceinline__ EdgeRec load_edge(const float* __restrict__ vec,
     return r;
 }
 
+// Y (L = 3) of one edge record, normalised first when NORM.
+template <bool NORM>
+__device__ __forceinline__ void edge_sh(EdgeRec r, float* Y) {
+    float x = r.x, y = r.y, z = r.z;
+    if constexpr (NORM) {
+        // v / max(|v|, 1e-10) with one reciprocal square root (about 1 ulp)
+        const float inv = __builtin_amdgcn_rsqf(fmaxf(x * x + y * y + z * z, 1e-20f));
+        x *= inv;
+        y *= inv;
+        z *= inv;
+    }
+    sh_forward<3>(x, y, z, Y);
+}
+
+// Wave w's four operator rows of one edge, from its Y, into sMj.
+__device__ __forceinline__ void edge_rows(const float* Y, float* sMj, int w) {
+    switch (w) {
+        case 0: build_rows<0>(Y, sMj); break;
+        case 1: build_rows<1>(Y, sMj); break;
+        case 2: build_rows<2>(Y, sMj); break;
+        default: build_rows<3>(Y, sMj); break;
+    }
+}
+
 // Phase 1 of a batch: lane j < nb of wave w builds rows 4w..4w+3 of the
 // operator of its edge into sM (no global memory access: the edge was loaded
 // into registers during the previous batch).
@@ -86,23 +110,9 @@ __device__ __forceinline__ void phase1_build(EdgeRec r, int nb, float* sM) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     if (lane < nb) {
-        float x = r.x, y = r.y, z = r.z;
-        if constexpr (NORM) {
-            // v / max(|v|, 1e-10) with one reciprocal square root (about 1 ulp)
-            const float inv = __builtin_amdgcn_rsqf(fmaxf(x * x + y * y + z * z, 1e-20f));
-            x *= inv;
-            y *= inv;
-            z *= inv;
-        }
         float Y[16];
-        sh_forward<3>(x, y, z, Y);
-        float* sMj = sM + lane * kMStride;
-        switch (w) {
-            case 0: build_rows<0>(Y, sMj); break;
-            case 1: build_rows<1>(Y, sMj); break;
-            case 2: build_rows<2>(Y, sMj); break;
-            default: build_rows<3>(Y, sMj); break;
-        }
+        edge_sh<NORM>(r, Y);
+        edge_rows(Y, sM + lane * kMStride, w);
     }
 }
 
@@ -320,27 +330,38 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 // Scatter kernel: out[d, c, :] = sum over the CSR row of d, for the
 // rows_per_block (<= kScatterRows, scheduled) rows of this workgroup.
 //
-// Same operator/MFMA scheme as above, arranged so that the compiler can keep
-// kRing gathers in flight.  On gfx9 loads and stores share one counter, and
-// with a store pending the compiler treats the counter as out of order and
-// drains every outstanding gather before the next use; a gather issued under a
-// data-dependent condition has the same effect.  Hence the edge loop has
-// neither:
+// Same operator/MFMA scheme as above, in batches of 64 edges so that phase 1
+// (Y and four operator rows per wave) runs on every lane: on gfx950 VALU work
+// does not overlap the MFMAs of its SIMD, so each phase-1 instruction costs its
+// full issue time, and a 32-edge batch would leave half of the lanes idle.
+//
+// On gfx9 loads and stores share one counter, and with a store pending the
+// compiler treats the counter as out of order and drains every outstanding
+// gather at the next use; a gather issued under a data-dependent condition has
+// the same effect.  Hence the edge loop has neither:
 //   - every batch is kSBatch edges fully unrolled, and every edge issues the
 //     gather for the edge kRing positions ahead (past the block's last edge it
 //     gathers row 0 of the same tensor, a valid address whose value is never
 //     used: edges past the end only touch the accumulator after the block's
-//     last row has been staged);
-//   - a finished row is staged in LDS (the workgroup owns at most kScatterRows
-//     rows) and written to HBM only where no gather is in flight: at the start
-//     of the last batch and at the end.
+//     last row has been written or staged);
+//   - a row that closes inside a batch is staged in LDS (kStageSlots per wave)
+//     and written to HBM during the next batch's phase 1, after the edge
+//     records it needs are in registers: the drain that the stores force then
+//     happens at the first gather of phase 2, by which time phase 1 has covered
+//     the latency of the gathers and of the stores;
+//   - a batch in which more than kStageSlots rows close (rows much shorter
+//     than the batch) takes a copy of the loop that writes each row as it
+//     closes and drains the counter at the end of the batch;
+//   - the last batch issues no gathers for a next batch, stages its rows the
+//     same way, and the remaining rows are written after it.
 // The per-edge control is one scalar bit test: `ends` (a 64-bit mask per batch,
 // built with scalar arithmetic from the row ends) marks the edges that close a
-// row; there the accumulator is staged and reset to zero.
+// row; there the accumulator is staged (or written) and reset to zero.
 // ---------------------------------------------------------------------------
-constexpr int kSBatch = 32;       // edges per batch (operators in LDS)
+constexpr int kSBatch = 64;       // edges per batch (operators in LDS, one edge per lane in phase 1)
 constexpr int kRing = 32;         // gathers in flight per lane (edges ahead)
-constexpr int kScatterRows = 11;  // row slots per workgroup (all staged in LDS)
+constexpr int kScatterRows = 11;  // row slots per workgroup
+constexpr int kStageSlots = 3;    // rows staged per wave between two flushes
 constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
 template <bool NORM, bool BUF, bool PERM>
@@ -349,12 +370,14 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const int64_t* __restrict__ perm, const int64_t* __restrict__ row_ptr,
     const int64_t* __restrict__ row_dst, float* __restrict__ out, int64_t n_rows, int C,
     int rows_per_block, int n_logical, uint32_t x_bytes) {
-    static_assert(kSBatch % 2 == 0 && kSBatch <= 64, "one edge per lane in phase 1");
+    static_assert(kSBatch == 64, "one edge per lane in phase 1, 64-bit row-end mask");
     static_assert(kSBatch % kRing == 0, "ring slots must line up across batches");
+    // 66.5 KB + 12 KB + row ranges: two workgroups per compute unit
     __shared__ __attribute__((aligned(16))) float sM[kSBatch * kMStride];
-    __shared__ float4 sStage[4][kScatterRows][64];
+    __shared__ float4 sStage[4][kStageSlots][64];
     __shared__ int64_t sRow[kScatterRows + 1];
     __shared__ int64_t sDst[kScatterRows];
+    __shared__ int64_t sNE[kScatterRows];  // output rows of the non-empty rows, in row order
 
     const int per_xcd = (n_logical + 7) / 8;
     const int logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
@@ -378,6 +401,16 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     }
     __syncthreads();
     const int64_t e0 = sRow[0], e1 = sRow[nrows];
+    auto put_out = [&](int64_t orow, float4 v) {
+        if (c < C && orow >= 0) *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
+    };
+    // list the non-empty rows (the empty ones are written as zeros at the end)
+    if (threadIdx.x < nrows && sRow[threadIdx.x + 1] > sRow[threadIdx.x]) {
+        int k = 0;
+        for (int i = 0; i < (int)threadIdx.x; ++i) k += sRow[i + 1] > sRow[i] ? 1 : 0;
+        sNE[k] = sDst[threadIdx.x];
+    }
+    __syncthreads();
 
     // Last edge of each non-empty row, relative to e0 (-1: empty or absent row).
     // Wave-uniform, kept in scalar registers.
@@ -391,12 +424,12 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
 
     // Edge records move through a three-stage pipeline so that no wait is on a
     // load younger than the gathers in flight: the edge id of batch b+3 (one
-    // load when PERM) and the record of batch b+2 are issued during batch b; the
-    // record of batch b+1 (its source rows feed this batch's gathers) and of
-    // batch b (phase 1) were issued one and two batches earlier.
+    // load when PERM) and the record of batch b+2 are issued at the start of
+    // batch b; the record of batch b+1 (its source rows feed this batch's
+    // gathers) and of batch b (phase 1) were issued one and two batches earlier.
     auto edge_id = [&](int64_t kbatch) -> int64_t {
         const int64_t k = kbatch + lane;
-        if (lane >= kSBatch || k >= e1) return -1;
+        if (k >= e1) return -1;
         if constexpr (PERM) return perm[k];
         else return k;
     };
@@ -413,8 +446,13 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
 
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
     v4f acc = zero4;
-    int slot = 0;  // staged rows so far (the non-empty rows, in order)
 
+    // Non-empty rows close in row order: k_ne of them have closed, k_out of
+    // those are written, and rows k_out .. k_ne-1 sit in sStage[w][0 ..).
+    int k_ne = 0, k_out = 0;
+    auto flush = [&]() {
+        for (int s = 0; k_out < k_ne; ++s, ++k_out) put_out(sNE[k_out], sStage[w][s][lane]);
+    };
     EdgeRec cur = record(edge_id(e0));
     EdgeRec nxt = record(edge_id(e0 + kSBatch));
     int64_t id2 = edge_id(e0 + 2 * kSBatch);
@@ -424,31 +462,64 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     // path, and the compiler would drain every gather at the loop latch.  (The
     // guard encloses the ring fill and the loop together for the same reason:
     // the loop header is reached only after the ring fill.)
-    // Write the rows that end at or before edge `upto` and are not written yet
-    // (staged rows in slot order; empty rows are zeros).
-    int r_out = 0, s_out = 0;
-    auto store_rows = [&](int64_t upto) {
-        for (; r_out < nrows && sRow[r_out + 1] <= upto; ++r_out) {
-            const int64_t orow = sDst[r_out];
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (sRow[r_out + 1] > sRow[r_out]) v = sStage[w][s_out++][lane];
-            if (c < C && orow >= 0)
-                *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
+    float4 ring[kRing];
+    // Per-half state of phase 2, shared with the last half's walk after the loops.
+    const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));
+    const float* mh = mrow;
+    float4 mr[kLdsAhead + 1];
+    int gsrc = 0, lsel = 0;
+    uint32_t ends_h = 0;
+    int64_t kh = e0;
+    bool direct = false;
+    // edge j of a half: four MFMAs into the row accumulator, the gather of the
+    // edge kRing positions ahead (GATHER), and where j closes a row its staging
+    // or, in a batch with more closing rows than staging slots, its store,
+    // waited for at once so that no store is pending where the paths meet
+    auto edge = [&](auto jj, auto gather_c) {
+        constexpr int j = decltype(jj)::value;
+        mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
+            *reinterpret_cast<const float4*>(mh + (j + kLdsAhead) * kMStride);
+        acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
+        // the slot's next gather after the MFMAs that read it: hoisted above
+        // them it would need a second register ring
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(gather_c)::value)
+            ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(gsrc, lsel + j), row_bytes);
+        if ((ends_h >> j) & 1u) {
+            const float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            if (!direct) {
+                sStage[w][k_ne - k_out][lane] = v;
+            } else {
+                put_out(sNE[k_ne], v);
+                ++k_out;
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            }
+            ++k_ne;
+            acc = zero4;
         }
     };
-    float4 ring[kRing];
-    if (e0 < e1) {
+    if (e0 == e1) goto done;
     static_for<kRing>([&](auto uu) {
         constexpr int u = decltype(uu)::value;
         ring[u] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, u), row_bytes);
     });
-    // The loop's back edge is taken from full batches only; the last batch
-    // (full or not) leaves through the tail path, which issues no gathers and
-    // walks only the groups of 8 edges that hold real edges.
     for (int64_t kb = e0;; kb += kSBatch) {
         const int nb = (int)min<int64_t>(kSBatch, e1 - kb);
         __syncthreads();
-        phase1_build<NORM>(cur, nb, sM);
+        // records of batch b+2 and the edge ids of b+3 (no load past e1)
+        const EdgeRec nn = record(id2);
+        id2 = edge_id(kb + 3 * kSBatch);
+        // the wait for this batch's records comes before the flush's stores
+        // (after them it would be a full drain): the empty asm takes the
+        // record as an operand, so its wait is placed here
+        asm volatile("" : "+v"(cur.x), "+v"(cur.y), "+v"(cur.z));
+        float Y[16];
+        edge_sh<NORM>(cur, Y);
+        // rows closed in the previous batch go to HBM here (see above)
+        __builtin_amdgcn_sched_barrier(0);
+        flush();
+        __builtin_amdgcn_sched_barrier(0);
+        if (lane < nb) edge_rows(Y, sM + lane * kMStride, w);
         // edges of this batch that close a row
         const int rel = (int)(kb - e0);
         uint64_t ends = 0;
@@ -457,64 +528,56 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             const int p = row_last[r] - rel;
             if (row_last[r] >= 0 && p >= 0 && p < kSBatch) ends |= 1ull << p;
         });
+        direct = __builtin_popcountll(ends) > kStageSlots;
+        // The flush's stores (and this batch's record loads) are waited for
+        // here, at the end of phase 1, where they have had its whole length to
+        // complete: pending at the half loop's header, they would make the
+        // compiler drain the gathers at the first edge of every half.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
-        const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));
-        float4 mr[kLdsAhead + 1];
-        // edge j: four MFMAs into the row accumulator, the gather of the edge
-        // kRing positions ahead (of the next batch only when NEXT), the row's
-        // staging when j closes it
-        auto edge = [&](auto jj, auto next_c) {
-            constexpr int j = decltype(jj)::value;
-            constexpr int jn = j + kRing;
-            if constexpr (j + kLdsAhead < kSBatch)
-                mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
-                    *reinterpret_cast<const float4*>(mrow + (j + kLdsAhead) * kMStride);
-            acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j % kRing], acc);
-            if constexpr (jn < kSBatch)
-                ring[j % kRing] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, jn), row_bytes);
-            else if constexpr (decltype(next_c)::value)
-                ring[j % kRing] =
-                    gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(nxt.src, jn - kSBatch), row_bytes);
-            if ((ends >> j) & 1ull) {
-                sStage[w][slot][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-                ++slot;
-                acc = zero4;
-            }
-        };
-        if (kb + kSBatch >= e1) {
-            // rows closed before this batch go to HBM now: the tail issues no
-            // gathers, so these stores hold nothing up, and the output is not
-            // written in one burst at the end of the kernel
-            store_rows(kb);
-            static_for<kLdsAhead>([&](auto qq) {
-                constexpr int q = decltype(qq)::value;
-                mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
-            });
-            static_for<kSBatch / 8>([&](auto gg) {
-                constexpr int g8 = decltype(gg)::value;
-                if (8 * g8 < nb)
-                    static_for<8>([&](auto ii) {
-                        edge(std::integral_constant<int, 8 * g8 + decltype(ii)::value>{},
-                             std::false_type{});
-                    });
-            });
-            break;
-        }
-        const EdgeRec nn = record(id2);
-        id2 = edge_id(kb + 3 * kSBatch);
-        // keep these loads ahead of the gathers: sunk below them, they would be
-        // the youngest loads when the next batch needs them
-        __builtin_amdgcn_sched_barrier(0);
         static_for<kLdsAhead>([&](auto qq) {
             constexpr int q = decltype(qq)::value;
             mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
         });
-        static_for<kSBatch>([&](auto jj) { edge(jj, std::true_type{}); });
+        // Phase 2 in two halves of kRing edges, a loop that is not unrolled:
+        // each ring slot is then defined once per iteration (by the gather
+        // kRing edges ahead) and stays in its registers.  Half h gathers the
+        // source rows of the edges kRing ahead from lanes lsel + j of gsrc:
+        // this batch's records (lanes 32..63) in half 0, the next batch's
+        // (lanes 0..31) in half 1.  The loop has one path: a half that is not
+        // full (last batch) leaves at its top for the walk after the loops,
+        // and the last full half leaves at its end (exits from inside a half
+        // would make the compiler wait for most gathers at every edge).
+#pragma clang loop unroll(disable)
+        for (int h = 0; h < kSBatch / kRing; ++h) {
+            const int jb = h * kRing;
+            mh = mrow + jb * kMStride;
+            gsrc = h == 0 ? cur.src : nxt.src;
+            lsel = h == 0 ? kRing : 0;
+            ends_h = (uint32_t)(ends >> jb);
+            kh = kb + jb;
+            if (kh + kRing > e1) goto partial;
+            static_for<kRing>([&](auto jj) { edge(jj, std::true_type{}); });
+            if (kh + kRing >= e1) goto done;
+        }
         cur = nxt;
         nxt = nn;
     }
-    }
-    store_rows(e1);
+partial:
+    // the last half, not full: the groups of 8 edges that hold real edges, no
+    // gathers (no edge follows); edges past e1 in the last group only touch the
+    // accumulator after the last row has closed
+    static_for<kRing / 8>([&](auto gg) {
+        constexpr int j8 = 8 * decltype(gg)::value;
+        if (kh + j8 < e1)
+            static_for<8>([&](auto ii) {
+                edge(std::integral_constant<int, j8 + decltype(ii)::value>{}, std::false_type{});
+            });
+    });
+done:
+    flush();
+    for (int r = 0; r < nrows; ++r)
+        if (sRow[r + 1] == sRow[r]) put_out(sDst[r], make_float4(0.f, 0.f, 0.f, 0.f));
 }
 
 // ---------------------------------------------------------------------------

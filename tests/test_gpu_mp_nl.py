@@ -381,3 +381,38 @@ def test_schedule_with_col_perm_matches_fused_message_passing_simple(bm, dev):
                                      False)
     ref = bm.fused_message_passing_simple(x.to(dev), vec.to(dev), ei, rp, ci)
     assert torch.equal(out, ref)
+
+
+def test_scatter_batch_boundaries(bm, dev):
+    """Index order with 11 destinations per workgroup (n = 512 * 11, C = 16) and
+    degree patterns that put row ends on both sides of the 32- and 64-edge
+    boundaries: rows of exactly 32, 64, 96 edges, a batch whose last edge closes a
+    row, batches with more closing rows than staging slots (written as they
+    close) next to staged ones, empty rows between, and single long rows."""
+    patterns = [
+        [64] + [0] * 10, [32] + [0] * 10, [33], [31], [63], [65], [96], [127], [128], [200],
+        [1] * 11, [5] * 11, [10, 10, 10, 10, 10, 10, 4], [20, 20, 20, 4], [21, 21, 22],
+        [64, 64, 64], [0, 0, 30, 0, 34, 0], [100, 1, 1, 1, 1, 1], [30] * 11,
+        [16, 16, 16, 16, 16, 16, 16, 16], [3, 61, 3, 61], [0] * 11,
+    ]
+    n_wg = 512
+    deg = []
+    for k in range(n_wg):
+        p = patterns[k % len(patterns)]
+        deg += (p + [0] * 11)[:11]
+    deg = torch.tensor(deg, dtype=torch.int64)
+    n = deg.numel()
+    c = 16
+    dst = torch.repeat_interleave(torch.arange(n), deg)
+    e = dst.numel()
+    src = torch.randint(0, n, (e,), generator=gen(71))
+    vec = unit_vectors(e, 72) * (0.5 + torch.rand(e, 1, generator=gen(73)))
+    x = torch.randn(n, c, 16, generator=gen(74))
+    rp = torch.zeros(n + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(deg, 0)
+    out = bm.sh_tp_scatter(vec.to(dev), x.to(dev), src.to(dev), rp.to(dev), None, True)
+    want = omp.sh_tp_scatter(vec.double().numpy(), x.double().numpy(), src.numpy(), dst.numpy(), n,
+                             normalize=True)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    assert out[deg == 0].abs().max().item() == 0.0
+    assert torch.equal(out, bm.sh_tp_scatter(vec.to(dev), x.to(dev), src.to(dev), rp.to(dev), None, True))
