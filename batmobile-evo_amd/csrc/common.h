@@ -72,6 +72,16 @@ __device__ __forceinline__ float4 buffer_ld4(__amdgpu_buffer_rsrc_t r, int voff,
                        __int_as_float(v[3]));
 }
 
+// Index-mode buffer load (buffer_load_dwordx4 ... idxen offen): 16 bytes at
+// base + vindex * stride + voffset + soffset, the stride taken from the
+// descriptor (at most 16383 bytes on gfx9).  vindex and voffset are VGPRs, so a
+// row index that is uniform across the wave needs no scalar register.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+__device__ v4i_t struct_buffer_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset,
+                                         int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+constexpr int kMaxBufferStride = 16383;
+
 __device__ __forceinline__ v4f mfma4(const float4 a, const float4 b, v4f acc) {
     acc = mfma1(a.x, b.x, acc);
     acc = mfma1(a.y, b.y, acc);
@@ -242,6 +252,13 @@ constexpr int fwd_slot_pos(int q) {
 // small helpers
 // ---------------------------------------------------------------------------
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// A wave-uniform 64-bit value in scalar registers.
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 }  // namespace bmhip
 

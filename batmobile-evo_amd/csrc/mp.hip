@@ -364,7 +364,7 @@ constexpr int kScatterRows = 11;  // row slots per workgroup
 constexpr int kStageSlots = 3;    // rows staged per wave between two flushes
 constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
-template <bool NORM, bool BUF, bool PERM>
+template <bool NORM, bool BUF, bool PERM, bool IDX>
 __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const float* __restrict__ vec, const float* __restrict__ X, const int64_t* __restrict__ src_idx,
     const int64_t* __restrict__ perm, const int64_t* __restrict__ row_ptr,
@@ -372,12 +372,15 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     int rows_per_block, int n_logical, uint32_t x_bytes) {
     static_assert(kSBatch == 64, "one edge per lane in phase 1, 64-bit row-end mask");
     static_assert(kSBatch % kRing == 0, "ring slots must line up across batches");
+    static_assert(!IDX || BUF, "index-mode gathers use the buffer descriptor");
     // 66.5 KB + 12 KB + row ranges: two workgroups per compute unit
     __shared__ __attribute__((aligned(16))) float sM[kSBatch * kMStride];
     __shared__ float4 sStage[4][kStageSlots][64];
     __shared__ int64_t sRow[kScatterRows + 1];
     __shared__ int64_t sDst[kScatterRows];
     __shared__ int64_t sNE[kScatterRows];  // output rows of the non-empty rows, in row order
+    // IDX: source rows of the gather targets, entry t for edge kb + kRing + t
+    __shared__ int sTgt[kSBatch];
 
     const int per_xcd = (n_logical + 7) / 8;
     const int logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
@@ -392,6 +395,10 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const int voff = (c < C ? c : C - 1) * 64 + g * 16;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(X), (short)0, BUF ? (int)x_bytes : 0, kBufferDword3);
+    // IDX: rows of row_bytes as records (index = source row, no scalar offset)
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), (short)(IDX ? row_bytes : 0u), IDX ? (int)(x_bytes / row_bytes) : 0,
+        kBufferDword3);
 
     const int64_t d0 = (int64_t)logical * rows_per_block;
     const int nrows = (int)(min<int64_t>(n_rows, d0 + rows_per_block) - d0);
@@ -400,7 +407,8 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         if (i < nrows) sDst[i] = row_dst ? row_dst[d0 + i] : d0 + i;
     }
     __syncthreads();
-    const int64_t e0 = sRow[0], e1 = sRow[nrows];
+    // the edge range in scalar registers (compared at every half)
+    const int64_t e0 = uniform_i64(sRow[0]), e1 = uniform_i64(sRow[nrows]);
     auto put_out = [&](int64_t orow, float4 v) {
         if (c < C && orow >= 0) *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
     };
@@ -467,10 +475,11 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));
     const float* mh = mrow;
     float4 mr[kLdsAhead + 1];
+    const int* th = sTgt;
     int gsrc = 0, lsel = 0;
     uint32_t ends_h = 0;
     int64_t kh = e0;
-    bool direct = false;
+    int direct = 0;  // wave-uniform: rows of this batch are written as they close
     // edge j of a half: four MFMAs into the row accumulator, the gather of the
     // edge kRing positions ahead (GATHER), and where j closes a row its staging
     // or, in a batch with more closing rows than staging slots, its store,
@@ -479,15 +488,25 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         constexpr int j = decltype(jj)::value;
         mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
             *reinterpret_cast<const float4*>(mh + (j + kLdsAhead) * kMStride);
+        // IDX: the gather's source row, read before the MFMAs that cover its latency
+        int tg = 0;
+        if constexpr (IDX && decltype(gather_c)::value) tg = th[j];
         acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
         // the slot's next gather after the MFMAs that read it: hoisted above
         // them it would need a second register ring
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (decltype(gather_c)::value)
-            ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(gsrc, lsel + j), row_bytes);
+        if constexpr (decltype(gather_c)::value) {
+            if constexpr (IDX) {
+                const v4i_t r = struct_buffer_load_b128(xs, tg, voff, 0, 0);
+                ring[j] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                                      __int_as_float(r.w));
+            } else {
+                ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(gsrc, lsel + j), row_bytes);
+            }
+        }
         if ((ends_h >> j) & 1u) {
             const float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
-            if (!direct) {
+            if (direct == 0) {
                 sStage[w][k_ne - k_out][lane] = v;
             } else {
                 put_out(sNE[k_ne], v);
@@ -520,6 +539,8 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         flush();
         __builtin_amdgcn_sched_barrier(0);
         if (lane < nb) edge_rows(Y, sM + lane * kMStride, w);
+        if constexpr (IDX)
+            if (w == 0) sTgt[(lane + kRing) & (kSBatch - 1)] = lane >= kRing ? cur.src : nxt.src;
         // edges of this batch that close a row
         const int rel = (int)(kb - e0);
         uint64_t ends = 0;
@@ -528,7 +549,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             const int p = row_last[r] - rel;
             if (row_last[r] >= 0 && p >= 0 && p < kSBatch) ends |= 1ull << p;
         });
-        direct = __builtin_popcountll(ends) > kStageSlots;
+        direct = __builtin_amdgcn_readfirstlane(__builtin_popcountll(ends) > kStageSlots ? 1 : 0);
         // The flush's stores (and this batch's record loads) are waited for
         // here, at the end of phase 1, where they have had its whole length to
         // complete: pending at the half loop's header, they would make the
@@ -552,6 +573,10 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         for (int h = 0; h < kSBatch / kRing; ++h) {
             const int jb = h * kRing;
             mh = mrow + jb * kMStride;
+            // the table address of the half in one VGPR: voff >> 30 is 0, but
+            // not known to be uniform, so the address is not rebuilt from a
+            // scalar register at every edge
+            th = sTgt + jb + (voff >> 30);
             gsrc = h == 0 ? cur.src : nxt.src;
             lsel = h == 0 ? kRing : 0;
             ends_h = (uint32_t)(ends >> jb);
@@ -733,16 +758,20 @@ static int launch_mp(bool scatter, bool norm, const float* vec, const float* X, 
     const int64_t xb = n_src * (int64_t)C * 64;
     const bool buf = xb <= (int64_t)INT32_MAX;
     const uint32_t x_bytes = buf ? (uint32_t)xb : 0u;
+    // index-mode gathers: rows fit the descriptor's stride field
+    const bool idx = buf && (int64_t)C * 64 <= kMaxBufferStride;
 #define BM_LAUNCH(NO, BU)                                                                    \
     mp_simple_mfma_kernel<false, NO, BU><<<grid, kMpBlock, 0, s>>>(                           \
         vec, X, src_idx, perm, row_ptr, row_dst, out, n_items, n_edges, C, (int)per,          \
         (int)n_logical, x_bytes)
-#define BM_LAUNCH_SC(NO, BU, PE)                                                             \
-    mp_scatter_kernel<NO, BU, PE><<<grid, kMpBlock, 0, s>>>(vec, X, src_idx, perm, row_ptr,   \
-                                                            row_dst, out, n_items, C,         \
-                                                            (int)per, (int)n_logical, x_bytes)
+#define BM_LAUNCH_SC(NO, BU, PE, IX)                                                         \
+    mp_scatter_kernel<NO, BU, PE, IX><<<grid, kMpBlock, 0, s>>>(vec, X, src_idx, perm, row_ptr, \
+                                                                row_dst, out, n_items, C,       \
+                                                                (int)per, (int)n_logical, x_bytes)
+#define BM_LAUNCH_SC3(NO, BU, PE)                                                            \
+    do { if (idx) BM_LAUNCH_SC(NO, true, PE, true); else BM_LAUNCH_SC(NO, BU, PE, false); } while (0)
 #define BM_LAUNCH_SC2(NO, BU) \
-    do { if (perm) BM_LAUNCH_SC(NO, BU, true); else BM_LAUNCH_SC(NO, BU, false); } while (0)
+    do { if (perm) BM_LAUNCH_SC3(NO, BU, true); else BM_LAUNCH_SC3(NO, BU, false); } while (0)
     if (scatter) {
         if (norm) {
             if (buf) BM_LAUNCH_SC2(true, true); else BM_LAUNCH_SC2(true, false);
@@ -757,6 +786,7 @@ static int launch_mp(bool scatter, bool norm, const float* vec, const float* X, 
         }
     }
 #undef BM_LAUNCH_SC2
+#undef BM_LAUNCH_SC3
 #undef BM_LAUNCH_SC
 #undef BM_LAUNCH
     return (int)hipGetLastError();
