@@ -119,6 +119,73 @@ __device__ __forceinline__ void sh_forward(float x, float y, float z, float* Y) 
     });
 }
 
+// Coefficient of x^a y^b z^c in component k of the expanded recurrence (0 if absent).
+constexpr float sh_mono(int k, int a, int b, int c) {
+    for (int i = 0; i < kSHMonoCount; ++i)
+        if (kSHMono[i].k == k && kSHMono[i].a == a && kSHMono[i].b == b && kSHMono[i].c == c)
+            return kSHMono[i].v;
+    return 0.0f;
+}
+constexpr int sh_mono_terms(int k) {
+    int n = 0;
+    for (int i = 0; i < kSHMonoCount; ++i) n += kSHMono[i].k == k ? 1 : 0;
+    return n;
+}
+
+// The same Y (L = 3) as sh_forward<3>, as closed-form polynomials over shared
+// subexpressions (x^2, y^2, z^2, s = x^2 + z^2, d = z^2 - x^2): 33 operations
+// against about 70 for the recurrence.  The coefficients are those of the
+// expanded recurrence; the static_asserts check every term the factored form
+// relies on (and that there are no others).
+__device__ __forceinline__ void sh_forward_l3(float x, float y, float z, float* Y) {
+    constexpr float c1 = sh_mono(1, 1, 0, 0);
+    static_assert(c1 == sh_mono(2, 0, 1, 0) && c1 == sh_mono(3, 0, 0, 1), "l=1");
+    constexpr float c4 = sh_mono(4, 1, 0, 1), c7 = sh_mono(7, 0, 1, 1);
+    static_assert(c4 == sh_mono(5, 1, 1, 0), "xz and xy share a coefficient");
+    constexpr float c6y = sh_mono(6, 0, 2, 0), c6s = sh_mono(6, 2, 0, 0);
+    static_assert(c6s == sh_mono(6, 0, 0, 2), "Y6 = c6y y^2 + c6s (x^2 + z^2)");
+    constexpr float c8 = sh_mono(8, 0, 0, 2);
+    static_assert(-c8 == sh_mono(8, 2, 0, 0), "Y8 = c8 (z^2 - x^2)");
+    constexpr float c9z = sh_mono(9, 1, 0, 2), c9x = sh_mono(9, 3, 0, 0);
+    constexpr float c10 = sh_mono(10, 1, 1, 1);
+    constexpr float c11y = sh_mono(11, 1, 2, 0), c11s = sh_mono(11, 3, 0, 0);
+    static_assert(c11s == sh_mono(11, 1, 0, 2), "Y11 = x (c11y y^2 + c11s s)");
+    static_assert(c11y == sh_mono(13, 0, 2, 1) && c11s == sh_mono(13, 0, 0, 3) &&
+                      c11s == sh_mono(13, 2, 0, 1), "Y13 = z (c11y y^2 + c11s s)");
+    constexpr float c12y = sh_mono(12, 0, 3, 0), c12s = sh_mono(12, 2, 1, 0);
+    static_assert(c12s == sh_mono(12, 0, 1, 2), "Y12 = y (c12y y^2 + c12s s)");
+    constexpr float c14 = sh_mono(14, 0, 1, 2);
+    static_assert(-c14 == sh_mono(14, 2, 1, 0), "Y14 = c14 y (z^2 - x^2)");
+    constexpr float c15z = sh_mono(15, 0, 0, 3), c15x = sh_mono(15, 2, 0, 1);
+    static_assert(sh_mono(0, 0, 0, 0) == 1.0f && sh_mono_terms(0) == 1, "Y0");
+    static_assert(sh_mono_terms(1) == 1 && sh_mono_terms(2) == 1 && sh_mono_terms(3) == 1 &&
+                      sh_mono_terms(4) == 1 && sh_mono_terms(5) == 1 && sh_mono_terms(6) == 3 &&
+                      sh_mono_terms(7) == 1 && sh_mono_terms(8) == 2 && sh_mono_terms(9) == 2 &&
+                      sh_mono_terms(10) == 1 && sh_mono_terms(11) == 3 && sh_mono_terms(12) == 3 &&
+                      sh_mono_terms(13) == 3 && sh_mono_terms(14) == 2 && sh_mono_terms(15) == 2,
+                  "no other terms");
+    const float xx = x * x, yy = y * y, zz = z * z;
+    const float s = xx + zz, d = zz - xx;
+    Y[0] = 1.0f;
+    Y[1] = c1 * x;
+    Y[2] = c1 * y;
+    Y[3] = c1 * z;
+    const float cx = c4 * x;
+    Y[4] = cx * z;
+    Y[5] = cx * y;
+    Y[6] = fmaf(yy, c6y, c6s * s);
+    Y[7] = (c7 * y) * z;
+    Y[8] = c8 * d;
+    Y[9] = x * fmaf(zz, c9z, c9x * xx);
+    Y[10] = (Y[5] * z) * (c10 / c4);
+    const float t = fmaf(yy, c11y, c11s * s);
+    Y[11] = x * t;
+    Y[12] = y * fmaf(yy, c12y, c12s * s);
+    Y[13] = z * t;
+    Y[14] = (c14 * y) * d;
+    Y[15] = z * fmaf(zz, c15z, c15x * xx);
+}
+
 // Reverse-mode gradient of sh_forward: g (dL/dY, clobbered) -> dL/d(x,y,z).
 template <int L>
 __device__ __forceinline__ void sh_backward(float x, float y, float z, const float* Y, float* g,

@@ -123,6 +123,23 @@ def sh_recurrence():
     return steps
 
 
+def sh_polynomials(lmax=LMAX_TP):
+    """The recurrence expanded into monomials: per degree l and component M a
+    dict {(a, b, c): coeff} of x^a y^b z^c (homogeneous of degree l)."""
+    steps = sh_recurrence()
+    polys = [[{(0, 0, 0): 1.0}]]
+    for l in range(lmax):
+        new = [dict() for _ in range(2 * l + 3)]
+        for (M, m, j, c) in steps[l]:
+            for mono, v in polys[-1][m].items():
+                e = list(mono)
+                e[j] += 1
+                e = tuple(e)
+                new[M][e] = new[M].get(e, 0.0) + c * v
+        polys.append([{k: v for k, v in d.items() if abs(v) > 1e-12} for d in new])
+    return polys
+
+
 def _flit(v):
     return repr(float(v)) + "f" if "e" in repr(float(v)) or "." in repr(float(v)) else repr(float(v)) + ".0f"
 
@@ -204,6 +221,20 @@ def render():
         for (M, m, j, c) in terms:
             rows.append(f"    {{{M}, {m}, {j}, {_flit(c)}}}  /* l={l+1} */")
     w(",\n".join(rows))
+    w("};")
+    w("")
+    polys = sh_polynomials()
+    w("// The recurrence expanded for L <= 3: Y[l*l + M] = sum coeff * x^a y^b z^c.")
+    w("struct SHMono {")
+    w("    int k;     // component 0..15")
+    w("    int a, b, c;")
+    w("    float v;")
+    w("};")
+    mono = [(l * l + M, e, v) for l in range(LMAX_TP + 1) for M, d in enumerate(polys[l])
+            for e, v in sorted(d.items())]
+    w(f"constexpr int kSHMonoCount = {len(mono)};")
+    w("constexpr SHMono kSHMono[kSHMonoCount] = {")
+    w(",\n".join(f"    {{{k}, {e[0]}, {e[1]}, {e[2]}, {_flit(v)}}}" for k, e, v in mono))
     w("};")
     w("")
     w("}  // namespace bmhip")

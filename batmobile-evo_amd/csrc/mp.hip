@@ -89,7 +89,7 @@ __device__ __forceinline__ void edge_sh(EdgeRec r, float* Y) {
         y *= inv;
         z *= inv;
     }
-    sh_forward<3>(x, y, z, Y);
+    sh_forward_l3(x, y, z, Y);
 }
 
 // Wave w's four operator rows of one edge, from its Y, into sMj.
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     if (logical >= n_logical) return;
 
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int g = lane >> 4;
     const int i16 = lane & 15;
     const int c = blockIdx.y * kChanGroup + w * 16 + i16;
@@ -1469,7 +1469,7 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
                 const int64_t e = perm ? perm[slot] : slot;
                 float x = vec[e * 3 + 0], y = vec[e * 3 + 1], z = vec[e * 3 + 2];
                 if (normalize) normalize3(x, y, z);
-                sh_forward<3>(x, y, z, Y);
+                sh_forward_l3(x, y, z, Y);
                 src = (int)src_idx[e];
             } else {
 #pragma unroll
