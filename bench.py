@@ -464,7 +464,7 @@ def main():
     achieved_gbs = bytes_alg / (kernel_ms * 1e-3) / 1e9
     achieved_tf = flops_alg / (kernel_ms * 1e-3) / 1e12
 
-    traffic, traffic_note = measured_traffic("mp_scatter_kernel<true, true, true>", "configs[3]")
+    traffic, traffic_note = measured_traffic("mp_scatter_kernel<true, true, true, true>", "configs[3]")
 
     extra = {}
     if not a.headline_only:
@@ -495,7 +495,7 @@ def main():
             "workload": "configs[3] fused SH+TP+scatter, simple variant: N=5000 atoms, C=64, "
                         "cutoff 5.0 A (~30 nbr), edges sorted by destination, in-kernel normalisation",
             "N_atoms": N_ATOMS, "C": C, "E": E, "box_A": round(w["L"], 4), "seed": SEED,
-            "kernel": "mp_scatter_kernel<NORM=true, BUF=true, PERM=true> "
+            "kernel": "mp_scatter_kernel<NORM=true, BUF=true, PERM=true, IDX=true> "
                       "(batmobile.Graph.sh_tp_scatter: spatial schedule)",
             "reference_published_rtx3090_ms": 5.935,
         },
