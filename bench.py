@@ -297,36 +297,53 @@ def mace_config4(torch, bm, dev, reps=3):
     cell = torch.diag(torch.tensor([L, L, L]))
     x = torch.randn(n, c, 16, generator=g).to(dev)
     go = torch.randn(n, c, 16, generator=g).to(dev)
-    layer = bm.MACEInteraction(c, CUTOFF, device=dev, generator=g)
+    layer = bm.MACEInteraction(c, CUTOFF, device=dev, generator=g, save_edge_weights=True)
     graph = bm.Graph(pos, cell, CUTOFF, c)
     graph.reverse_edges()
     build = time_call(torch, lambda: (bm.Graph(pos, cell, CUTOFF, c).reverse_edges()), reps)
     p = pos.clone().requires_grad_(True)
-    fwd, bwd = [], []
-    for _ in range(reps + 1):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        out = layer(graph, p, x)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        out.backward(go)
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        fwd.append(t1 - t0)
-        bwd.append(t2 - t1)
-        p.grad = None
+
+    def run(lay, n_rep):
+        fwd, bwd = [], []
+        for _ in range(n_rep + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = lay(graph, p, x)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            out.backward(go)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            fwd.append(t1 - t0)
+            bwd.append(t2 - t1)
+            p.grad = None
+            del out
+        return min(fwd[1:]), min(bwd[1:])
+
+    torch.cuda.reset_peak_memory_stats(dev)
+    t_f, t_b = run(layer, reps)
+    peak = torch.cuda.max_memory_allocated(dev)
+    # the same layer without the saved weights: the backward recomputes them
+    layer.save_edge_weights = False
+    torch.cuda.reset_peak_memory_stats(dev)
+    _, t_b_re = run(layer, 1)
+    peak_re = torch.cuda.max_memory_allocated(dev)
+    layer.save_edge_weights = True
     e = graph.num_edges
     # the forward keeps the per-edge weights for the backward (positions require grad),
     # so the backward runs the MLP's transpose GEMM only
     f_fwd = e * (2 * (8 * 64 + 64 * 34 * c) + (1222 + 312) * c)
     f_bwd = e * (2 * (8 * 64 + 64 * 34 * c) + 2 * (1222 + 312) * c)
-    t_f, t_b = min(fwd[1:]), min(bwd[1:])
     return {
         "cfg4_mace_N": n, "cfg4_mace_C": c, "cfg4_mace_E": e,
         "cfg4_mace_graph_build_ms": round(build, 3),
         "cfg4_mace_fwd_ms": round(t_f * 1e3, 3), "cfg4_mace_bwd_ms": round(t_b * 1e3, 3),
         "cfg4_mace_fwd_TFLOPs": round(f_fwd / t_f / 1e12, 2),
         "cfg4_mace_bwd_TFLOPs": round(f_bwd / t_b / 1e12, 2),
+        "cfg4_mace_saved_edge_weights_GB": round(layer.edge_weight_bytes(graph) / 1e9, 2),
+        "cfg4_mace_peak_device_GB": round(peak / 1e9, 2),
+        "cfg4_mace_bwd_recompute_ms": round(t_b_re * 1e3, 3),
+        "cfg4_mace_peak_device_GB_recompute": round(peak_re / 1e9, 2),
     }
 
 

@@ -131,3 +131,60 @@ def test_mace_row_order_does_not_change_results(bm, dev):
         bm.mace_forward(*args, 5.0, None, graph.order[:-1].contiguous())
     with pytest.raises(RuntimeError, match="order"):
         bm.mace_forward(*args, 5.0, None, graph.order.to(torch.int32))
+
+
+def test_config4_full_size(bm, dev):
+    """configs[4] as bench.py runs it: N = 50,000, C = 128, ~1.5M edges in six chunks, the
+    per-edge weights saved by the forward.  Outputs of 100 sampled destinations against the
+    float64 oracle restricted to their incoming edges; forces on 100 sampled atoms against the
+    oracle over the edges incident to them (no other edge depends on their positions); the
+    forces sum to zero; two runs are bitwise identical; the backward from the saved weights
+    equals the one that recomputes them."""
+    import batmobile
+    n, c = 50000, 128
+    pos, cell = periodic_box(n, 4)
+    graph = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+    layer = batmobile.MACEInteraction(c, 5.0, device=dev, generator=gen(5), save_edge_weights=True)
+    x = torch.randn(n, c, 16, generator=gen(6))
+    go = torch.randn(n, c, 16, generator=gen(7))
+    e = graph.num_edges
+    assert e > 5 * 262144, e   # six edge chunks
+    torch.cuda.reset_peak_memory_stats(dev)
+    outs, grads = [], []
+    for _ in range(2):
+        p = pos.to(dev).requires_grad_(True)
+        o = layer(graph, p, x.to(dev))
+        o.backward(go.to(dev))
+        outs.append(o.detach().cpu())
+        grads.append(p.grad.cpu())
+        del o, p
+    peak = torch.cuda.max_memory_allocated(dev)
+    print(f"configs[4] E={e} saved R {layer.edge_weight_bytes(graph) / 1e9:.2f} GB, "
+          f"peak device memory {peak / 1e9:.2f} GB", flush=True)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
+    out, grad = outs[0], grads[0]
+    # the forces sum to zero (translation invariance)
+    assert grad.sum(0).abs().max().item() <= 1e-5 * grad.abs().sum().item()
+
+    src, dst = graph.src.cpu(), graph.dst.cpu()
+    box = torch.diagonal(cell).numpy().astype(np.float64)
+    w1, b1, w2 = (t.cpu().numpy() for t in (layer.W1, layer.b1, layer.W2))
+    sample = torch.randperm(n, generator=gen(8))[:100]
+    # outputs: the sampled destinations' incoming edges only
+    sel = torch.isin(dst, sample)
+    ref_out, _ = om.layer_and_position_grad(pos.numpy(), box, x.numpy(), src[sel].numpy(),
+                                            dst[sel].numpy(), w1, b1, w2, 5.0,
+                                            np.zeros((n, c, 16)))
+    assert normwise_err(out[sample], ref_out[sample.numpy()]) <= 1e-5
+    # forces: every edge whose source or destination is a sampled atom
+    sel = torch.isin(dst, sample) | torch.isin(src, sample)
+    _, ref_grad = om.layer_and_position_grad(pos.numpy(), box, x.numpy(), src[sel].numpy(),
+                                             dst[sel].numpy(), w1, b1, w2, 5.0, go.numpy())
+    assert normwise_err(grad[sample], ref_grad[sample.numpy()]) <= 1e-4
+
+    # the backward that recomputes the per-edge weights gives the same forces
+    layer.save_edge_weights = False
+    p = pos.to(dev).requires_grad_(True)
+    o = layer(graph, p, x.to(dev))
+    o.backward(go.to(dev))
+    assert torch.equal(o.detach().cpu(), out) and torch.equal(p.grad.cpu(), grad)
