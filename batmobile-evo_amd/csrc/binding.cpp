@@ -652,6 +652,51 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
     return {edge_index, vec, offsets};
 }
 
+// Extension for batmobile.Graph: the neighbor list in the message-passing layout,
+// (src int64 [E] = j, dst int64 [E] = i, edge_vectors [E, 3] = minimum-image
+// pos[i] - pos[j], row_offsets int64 [N+1], spatial order int64 [N]), edges
+// grouped by destination i and src ascending within; the neighbor_list result read
+// with roles swapped.
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor> neighbor_graph(
+    const torch::Tensor& positions, const torch::Tensor& cell, double cutoff, bool self_loops) {
+    TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
+    TORCH_CHECK(positions.dtype() == torch::kFloat32, "positions must be float32");
+    TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
+    check_device(positions, "positions");
+    const int64_t N = positions.size(0);
+    torch::Tensor cell_cpu = cell.detach().to(torch::kCPU, torch::kFloat32).contiguous();
+    const float* h = cell_cpu.data_ptr<float>();
+    const float box[3] = {h[0], h[4], h[8]};
+    const float rc = (float)cutoff;
+    const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, rc);
+    TORCH_CHECK(wsb > 0, "invalid cell or cutoff");
+    auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(positions.device());
+    auto i32 = torch::TensorOptions().dtype(torch::kInt32).device(positions.device());
+    const c10::DeviceGuard guard(positions.device());
+    hipStream_t s = current_stream(positions);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
+    torch::Tensor total = torch::empty({1}, i64);
+    check_status(batteries_neighbor_list_count(cptr<float>(positions, "positions"), box, N, rc,
+                                               self_loops ? 1 : 0, ws.data_ptr(), wsb,
+                                               total.data_ptr<int64_t>(), s),
+                 "neighbor_graph");
+    const int64_t E = total.item<int64_t>();  // one host sync, as in the reference
+    torch::Tensor tmp_j = torch::empty({E}, i32);
+    torch::Tensor tmp_vec = torch::empty({E, 3}, f32_like(positions));
+    torch::Tensor src = torch::empty({E}, i64);
+    torch::Tensor dst = torch::empty({E}, i64);
+    torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
+    torch::Tensor offsets = torch::empty({N + 1}, i64);
+    torch::Tensor order = torch::empty({N}, i64);
+    check_status(batteries_neighbor_graph_write(
+                     cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
+                     ws.data_ptr(), wsb, tmp_j.data_ptr<int>(), tmp_vec.data_ptr<float>(),
+                     src.data_ptr<int64_t>(), dst.data_ptr<int64_t>(), vec.data_ptr<float>(),
+                     offsets.data_ptr<int64_t>(), order.data_ptr<int64_t>(), s),
+                 "neighbor_graph");
+    return {src, dst, vec, offsets, order};
+}
+
 torch::Tensor selftest_mfma_16x16x4(const torch::Tensor& A, const torch::Tensor& B) {
     TORCH_CHECK(A.numel() == 64 && B.numel() == 64 && A.dtype() == torch::kFloat32 &&
                     B.dtype() == torch::kFloat32,
@@ -891,6 +936,9 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("node_features"), py::arg("weights"), py::arg("source_idx"), py::arg("row_ptr"),
           py::arg("perm") = py::none(), py::arg("order") = py::none(), py::arg("normalize") = true,
           "Fused SH + weighted TP (W [34, C_in, C_out]) + scatter-add over CSR rows");
+    m.def("neighbor_graph", &neighbor_graph, py::arg("positions"), py::arg("cell"),
+          py::arg("cutoff"), py::arg("self_loops") = false,
+          "neighbor list in the message-passing layout: (src = j, dst = i, pos[i] - pos[j], row_offsets, spatial_order)");
     m.def("neighbor_list", &neighbor_list, py::arg("positions"), py::arg("cell"),
           py::arg("cutoff"), py::arg("self_loops") = false,
           "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], row_offsets)");

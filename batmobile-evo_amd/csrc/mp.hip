@@ -1099,17 +1099,220 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
     }
 }
 
-__global__ void sched_edges_kernel(const int64_t* __restrict__ row_ptr,
-                                   const int64_t* __restrict__ col_perm,
-                                   const int64_t* __restrict__ row_dst,
-                                   const int64_t* __restrict__ row_ptr_s,
-                                   int64_t* __restrict__ edge_perm, int64_t n_sched) {
-    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= n_sched) return;
+// The same dealing and swap rounds as sched_balance_kernel, by a block of four
+// waves per group (Qg <= 64 workgroups; lane k of wave 0 = workgroup k, whose
+// slots it keeps in registers).  Ranks come from comparing every key with each
+// other one: rows heaviest first, key deg * 64 + (63 - k); workgroups lightest
+// first, key load * 64 + k (the tie rules of the block version; keys fit 32
+// bits when the edges number under 2^25).  The four waves rank the slices' rows
+// in parallel, and each workgroup ranking is split between them (16 keys per
+// wave, partial counts added through LDS).  Rows and swap partners are
+// exchanged by rank through LDS.  At configs[3]: 68 us for the block version
+// (serial LDS loops in one active wave).
+constexpr int kBalWaves = 4;
+__global__ __launch_bounds__(64 * kBalWaves) void sched_balance_wave_kernel(
+    const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
+    const int64_t* __restrict__ gb, int64_t n_dst, int P, int Q, int R,
+    int64_t* __restrict__ row_dst, int64_t* __restrict__ slot_deg) {
+    __shared__ __attribute__((aligned(16))) int sRk[kScatterRows][64];  // row keys per slice
+    __shared__ __attribute__((aligned(16))) int sKey[64];               // workgroup load keys
+    __shared__ int sPart[kBalWaves][64];      // partial load ranks
+    __shared__ int sRowAt[kScatterRows][64];  // row offset (in the group) of row rank r
+    __shared__ int sDegAt[kScatterRows][64];
+    __shared__ int sA[64][kScatterRows];  // slot degrees of the workgroup of load rank r
+    __shared__ int sP[64][kScatterRows];  // slot rows of the workgroup of load rank r
+    __shared__ int sL[64];                // load of the workgroup of load rank r
+    const int G = (P + Q - 1) / Q;
+    const int gi = blockIdx.x;
+    const int x = gi / G, gen = gi - x * G;
+    const int Qg = min(Q, P - gen * Q);
+    const int k = threadIdx.x & 63;
+    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t s0 = gb[gi], s1 = gb[gi + 1];
+    const int n = (int)(s1 - s0);
+    const int T = (n + Qg - 1) / Qg;  // <= R: a group holds at most Qg * R rows
+    if (n <= 0) {  // no rows: every slot empty
+        if (v == 0 && k < Qg) {
+            const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
+            for (int t = 0; t < R; ++t) {
+                row_dst[b * R + t] = -1;
+                slot_deg[b * R + t] = 0;
+            }
+        }
+        return;
+    }
+    auto wave_sync = [] {
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS accesses are done
+        __builtin_amdgcn_wave_barrier();
+    };
+    // how many of the keys [4 Q0, 4 Q0 + 4 NQ) rank before key
+    auto count_before = [&](const int* keys, int key, bool desc, auto q0_c, auto nq_c) {
+        constexpr int Q0 = decltype(q0_c)::value, NQ = decltype(nq_c)::value;
+        int r = 0;
+        static_for<NQ>([&](auto qq) {
+            const int4 w = reinterpret_cast<const int4*>(keys)[Q0 + decltype(qq)::value];
+            if (desc) r += (w.x > key) + (w.y > key) + (w.z > key) + (w.w > key);
+            else r += (w.x < key) + (w.y < key) + (w.z < key) + (w.w < key);
+        });
+        return r;
+    };
+    // load rank of lane k's workgroup (wave 0 holds the loads): sKey written by wave
+    // 0, every wave counts over its 16 keys, wave 0 adds the partials
+    auto load_rank = [&](int load) {
+        if (v == 0) sKey[k] = k < Qg ? load * 64 + k : INT32_MAX;
+        __syncthreads();
+        const int key = sKey[k];
+        int part = 0;
+        switch (v) {
+            case 0: part = count_before(sKey, key, false, std::integral_constant<int, 0>{}, std::integral_constant<int, 4>{}); break;
+            case 1: part = count_before(sKey, key, false, std::integral_constant<int, 4>{}, std::integral_constant<int, 4>{}); break;
+            case 2: part = count_before(sKey, key, false, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}); break;
+            default: part = count_before(sKey, key, false, std::integral_constant<int, 12>{}, std::integral_constant<int, 4>{}); break;
+        }
+        sPart[v][k] = part;
+        __syncthreads();
+        return v == 0 ? sPart[0][k] + sPart[1][k] + sPart[2][k] + sPart[3][k] : 0;
+    };
+
+    // row ranks of all slices (heaviest first): slice t by wave t % 4, the wave's
+    // degrees loaded up front (clamped, unconditional loads in flight together)
+    constexpr int kSl = (kScatterRows + kBalWaves - 1) / kBalWaves;
+    int dgs[kSl];
+    static_for<kSl>([&](auto ii) {
+        constexpr int i = decltype(ii)::value;
+        dgs[i] = (int)degm[s0 + min((v + i * kBalWaves) * Qg + k, n - 1)];
+    });
+    static_for<kSl>([&](auto ii) {
+        constexpr int i = decltype(ii)::value;
+        const int t = v + i * kBalWaves;
+        if (t >= T) return;
+        const int nt = min(Qg, n - t * Qg);
+        const int dk = k < nt ? dgs[i] : 0;
+        const int key = k < nt ? dk * 64 + (63 - k) : -1;
+        sRk[t][k] = key;
+        wave_sync();
+        if (k < nt) {
+            const int rr = count_before(sRk[t], key, true, std::integral_constant<int, 0>{},
+                                        std::integral_constant<int, 16>{});
+            sRowAt[t][rr] = t * Qg + k;
+            sDegAt[t][rr] = dk;
+        }
+        wave_sync();
+    });
+    __syncthreads();
+
+    int a[kScatterRows], pos[kScatterRows];
+    int load = 0;
+    static_for<kScatterRows>([&](auto tt) {
+        constexpr int t = decltype(tt)::value;
+        a[t] = 0;
+        pos[t] = -1;
+    });
+    // slice by slice: the r-th heaviest row to the r-th lightest workgroup so far
+    static_for<kScatterRows>([&](auto tt) {
+        constexpr int t = decltype(tt)::value;
+        if (t < T) {
+            const int nt = min(Qg, n - t * Qg);
+            const int rw = load_rank(load);
+            if (v == 0 && k < Qg && rw < nt) {
+                pos[t] = sRowAt[t][rw];
+                a[t] = sDegAt[t][rw];
+                load += a[t];
+            }
+        }
+    });
+    for (int rd = 0; rd < kSchedSwapRounds; ++rd) {
+        const int rw = load_rank(load);
+        if (v == 0) {
+            if (k < Qg) {
+                static_for<kScatterRows>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    sA[rw][t] = a[t];
+                    sP[rw][t] = pos[t];
+                });
+                sL[rw] = load;
+            }
+            wave_sync();
+            // pairs: the i-th lightest with the i-th heaviest (i < Qg / 2); both lanes of
+            // a pair compute the same choice from the same values
+            const int pr = Qg - 1 - rw;
+            const bool paired = k < Qg && min(rw, pr) < Qg / 2 && rw != pr;
+            if (paired) {
+                const bool heavy = rw > pr;
+                int pa[kScatterRows];
+                static_for<kScatterRows>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    pa[t] = sA[pr][t];
+                });
+                const int pl = sL[pr];
+                const int diff = heavy ? load - pl : pl - load;
+                int best = -1, bv = diff;
+                static_for<kScatterRows>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    if (t < T) {
+                        const int d = heavy ? a[t] - pa[t] : pa[t] - a[t];
+                        if (d > 0 && d < diff) {
+                            const int dv = diff > 2 * d ? diff - 2 * d : 2 * d - diff;
+                            if (dv < bv) {
+                                bv = dv;
+                                best = t;
+                            }
+                        }
+                    }
+                });
+                if (best >= 0) {
+                    int d = 0;
+                    static_for<kScatterRows>([&](auto tt) {
+                        constexpr int t = decltype(tt)::value;
+                        if (t == best) {
+                            d = heavy ? a[t] - pa[t] : pa[t] - a[t];
+                            a[t] = pa[t];
+                            pos[t] = sP[pr][t];
+                        }
+                    });
+                    load += heavy ? -d : d;
+                }
+            }
+            wave_sync();
+        }
+    }
+    if (v == 0 && k < Qg) {
+        const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
+        int64_t od[kScatterRows];  // destinations of the slots, loaded together
+        static_for<kScatterRows>([&](auto tt) {
+            constexpr int t = decltype(tt)::value;
+            od[t] = order[s0 + (pos[t] >= 0 ? pos[t] : 0)];
+        });
+        static_for<kScatterRows>([&](auto tt) {
+            constexpr int t = decltype(tt)::value;
+            if (t < R) {
+                const int p = t < T ? pos[t] : -1;
+                int64_t d = -1, sd = 0;
+                if (p >= 0 && od[t] >= 0 && od[t] < n_dst) {
+                    d = od[t];
+                    sd = a[t];
+                }
+                row_dst[b * R + t] = d;
+                slot_deg[b * R + t] = sd;
+            }
+        });
+    }
+}
+
+// edge_perm over the scheduled slots: one wave per slot, a lane per edge of its row.
+__global__ __launch_bounds__(256) void sched_edges_kernel(const int64_t* __restrict__ row_ptr,
+                                                          const int64_t* __restrict__ col_perm,
+                                                          const int64_t* __restrict__ row_dst,
+                                                          const int64_t* __restrict__ row_ptr_s,
+                                                          int64_t* __restrict__ edge_perm,
+                                                          int64_t n_sched) {
+    const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (q >= n_sched) return;  // uniform per wave
     const int64_t d = row_dst[q];
     if (d < 0) return;
     const int64_t s0 = row_ptr[d], n = row_ptr[d + 1] - s0, o = row_ptr_s[q];
-    for (int64_t i = 0; i < n; ++i) edge_perm[o + i] = col_perm ? col_perm[s0 + i] : s0 + i;
+    for (int64_t i = lane; i < n; i += 64) edge_perm[o + i] = col_perm ? col_perm[s0 + i] : s0 + i;
 }
 
 }  // namespace bmhip
@@ -1166,12 +1369,16 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
     sched_group_targets_kernel<<<(unsigned)ceil_div(8 * (int64_t)G, 64), 64, 0, stream>>>(cum, N_dst,
                                                                                          P, Q, gb);
     sched_groups_kernel<<<1, 64, 0, stream>>>(N_dst, P, Q, rows_per_block, gb);
-    sched_balance_kernel<<<(unsigned)(8 * G), kSchedMaxQ, 0, stream>>>(
-        degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
+    if (Q <= 64 && N_edges < ((int64_t)1 << 25))
+        sched_balance_wave_kernel<<<(unsigned)(8 * G), 64 * kBalWaves, 0, stream>>>(
+            degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
+    else
+        sched_balance_kernel<<<(unsigned)(8 * G), kSchedMaxQ, 0, stream>>>(
+            degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
     rc = batteries_exclusive_scan_i64(slot_deg, row_ptr_s, n_sched, stream);
     if (rc != BM_OK) return rc;
-    sched_edges_kernel<<<(unsigned)ceil_div(n_sched, B), B, 0, stream>>>(row_ptr, col_perm, row_dst,
-                                                                        row_ptr_s, edge_perm, n_sched);
+    sched_edges_kernel<<<(unsigned)ceil_div(n_sched, 4), 256, 0, stream>>>(row_ptr, col_perm, row_dst,
+                                                                          row_ptr_s, edge_perm, n_sched);
     return (int)hipGetLastError();
 }
 

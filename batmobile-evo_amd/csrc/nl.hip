@@ -162,55 +162,62 @@ __global__ __launch_bounds__(64) void nl_sort_bins_wave_kernel(const int64_t* __
 }
 
 // ---------------------------------------------------------------------------
-// Stencil passes (count, then write): one wave per home cell.  The atoms of the
-// 27 cells around it (reference order: dz, dy, dx from -1 to 1, atoms of a cell
-// in ascending index) are staged in LDS as (x, y, z, j); then for each home
-// atom i the lanes test 64 candidates at a time and a ballot gives every kept
-// pair its slot, so row i lists its neighbors in stencil order.  Candidate
-// lists longer than the LDS buffer are processed in chunks.
+// Stencil passes (count, then write): one workgroup of kNlWaves waves per home
+// cell.  The atoms of the 27 cells around it (reference order: dz, dy, dx from
+// -1 to 1, atoms of a cell in ascending index) are staged in LDS as (x, y, z, j)
+// by all its threads; then each wave takes every kNlWaves-th home atom i (read
+// from the staged home cell), its lanes test 64 candidates at a time, and a
+// ballot gives every kept pair its slot, so row i lists its neighbors in stencil
+// order.  Candidate lists longer than the LDS buffer are processed in chunks.
+// esrc may be null (the row is the source).
 // ---------------------------------------------------------------------------
 constexpr int kNlCap = 2048;  // candidates staged per chunk (32 KB)
+constexpr int kNlWaves = 4;   // waves per cell
 
 template <bool WRITE>
-__global__ __launch_bounds__(64) void nl_cell_kernel(const float* __restrict__ pos, BinCfg c,
-                                                     float rc2, int self_loops,
-                                                     const int64_t* __restrict__ bin_start,
-                                                     const int* __restrict__ order,
-                                                     int64_t* __restrict__ counts,
-                                                     const int64_t* __restrict__ offsets,
-                                                     int* __restrict__ esrc, int* __restrict__ edst,
-                                                     float* __restrict__ evec) {
+__global__ __launch_bounds__(64 * kNlWaves) void nl_cell_kernel(const float* __restrict__ pos, BinCfg c,
+                                                                float rc2, int self_loops,
+                                                                const int64_t* __restrict__ bin_start,
+                                                                const int* __restrict__ order,
+                                                                int64_t* __restrict__ counts,
+                                                                const int64_t* __restrict__ offsets,
+                                                                int* __restrict__ esrc,
+                                                                int* __restrict__ edst,
+                                                                float* __restrict__ evec) {
     __shared__ float4 sCand[kNlCap];
     __shared__ int sStart[27], sPre[28];
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int k = blockIdx.x;
     const int bx = k % c.nb[0], by = (k / c.nb[0]) % c.nb[1], bz = k / (c.nb[0] * c.nb[1]);
-    int cnt_l = 0;
-    if (lane < 27) {
-        const int dz = lane / 9 - 1, dy = (lane / 3) % 3 - 1, dx = lane % 3 - 1;
-        const int kk = wrap_bin(bx + dx, c.nb[0]) + wrap_bin(by + dy, c.nb[1]) * c.nb[0] +
-                       wrap_bin(bz + dz, c.nb[2]) * c.nb[0] * c.nb[1];
-        const int64_t s0 = bin_start[kk];
-        sStart[lane] = (int)s0;
-        cnt_l = (int)(bin_start[kk + 1] - s0);
-    }
-    // exclusive prefix of the 27 counts (wave-level, lanes 0..26)
-    int incl = cnt_l;
+    if (wv == 0) {
+        int cnt_l = 0;
+        if (lane < 27) {
+            const int dz = lane / 9 - 1, dy = (lane / 3) % 3 - 1, dx = lane % 3 - 1;
+            const int kk = wrap_bin(bx + dx, c.nb[0]) + wrap_bin(by + dy, c.nb[1]) * c.nb[0] +
+                           wrap_bin(bz + dz, c.nb[2]) * c.nb[0] * c.nb[1];
+            const int64_t s0 = bin_start[kk];
+            sStart[lane] = (int)s0;
+            cnt_l = (int)(bin_start[kk + 1] - s0);
+        }
+        // exclusive prefix of the 27 counts (wave-level, lanes 0..26)
+        int incl = cnt_l;
 #pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-        const int v = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += v;
+        for (int off = 1; off < 32; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        if (lane < 27) sPre[lane] = incl - cnt_l;
+        if (lane == 26) sPre[27] = incl;
     }
-    if (lane < 27) sPre[lane] = incl - cnt_l;
-    if (lane == 26) sPre[27] = incl;
     __syncthreads();
     const int T = sPre[27];
     const int home0 = sStart[13], H = sPre[14] - sPre[13];
-    if (H == 0) return;  // uniform: no home atoms
+    if (H == 0) return;  // uniform: no home atoms (the home cell is entry 13 of the stencil)
 
-    // stage candidates [base, base + n) of the concatenated 27-cell list
+    // stage candidates [base, base + n) of the concatenated 27-cell list, all waves
     auto stage = [&](int base, int n) {
-        for (int t = lane; t < n; t += 64) {
+        for (int t = tid; t < n; t += 64 * kNlWaves) {
             const int idx = base + t;
             int cell = 0;
 #pragma unroll
@@ -220,49 +227,65 @@ __global__ __launch_bounds__(64) void nl_cell_kernel(const float* __restrict__ p
                                    pos[(int64_t)j * 3 + 2], __int_as_float(j));
         }
     };
-    const bool one_chunk = T <= kNlCap;
-    if (one_chunk) {
+    // home atom hh against candidates [0, n) of the staged chunk; w counts its neighbors
+    auto scan_cands = [&](int i, const float (&pi)[3], int n, int64_t& w) {
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            const int t = c0 + lane;
+            bool keep = false;
+            float d[3] = {0.f, 0.f, 0.f};
+            int j = 0;
+            if (t < n) {
+                const float4 cj = sCand[t];
+                j = __float_as_int(cj.w);
+                const float pj[3] = {cj.x, cj.y, cj.z};
+                keep = (self_loops || j != i) && min_image(pi, pj, c, d) <= rc2;
+            }
+            const uint64_t m = __ballot(keep);
+            if constexpr (WRITE) {
+                if (keep) {
+                    const int64_t at = w + __popcll(m & ((1ull << lane) - 1ull));
+                    if (esrc) esrc[at] = i;
+                    edst[at] = j;
+                    evec[at * 3 + 0] = d[0];
+                    evec[at * 3 + 1] = d[1];
+                    evec[at * 3 + 2] = d[2];
+                }
+            }
+            w += __popcll(m);
+        }
+    };
+    if (T <= kNlCap) {
+        // one chunk: the waves share the staged candidates and take every kNlWaves-th
+        // home atom, whose position is a staged candidate as well
         stage(0, T);
         __syncthreads();
+        for (int hh = wv; hh < H; hh += kNlWaves) {
+            const float4 ci = sCand[sPre[13] + hh];
+            const int i = __builtin_amdgcn_readfirstlane(__float_as_int(ci.w));
+            const float pi[3] = {ci.x, ci.y, ci.z};
+            int64_t w = WRITE ? offsets[i] : 0;
+            scan_cands(i, pi, T, w);
+            if constexpr (!WRITE) {
+                if (lane == 0) counts[i] = w;
+            }
+        }
+        return;
     }
+    // dense systems (more than kNlCap candidates): chunks staged by all waves, every
+    // home atom walked by wave 0 (the other waves take part in staging and barriers)
     for (int hh = 0; hh < H; ++hh) {
         const int i = __builtin_amdgcn_readfirstlane(order[home0 + hh]);
         const float pi[3] = {pos[(int64_t)i * 3], pos[(int64_t)i * 3 + 1], pos[(int64_t)i * 3 + 2]};
-        int64_t w = WRITE ? offsets[i] : 0;
+        int64_t w = (WRITE && wv == 0) ? offsets[i] : 0;
         for (int base = 0; base < T; base += kNlCap) {
             const int n = min(kNlCap, T - base);
-            if (!one_chunk) {
-                __syncthreads();
-                stage(base, n);
-                __syncthreads();
-            }
-            for (int c0 = 0; c0 < n; c0 += 64) {
-                const int t = c0 + lane;
-                bool keep = false;
-                float d[3] = {0.f, 0.f, 0.f};
-                int j = 0;
-                if (t < n) {
-                    const float4 cj = sCand[t];
-                    j = __float_as_int(cj.w);
-                    const float pj[3] = {cj.x, cj.y, cj.z};
-                    keep = (self_loops || j != i) && min_image(pi, pj, c, d) <= rc2;
-                }
-                const uint64_t m = __ballot(keep);
-                if constexpr (WRITE) {
-                    if (keep) {
-                        const int64_t at = w + __popcll(m & ((1ull << lane) - 1ull));
-                        esrc[at] = i;
-                        edst[at] = j;
-                        evec[at * 3 + 0] = d[0];
-                        evec[at * 3 + 1] = d[1];
-                        evec[at * 3 + 2] = d[2];
-                    }
-                }
-                w += __popcll(m);
-            }
+            __syncthreads();
+            stage(base, n);
+            __syncthreads();
+            if (wv == 0) scan_cands(i, pi, n, w);
         }
         if constexpr (!WRITE) {
-            if (lane == 0) counts[i] = w;
+            if (wv == 0 && lane == 0) counts[i] = w;
         }
     }
 }
@@ -270,16 +293,37 @@ __global__ __launch_bounds__(64) void nl_cell_kernel(const float* __restrict__ p
 // Sort each atom's neighbors by j: one wave per row.  Rows of at most 64
 // entries: lane l holds entry l and writes it at its rank (number of smaller j,
 // ties by position); longer rows (dense systems): insertion sort by one lane.
+// GRAPH: the sorted row goes to the message-passing layout instead (int64
+// gsrc = j, gdst = i, gvec = the vector negated: edges grouped by destination
+// i, each with vector r_i - r_j), and edst / evec are left as they are.
+template <bool GRAPH>
 __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __restrict__ offsets,
                                                            int* __restrict__ edst,
-                                                           float* __restrict__ evec, int64_t n) {
+                                                           float* __restrict__ evec, int64_t n,
+                                                           int64_t* __restrict__ gsrc,
+                                                           int64_t* __restrict__ gdst,
+                                                           float* __restrict__ gvec) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;  // uniform per wave
     const int64_t s = offsets[row], e = offsets[row + 1];
     const int len = (int)(e - s);
-    if (len <= 1) return;
+    auto put = [&](int64_t at, int j, float v0, float v1, float v2) {
+        if constexpr (GRAPH) {
+            gsrc[at] = j;
+            gdst[at] = row;
+            gvec[at * 3] = -v0;
+            gvec[at * 3 + 1] = -v1;
+            gvec[at * 3 + 2] = -v2;
+        } else {
+            edst[at] = j;
+            evec[at * 3] = v0;
+            evec[at * 3 + 1] = v1;
+            evec[at * 3 + 2] = v2;
+        }
+    };
     if (len <= 64) {
+        if (!GRAPH && len <= 1) return;
         int j = 0;
         float v0 = 0.f, v1 = 0.f, v2 = 0.f;
         if (lane < len) {
@@ -293,12 +337,7 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
             const int jm = __builtin_amdgcn_readlane(j, m);
             rank += (jm < j || (jm == j && m < lane)) ? 1 : 0;
         }
-        if (lane < len) {
-            edst[s + rank] = j;
-            evec[(s + rank) * 3] = v0;
-            evec[(s + rank) * 3 + 1] = v1;
-            evec[(s + rank) * 3 + 2] = v2;
-        }
+        if (lane < len) put(s + rank, j, v0, v1, v2);
         return;
     }
     if (lane != 0) return;
@@ -318,6 +357,8 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
         evec[(q + 1) * 3 + 1] = v1;
         evec[(q + 1) * 3 + 2] = v2;
     }
+    if constexpr (GRAPH)
+        for (int64_t a = s; a < e; ++a) put(a, edst[a], evec[a * 3], evec[a * 3 + 1], evec[a * 3 + 2]);
 }
 
 // ---------------------------------------------------------------------------
@@ -469,7 +510,7 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
                                                                     order, N);
         nl_sort_bins_wave_kernel<<<(unsigned)c.total, 64, 0, stream>>>(bin_start, order,
                                                                          c.total);
-        nl_cell_kernel<false><<<(unsigned)c.total, 64, 0, stream>>>(
+        nl_cell_kernel<false><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
             nullptr, nullptr);
     }
@@ -498,11 +539,90 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
     const int64_t* offsets = reinterpret_cast<const int64_t*>(ws + L.offsets);
     const int B = 256;
     if (N > 0) {
-        nl_cell_kernel<true><<<(unsigned)c.total, 64, 0, stream>>>(
+        nl_cell_kernel<true><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, edge_src,
             edge_dst, edge_vectors);
-        nl_sort_rows_kernel<<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(offsets, edge_dst,
-                                                                         edge_vectors, N);
+        nl_sort_rows_kernel<false><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
+            offsets, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr);
+    }
+    if (row_offsets) {
+        hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
+                                      hipMemcpyDeviceToDevice, stream);
+        if (e != hipSuccess) return (int)e;
+    }
+    return (int)hipGetLastError();
+}
+
+// Spatial order from the neighbor list's cells: the cells in serpentine
+// (boustrophedon) order, x fastest with the direction reversed on every other row,
+// rows reversed on every other plane, so that consecutive cells are always
+// adjacent; the atoms of a cell in ascending index (the binning's own order).
+// One workgroup: each thread takes a run of consecutive path positions, their
+// atom counts are scanned across the workgroup, then each thread writes its runs.
+constexpr int kSerpBlock = 1024;
+
+__device__ __forceinline__ int serpentine_cell(int p, const BinCfg& c) {
+    const int nx = c.nb[0], ny = c.nb[1];
+    const int row = p / nx, px = p - row * nx;
+    const int bz = row / ny, py = row - bz * ny;
+    const int by = (bz & 1) ? ny - 1 - py : py;
+    const int bx = (row & 1) ? nx - 1 - px : px;
+    return bx + by * nx + bz * nx * ny;
+}
+
+__global__ __launch_bounds__(kSerpBlock) void nl_serpentine_order_kernel(
+    const int64_t* __restrict__ bin_start, const int* __restrict__ order, BinCfg c,
+    int64_t* __restrict__ out) {
+    __shared__ int64_t sWave[kSerpBlock / 64];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int per = (c.total + kSerpBlock - 1) / kSerpBlock;
+    const int p0 = min(t * per, c.total), p1 = min(p0 + per, c.total);
+    int64_t sum = 0;
+    for (int p = p0; p < p1; ++p) {
+        const int k = serpentine_cell(p, c);
+        sum += bin_start[k + 1] - bin_start[k];
+    }
+    // exclusive scan of the thread sums: within each wave by shuffles, then the waves
+    int64_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+    }
+    if (lane == 63) sWave[w] = incl;
+    __syncthreads();
+    int64_t base = 0;
+    for (int i = 0; i < w; ++i) base += sWave[i];
+    int64_t o = base + incl - sum;
+    for (int p = p0; p < p1; ++p) {
+        const int k = serpentine_cell(p, c);
+        for (int64_t a = bin_start[k]; a < bin_start[k + 1]; ++a) out[o++] = order[a];
+    }
+}
+
+extern "C" int batteries_neighbor_graph_write(const float* positions, const float* box, int64_t N,
+                                              float cutoff, int self_loops, void* workspace,
+                                              size_t workspace_bytes, int* tmp_j, float* tmp_vec,
+                                              int64_t* src, int64_t* dst, float* edge_vectors,
+                                              int64_t* row_offsets, int64_t* spatial_order,
+                                              hipStream_t stream) {
+    if (N < 0 || !box || !valid_box(box, cutoff)) return BM_ERR_ARG;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    const NlLayout L = nl_layout(N, c.total);
+    if (!workspace || workspace_bytes < L.total_bytes) return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    const int64_t* bin_start = reinterpret_cast<const int64_t*>(ws + L.bin_start);
+    const int* order = reinterpret_cast<const int*>(ws + L.order);
+    const int64_t* offsets = reinterpret_cast<const int64_t*>(ws + L.offsets);
+    if (N > 0) {
+        nl_cell_kernel<true><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
+            positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, nullptr,
+            tmp_j, tmp_vec);
+        nl_sort_rows_kernel<true><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
+            offsets, tmp_j, tmp_vec, N, src, dst, edge_vectors);
+        if (spatial_order)
+            nl_serpentine_order_kernel<<<1, kSerpBlock, 0, stream>>>(bin_start, order, c,
+                                                                     spatial_order);
     }
     if (row_offsets) {
         hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
@@ -514,11 +634,19 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
 
 // ---------------------------------------------------------------------------
 // Spatial (Morton) order of atoms: positions wrapped into the box, quantised to
-// a 32^3 grid, keyed by the 15-bit Morton code of the cell; counting sort by key
-// with ascending atom index inside a cell (deterministic).
+// a grid of 2^b cells per axis, keyed by the 3b-bit Morton code of the cell;
+// counting sort by key with ascending atom index inside a cell (deterministic).
+// b is the largest value up to 5 with 8^b <= N (1 to 8 atoms per grid cell on
+// average), so the scan over the cells stays about as long as the atom list.
 // ---------------------------------------------------------------------------
-constexpr int kMortonBits = 5;
+constexpr int kMortonBits = 5;  // at most
 constexpr int kMortonCells = 1 << (3 * kMortonBits);
+
+static int morton_bits(int64_t N) {
+    int b = 1;
+    while (b < kMortonBits && ((int64_t)1 << (3 * (b + 1))) <= N) ++b;
+    return b;
+}
 
 __device__ __forceinline__ int spread3(int v) {
     int r = 0;
@@ -528,7 +656,8 @@ __device__ __forceinline__ int spread3(int v) {
 }
 
 __global__ void morton_key_kernel(const float* __restrict__ pos, float bx, float by, float bz,
-                                  int* __restrict__ key, int* __restrict__ count, int64_t n) {
+                                  int bits, int* __restrict__ key, int* __restrict__ count,
+                                  int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float box[3] = {bx, by, bz};
@@ -537,8 +666,8 @@ __global__ void morton_key_kernel(const float* __restrict__ pos, float bx, float
     for (int d = 0; d < 3; ++d) {
         const float p = pos[i * 3 + d];
         const float w = p - floorf(p / box[d]) * box[d];
-        int v = (int)(w / box[d] * (float)(1 << kMortonBits));
-        v = v < 0 ? 0 : (v > (1 << kMortonBits) - 1 ? (1 << kMortonBits) - 1 : v);
+        int v = (int)(w / box[d] * (float)(1 << bits));
+        v = v < 0 ? 0 : (v > (1 << bits) - 1 ? (1 << bits) - 1 : v);
         q[d] = v;
     }
     const int k = spread3(q[0]) | (spread3(q[1]) << 1) | (spread3(q[2]) << 2);
@@ -580,14 +709,16 @@ extern "C" int batteries_spatial_order(const float* positions, const float* box,
     int64_t* start = reinterpret_cast<int64_t*>(ws + 2 * align256(sizeof(int) * (size_t)N) +
                                                 align256(sizeof(int) * kMortonCells));
     const int B = 256;
-    nl_zero_i32_kernel<<<kMortonCells / B, B, 0, stream>>>(count, kMortonCells);
+    const int bits = morton_bits(N);
+    const int cells = 1 << (3 * bits);
+    nl_zero_i32_kernel<<<(unsigned)ceil_div(cells, B), B, 0, stream>>>(count, cells);
     morton_key_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(positions, box[0], box[1], box[2],
-                                                                  key, count, N);
-    int rc = scan_i32(count, start, kMortonCells, stream);
+                                                                  bits, key, count, N);
+    int rc = scan_i32(count, start, cells, stream);
     if (rc != BM_OK) return rc;
-    nl_zero_i32_kernel<<<kMortonCells / B, B, 0, stream>>>(count, kMortonCells);
+    nl_zero_i32_kernel<<<(unsigned)ceil_div(cells, B), B, 0, stream>>>(count, cells);
     morton_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(key, start, count, tmp, N);
-    nl_sort_bins_kernel<<<kMortonCells / B, B, 0, stream>>>(start, tmp, kMortonCells);
+    nl_sort_bins_kernel<<<(unsigned)ceil_div(cells, B), B, 0, stream>>>(start, tmp, cells);
     morton_finish_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(tmp, order, N);
     return (int)hipGetLastError();
 }

@@ -7,7 +7,9 @@ scatter) into GPU-resident tensors that the fused kernel consumes directly:
   src, dst, vec   edges grouped by destination (dst ascending, src ascending within),
                   vec = minimum-image r_dst - r_src
   row_ptr         CSR row pointer over destinations [N + 1]
-  schedule        spatial processing order of the destinations (mp_schedule)
+  order           spatial order of the atoms (the cell list's cells along a serpentine
+                  path, atoms of a cell ascending)
+  schedule        processing schedule of the destinations in that order (mp_schedule)
 
 The neighbor relation of a cell list is symmetric, so the neighbor list sorted
 by (i, j) read with roles swapped is exactly the edge list sorted by destination,
@@ -20,23 +22,36 @@ import _batmobile
 
 class Graph:
     def __init__(self, positions, cell, cutoff, channels, self_loops=False):
-        ei, vec, off = _batmobile.neighbor_list(positions, cell, float(cutoff), bool(self_loops))
+        # the neighbor list written directly in this layout (one pass, no torch glue),
+        # with a spatial order of the atoms from its cells
+        src, dst, vec, off, order = _batmobile.neighbor_graph(positions, cell, float(cutoff),
+                                                              bool(self_loops))
         self.cell = cell
         self.cutoff = float(cutoff)
+        self.positions = positions
         self._rev = None
+        self._fine_order = None
         self.n_atoms = positions.shape[0]
-        self.src = ei[1].contiguous()
-        self.dst = ei[0].contiguous()
-        self.vec = (-vec).contiguous()
+        self.src = src
+        self.dst = dst
+        self.vec = vec
         self.row_ptr = off
         self.channels = int(channels)
-        self.order = _batmobile.spatial_order(positions, cell)
+        self.order = order
         (self.row_ptr_s, self.edge_perm, self.row_dst, self.n_blocks,
          self.rows_per_block) = _batmobile.mp_schedule(self.row_ptr, self.order, self.channels)
 
     @property
     def num_edges(self):
         return int(self.src.numel())
+
+    def fine_order(self):
+        """Morton order of the atoms on a grid of 1 to 8 atoms per cell (spatial_order; built
+        on first use).  The MACE layer walks its destination rows in this order, 1.5% faster
+        at configs[4] than in the cell list's order."""
+        if self._fine_order is None:
+            self._fine_order = _batmobile.spatial_order(self.positions, self.cell)
+        return self._fine_order
 
     def reverse_edges(self):
         """rev[e]: index of the edge with source and destination swapped (built once)."""

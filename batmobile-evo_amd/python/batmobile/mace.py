@@ -61,10 +61,10 @@ class MaceLayerFunction(torch.autograd.Function):
             if _keep_edge_weights(save_edge_weights, edge_weight_bytes(e, c), x.device):
                 ew = torch.empty(_batmobile.mace_edge_weight_rows(e, c), NUM_PATHS * c,
                                  dtype=torch.float32, device=x.device)
-        # destination rows in the graph's spatial order: neighbouring destinations share
+        # destination rows in the graph's Morton order: neighbouring destinations share
         # source rows, which then stay in cache
         out = _batmobile.mace_forward(pos, graph.cell, x, w1, b1, w2, graph.src, graph.dst,
-                                      graph.row_ptr, float(cutoff), ew, graph.order)
+                                      graph.row_ptr, float(cutoff), ew, graph.fine_order())
         ctx.save_for_backward(pos, x, w1, b1, w2)
         ctx.edge_weights = ew
         ctx.graph = graph
@@ -83,7 +83,7 @@ class MaceLayerFunction(torch.autograd.Function):
             grad_pos = _batmobile.mace_backward(pos, g.cell, x, w1, b1, w2, g.src, g.dst,
                                                 g.row_ptr, g.reverse_edges(),
                                                 grad_out.contiguous(), ctx.cutoff,
-                                                ctx.edge_weights, g.order)
+                                                ctx.edge_weights, g.fine_order())
         ctx.edge_weights = None
         return grad_pos, None, None, None, None, None, None, None
 

@@ -164,7 +164,8 @@ int batteries_sh_tp_scatter_csr(const float* edge_vectors, const float* node_fea
 /* Spatial processing schedule for the fused scatter (no reference counterpart:
  * the reference processes destinations in index order).  Built once per graph:
  *   batteries_spatial_order      order[N] = atoms sorted by the Morton code of
- *                                their cell in a 32^3 grid over the box (host box[3])
+ *                                their cell in a 2^b-per-axis grid over the box (host
+ *                                box[3]; b <= 5 the largest with 8^b <= N)
  *   batteries_mp_schedule_shape  n_blocks (multiple of 8) x rows_per_block for C
  *   batteries_mp_schedule        row_ptr_s[n_blocks*rows_per_block + 1],
  *                                row_dst[n_blocks*rows_per_block] (-1 = empty slot),
@@ -273,6 +274,25 @@ int batteries_neighbor_list_write(const float* positions, const float* box, int6
                                   float cutoff, int self_loops, void* workspace,
                                   size_t workspace_bytes, int* edge_src, int* edge_dst,
                                   float* edge_vectors, int64_t* row_offsets, hipStream_t stream);
+
+/* Phase 2 in the layout of the message-passing kernels (same workspace, after
+ * phase 1): the neighbor list read with roles swapped, src[E] = j, dst[E] = i
+ * (int64, sorted by (i, j): grouped by destination), edge_vectors[E,3] =
+ * minimum-image pos[i] - pos[j] (the phase-2 vector negated exactly);
+ * row_offsets[N+1] (may be NULL) = start of each destination; spatial_order[N]
+ * (may be NULL) = the atoms by cell of the cell list, cells along a serpentine
+ * path (consecutive cells adjacent), atoms of a cell in ascending index (a
+ * processing order for batteries_mp_schedule).  tmp_j [E] and tmp_vec [E,3] are
+ * scratch.  No counterpart in the reference, whose message
+ * passing callers convert edge_index and negate the vectors with torch
+ * (benchmarks/benchmark_e2e_mace.py:192-278); the neighbor set and vectors are
+ * those of batteries::neighbor_list_cuda. */
+int batteries_neighbor_graph_write(const float* positions, const float* box, int64_t N,
+                                   float cutoff, int self_loops, void* workspace,
+                                   size_t workspace_bytes, int* tmp_j, float* tmp_vec,
+                                   int64_t* src, int64_t* dst, float* edge_vectors,
+                                   int64_t* row_offsets, int64_t* spatial_order,
+                                   hipStream_t stream);
 
 /* Result of neighbor_list_cuda; same layout as include/neighbor_list.cuh:25-33. */
 typedef struct NeighborListResult {

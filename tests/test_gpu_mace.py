@@ -119,12 +119,13 @@ def test_mace_row_order_does_not_change_results(bm, dev):
     p, xd, god = pos.to(dev), x.to(dev), go.to(dev)
     args = (p, cell, xd, layer.W1, layer.b1, layer.W2, graph.src, graph.dst, graph.row_ptr)
     out_idx = bm.mace_forward(*args, 5.0)
-    out_sp = bm.mace_forward(*args, 5.0, None, graph.order)
-    assert torch.equal(out_idx, out_sp)
     rev = graph.reverse_edges()
     g_idx = bm.mace_backward(*args, rev, god, 5.0)
-    g_sp = bm.mace_backward(*args, rev, god, 5.0, None, graph.order)
-    assert torch.equal(g_idx, g_sp)
+    for order in (graph.fine_order(), graph.order):   # as MACEInteraction runs them, and the cell order
+        out_sp = bm.mace_forward(*args, 5.0, None, order)
+        assert torch.equal(out_idx, out_sp)
+        g_sp = bm.mace_backward(*args, rev, god, 5.0, None, order)
+        assert torch.equal(g_idx, g_sp)
     # a reversed order as well (any permutation)
     assert torch.equal(bm.mace_forward(*args, 5.0, None, graph.order.flip(0).contiguous()), out_idx)
     with pytest.raises(RuntimeError, match="order"):

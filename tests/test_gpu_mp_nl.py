@@ -278,16 +278,20 @@ def test_config4_scatter_full_size(bm, dev):
     assert torch.equal(out, bm.sh_tp_scatter(v, x, src, off, None, True))
 
 
-def test_spatial_order_is_a_morton_permutation(bm, dev):
-    pos, cell = periodic_box(5000, 3)
+@pytest.mark.parametrize("n", [5000, 50000, 40])
+def test_spatial_order_is_a_morton_permutation(bm, dev, n):
+    pos, cell = periodic_box(n, 3)
     order = bm.spatial_order(pos.to(dev), cell).cpu().numpy()
-    assert np.array_equal(np.sort(order), np.arange(5000))
+    assert np.array_equal(np.sort(order), np.arange(n))
     L = float(cell[0, 0])
-    q = np.clip((pos.numpy() / L * 32).astype(int), 0, 31)
+    bits = 1                              # 2^bits cells per axis: the largest bits <= 5
+    while bits < 5 and 8 ** (bits + 1) <= n:   # with 8^bits <= N
+        bits += 1
+    q = np.clip((pos.numpy() / L * (1 << bits)).astype(int), 0, (1 << bits) - 1)
 
     def spread(v):
         r = np.zeros_like(v)
-        for b in range(5):
+        for b in range(bits):
             r |= ((v >> b) & 1) << (3 * b)
         return r
 
@@ -416,3 +420,37 @@ def test_scatter_batch_boundaries(bm, dev):
     assert normwise_err(out.cpu(), want) <= 1e-5
     assert out[deg == 0].abs().max().item() == 0.0
     assert torch.equal(out, bm.sh_tp_scatter(vec.to(dev), x.to(dev), src.to(dev), rp.to(dev), None, True))
+
+
+def _bin_coords_f32(pos, L, rc):
+    """The cell list's bin coordinates in float32, with the cell-list kernels' operations
+    (no contraction): t = p / L, wrapped p - floor(t) L, divided by the bin width."""
+    L32, rc32 = np.float32(L), np.float32(rc)
+    nb = max(3, int(L32 / rc32))
+    inv = np.float32(1.0) / L32
+    binw = L32 / np.float32(nb)
+    p = pos.astype(np.float32)
+    fl = (np.floor(p * inv).astype(np.float32) * L32).astype(np.float32)
+    w = (p - fl).astype(np.float32)
+    v = (w / binw).astype(np.int64)
+    return np.clip(v, 0, nb - 1), nb
+
+
+@pytest.mark.parametrize("n", [5000, 700, 20000])
+def test_graph_order_is_a_serpentine_cell_order(bm, dev, n):
+    """Graph.order: a permutation of the atoms, the cell list's cells along a serpentine
+    path (x fastest, every other row and every other plane reversed) and the atoms of a
+    cell in ascending index."""
+    import batmobile
+    pos, cell = periodic_box(n, 5)
+    g = batmobile.Graph(pos.to(dev), cell, 5.0, 16)
+    order = g.order.cpu().numpy()
+    assert np.array_equal(np.sort(order), np.arange(n))
+    b, nb = _bin_coords_f32(pos.numpy(), float(cell[0, 0]), 5.0)
+    bx, by, bz = b[:, 0], b[:, 1], b[:, 2]
+    py = np.where(bz % 2 == 1, nb - 1 - by, by)
+    row = bz * nb + py
+    px = np.where(row % 2 == 1, nb - 1 - bx, bx)
+    path = row * nb + px                      # serpentine position of each atom's cell
+    key = path[order] * n + order             # path position, then atom index
+    assert (np.diff(key) > 0).all()
