@@ -410,6 +410,9 @@ def main():
     ap.add_argument("--scatter-sweep", action="store_true",
                     help="time only the headline kernel at N = 5000, 20000, 50000 (C = 64) and "
                          "print the figures")
+    ap.add_argument("--graph-only", action="store_true",
+                    help="build the configs[3] graph --steps times, then run as many end-to-end "
+                         "steps, and print the times (for kernel traces of the build)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the workload, run 5 plain device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -446,6 +449,17 @@ def main():
     if a.weighted_only:
         print(json.dumps(weighted_config3(torch, bm, dev, w, wt, reps=max(a.steps, 1))[0]),
               flush=True)
+        return
+    if a.graph_only:
+        # the configs[3] graph built a.steps times (neighbor list, order, schedule), then as
+        # many end-to-end steps (graph + fused kernel), for kernel traces of the build
+        pos_d = w["pos"].to(dev)
+        reps = max(a.steps, 1)
+        build = time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS), reps)
+        e2e = time_call(torch, lambda: bm.Graph(pos_d, w["cell"], CUTOFF, CHANNELS).sh_tp_scatter(w["x"]),
+                        reps)
+        print(json.dumps({"graph_build_ms": round(build, 4), "e2e_step_ms": round(e2e, 4),
+                          "builds": 2 * (reps + 1)}), flush=True)
         return
 
     graph = w["graph"]
