@@ -124,12 +124,16 @@ __global__ void nl_sort_bins_kernel(const int64_t* __restrict__ bin_start, int* 
 }
 
 // The same with one wave per bin (bins of a few atoms each, as many bins as a few
-// workgroups per compute unit): the bin's atom indices are staged in LDS and each
-// goes to its rank (indices in a bin are distinct).  A bin of more than
-// kBinSortCap atoms is sorted by one lane as above.
+// workgroups per compute unit): each atom index goes to its rank, the number of
+// smaller indices in the bin (indices in a bin are distinct).  Bins of at most
+// kBinSortCap atoms are staged in LDS and written back in place.  Larger bins
+// (cells much larger than the density needs) are ranked against the bin read
+// again from memory, 64 indices at a time, into spare[] (the binning's per-atom
+// bin array, free once the atoms are placed), then copied back.
 constexpr int kBinSortCap = 1024;
 __global__ __launch_bounds__(64) void nl_sort_bins_wave_kernel(const int64_t* __restrict__ bin_start,
-                                                               int* __restrict__ order, int total) {
+                                                               int* __restrict__ order,
+                                                               int* __restrict__ spare, int total) {
     __shared__ int sv[kBinSortCap];
     const int k = blockIdx.x;
     if (k >= total) return;
@@ -138,17 +142,19 @@ __global__ __launch_bounds__(64) void nl_sort_bins_wave_kernel(const int64_t* __
     const int lane = threadIdx.x;
     if (n <= 1) return;
     if (n > kBinSortCap) {
-        if (lane == 0) {
-            for (int64_t i = s + 1; i < s + n; ++i) {
-                const int v = order[i];
-                int64_t j = i - 1;
-                while (j >= s && order[j] > v) {
-                    order[j + 1] = order[j];
-                    --j;
-                }
-                order[j + 1] = v;
+        for (int base = 0; base < n; base += 64) {
+            const int a = base + lane;
+            const int v = a < n ? order[s + a] : 0;
+            int r = 0;
+            for (int c0 = 0; c0 < n; c0 += 64) {
+                const int x = c0 + lane < n ? order[s + c0 + lane] : 0;
+                const int m_end = min(64, n - c0);
+                for (int m = 0; m < m_end; ++m) r += __builtin_amdgcn_readlane(x, m) < v ? 1 : 0;
             }
+            if (a < n) spare[s + r] = v;
         }
+        __syncthreads();  // the wave's stores to spare[] are complete and visible to it
+        for (int i = lane; i < n; i += 64) order[s + i] = spare[s + i];
         return;
     }
     for (int i = lane; i < n; i += 64) sv[i] = order[s + i];
@@ -290,14 +296,23 @@ __global__ __launch_bounds__(64 * kNlWaves) void nl_cell_kernel(const float* __r
     }
 }
 
-// Sort each atom's neighbors by j: one wave per row.  Rows of at most 64
-// entries: lane l holds entry l and writes it at its rank (number of smaller j,
-// ties by position); longer rows (dense systems): insertion sort by one lane.
+// Sort each atom's neighbors by j: one wave per row, each entry written at its
+// rank (the number of entries with a smaller j, ties by position in the row, so
+// equal j from different periodic images keep the stencil order).  Rows of at
+// most 64 * kRowRegs entries are held in registers (lane l owns entries l,
+// l + 64, ...), all read before any is written.  Longer rows (denser than any
+// system at an interatomic cutoff) are ranked against the row read again from
+// memory, 64 entries at a time: GRAPH writes each entry at its rank in the
+// output arrays; the in-place form keeps the ranks in esrc (the row's source
+// column, which holds the row index and is restored afterwards), and one lane
+// applies the permutation by following its cycles (one swap per entry).
 // GRAPH: the sorted row goes to the message-passing layout instead (int64
 // gsrc = j, gdst = i, gvec = the vector negated: edges grouped by destination
 // i, each with vector r_i - r_j), and edst / evec are left as they are.
+constexpr int kRowRegs = 8;
 template <bool GRAPH>
 __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __restrict__ offsets,
+                                                           int* __restrict__ esrc,
                                                            int* __restrict__ edst,
                                                            float* __restrict__ evec, int64_t n,
                                                            int64_t* __restrict__ gsrc,
@@ -340,25 +355,85 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
         if (lane < len) put(s + rank, j, v0, v1, v2);
         return;
     }
-    if (lane != 0) return;
-    for (int64_t a = s + 1; a < e; ++a) {
-        const int v = edst[a];
-        const float v0 = evec[a * 3], v1 = evec[a * 3 + 1], v2 = evec[a * 3 + 2];
-        int64_t q = a - 1;
-        while (q >= s && edst[q] > v) {
-            edst[q + 1] = edst[q];
-            evec[(q + 1) * 3] = evec[q * 3];
-            evec[(q + 1) * 3 + 1] = evec[q * 3 + 1];
-            evec[(q + 1) * 3 + 2] = evec[q * 3 + 2];
-            --q;
+    if (len <= 64 * kRowRegs) {
+        const int nk = (len + 63) >> 6;
+        int jk[kRowRegs], rk[kRowRegs];
+        float xk[kRowRegs], yk[kRowRegs], zk[kRowRegs];
+#pragma unroll
+        for (int k = 0; k < kRowRegs; ++k) {
+            const int a = k * 64 + lane;
+            jk[k] = 0;
+            rk[k] = 0;
+            xk[k] = yk[k] = zk[k] = 0.f;
+            if (a < len) {
+                jk[k] = edst[s + a];
+                xk[k] = evec[(s + a) * 3];
+                yk[k] = evec[(s + a) * 3 + 1];
+                zk[k] = evec[(s + a) * 3 + 2];
+            }
         }
-        edst[q + 1] = v;
-        evec[(q + 1) * 3] = v0;
-        evec[(q + 1) * 3 + 1] = v1;
-        evec[(q + 1) * 3 + 2] = v2;
+#pragma unroll
+        for (int k2 = 0; k2 < kRowRegs; ++k2) {
+            if (k2 < nk) {
+                const int m_end = min(64, len - k2 * 64);
+                for (int m = 0; m < m_end; ++m) {
+                    const int jm = __builtin_amdgcn_readlane(jk[k2], m);
+                    const int pm = k2 * 64 + m;
+#pragma unroll
+                    for (int k = 0; k < kRowRegs; ++k)
+                        rk[k] += (jm < jk[k] || (jm == jk[k] && pm < k * 64 + lane)) ? 1 : 0;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kRowRegs; ++k)
+            if (k * 64 + lane < len) put(s + rk[k], jk[k], xk[k], yk[k], zk[k]);
+        return;
     }
-    if constexpr (GRAPH)
-        for (int64_t a = s; a < e; ++a) put(a, edst[a], evec[a * 3], evec[a * 3 + 1], evec[a * 3 + 2]);
+    for (int base = 0; base < len; base += 64) {
+        const int a = base + lane;
+        const int ja = a < len ? edst[s + a] : 0;
+        int r = 0;
+        for (int c0 = 0; c0 < len; c0 += 64) {
+            const int x = c0 + lane < len ? edst[s + c0 + lane] : 0;
+            const int m_end = min(64, len - c0);
+            for (int m = 0; m < m_end; ++m) {
+                const int jm = __builtin_amdgcn_readlane(x, m);
+                r += (jm < ja || (jm == ja && c0 + m < a)) ? 1 : 0;
+            }
+        }
+        if (a < len) {
+            if constexpr (GRAPH)
+                put(s + r, ja, evec[(s + a) * 3], evec[(s + a) * 3 + 1], evec[(s + a) * 3 + 2]);
+            else
+                esrc[s + a] = r;
+        }
+    }
+    if constexpr (!GRAPH) {
+        __threadfence_block();  // the wave's rank stores are complete before lane 0 reads them
+        if (lane == 0) {
+            for (int a = 0; a < len; ++a) {
+                int r = esrc[s + a];
+                while (r != a) {  // the entry at a belongs at r: swap it there
+                    const int64_t pa = s + a, pr = s + r;
+                    const int tj = edst[pa];
+                    edst[pa] = edst[pr];
+                    edst[pr] = tj;
+#pragma unroll
+                    for (int d = 0; d < 3; ++d) {
+                        const float tv = evec[pa * 3 + d];
+                        evec[pa * 3 + d] = evec[pr * 3 + d];
+                        evec[pr * 3 + d] = tv;
+                    }
+                    const int rr = esrc[pr];
+                    esrc[pr] = r;
+                    r = rr;
+                }
+            }
+        }
+        __threadfence_block();
+        for (int a = lane; a < len; a += 64) esrc[s + a] = (int)row;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -509,7 +584,7 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
         nl_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(bin_of, bin_start, bin_count,
                                                                     order, N);
         nl_sort_bins_wave_kernel<<<(unsigned)c.total, 64, 0, stream>>>(bin_start, order,
-                                                                         c.total);
+                                                                         bin_of, c.total);
         nl_cell_kernel<false><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
             nullptr, nullptr);
@@ -543,7 +618,7 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, edge_src,
             edge_dst, edge_vectors);
         nl_sort_rows_kernel<false><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
-            offsets, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr);
+            offsets, edge_src, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr);
     }
     if (row_offsets) {
         hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
@@ -619,7 +694,7 @@ extern "C" int batteries_neighbor_graph_write(const float* positions, const floa
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, nullptr,
             tmp_j, tmp_vec);
         nl_sort_rows_kernel<true><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
-            offsets, tmp_j, tmp_vec, N, src, dst, edge_vectors);
+            offsets, nullptr, tmp_j, tmp_vec, N, src, dst, edge_vectors);
         if (spatial_order)
             nl_serpentine_order_kernel<<<1, kSerpBlock, 0, stream>>>(bin_start, order, c,
                                                                      spatial_order);

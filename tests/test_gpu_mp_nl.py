@@ -179,7 +179,7 @@ def test_neighbor_list_reference_cases(bm, dev):
 def test_neighbor_list_dense_long_rows_and_chunked_cells(bm, dev):
     """3000 atoms in a 12 A box with r_c = 4 A: 3 bins per axis, so every cell's
     27-cell candidate list is the whole system (> 2048 staged per chunk), and
-    rows hold ~300 neighbours (> 64: the single-lane row sort)."""
+    rows hold ~300 neighbours (> 64: ranked in registers, five entries per lane)."""
     pos = torch.rand(3000, 3, generator=gen(7)) * 12.0
     cell = torch.diag(torch.tensor([12.0, 12.0, 12.0]))
     ei, vec, off = _nl_gpu(bm, dev, pos, cell, 4.0)
@@ -189,6 +189,34 @@ def test_neighbor_list_dense_long_rows_and_chunked_cells(bm, dev):
     np.testing.assert_array_equal(vec, v)
     bs, bd, bv = onl.brute_force(pos.numpy(), cell.numpy(), 4.0)
     np.testing.assert_array_equal(ei, np.stack([bs, bd]))
+
+
+def test_neighbor_list_bin_over_1024_atoms_and_rows_over_512(bm, dev):
+    """1100 atoms packed into one 5 A cell of a 30 A box (6 bins per axis) among 1500
+    spread over the box: that bin holds > 1024 atoms (the bin sort ranks them from
+    memory instead of LDS) and its atoms' rows hold > 512 neighbours (ranked from
+    memory: permuted in place by cycles in the [2, E] layout, written out in the
+    message-passing layout), the rows of atoms near it 65..512 (ranked in registers).
+    Both layouts bit-exact against the C restatement and brute force."""
+    g = gen(11)
+    dense = torch.rand(1100, 3, generator=g) * 4.6 + 0.2
+    spread = torch.rand(1500, 3, generator=g) * 30.0
+    pos = torch.cat([spread[:700], dense, spread[700:]])
+    cell = torch.diag(torch.tensor([30.0, 30.0, 30.0]))
+    ei, vec, off = _nl_gpu(bm, dev, pos, cell, 5.0)
+    deg = np.diff(off)
+    assert deg.max() > 512 and ((deg > 64) & (deg <= 512)).any()
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
+    np.testing.assert_array_equal(ei, np.stack([s, d]))
+    np.testing.assert_array_equal(vec, v)
+    bs, bd, bv = onl.brute_force(pos.numpy(), cell.numpy(), 5.0)
+    np.testing.assert_array_equal(ei, np.stack([bs, bd]))
+    np.testing.assert_array_equal(vec, bv)
+    src, dst, gvec, goff, _ = bm.neighbor_graph(pos.to(dev), cell, 5.0, False)
+    np.testing.assert_array_equal(src.cpu().numpy(), d)
+    np.testing.assert_array_equal(dst.cpu().numpy(), s)
+    np.testing.assert_array_equal(gvec.cpu().numpy(), -v)
+    np.testing.assert_array_equal(goff.cpu().numpy(), off)
 
 
 def test_neighbor_list_small_box_self_loops_and_lattice(bm, dev):
