@@ -122,8 +122,10 @@ def test_tp_simple_backward(bm, dev):
 
 
 @pytest.mark.parametrize("n,cin,cout", [(1000, 32, 64), (37, 3, 5), (64, 16, 16), (5, 64, 128),
-                                         (17, 40, 200)])
+                                         (17, 40, 200), (256, 24, 64), (129, 16, 80)])
 def test_tp_weighted_forward(bm, dev, n, cin, cout):
+    # row tiles are dealt to workgroups eight at a time (one per XCD): 256 rows fill
+    # two rounds exactly, 129 rows leave one row in a ninth tile and seven idle ones
     # (1000, 32, 64) is configs[1]: x ~ N(0,1), Y of normalised Gaussian vectors, W ~ N(0, 1/C_in)
     x = torch.randn(n, cin, 16, generator=gen(1))
     y = bm.spherical_harmonics(unit_vectors(n, 2).to(dev), 3).cpu()
