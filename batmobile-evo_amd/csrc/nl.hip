@@ -167,6 +167,109 @@ __global__ __launch_bounds__(64) void nl_sort_bins_wave_kernel(const int64_t* __
     }
 }
 
+// Binning of a small system in one workgroup, in place of the zero / assign /
+// scan / zero / place / sort-bins sequence (six launches of a few microseconds
+// each) when the atoms and bins fit in LDS: bins counted with LDS atomics and
+// scanned in LDS, atoms placed in arbitrary order within their bin, then each
+// atom written at its bin's start plus its rank in the bin (the number of its
+// atoms with a smaller index).  The same bin_start and order as the sequence.
+constexpr int kBinSmallBlock = 1024;
+constexpr int kBinSmallAtoms = 8192;
+constexpr int kBinSmallBins = 4096;
+constexpr int kBinSmallPer = kBinSmallAtoms / kBinSmallBlock;  // atoms per thread
+static_assert(kBinSmallBins == 4 * kBinSmallBlock, "four bins per thread in the scan");
+
+__global__ __launch_bounds__(kBinSmallBlock) void nl_bin_small_kernel(
+    const float* __restrict__ pos, BinCfg c, int n, int64_t* __restrict__ bin_start,
+    int* __restrict__ order) {
+    __shared__ int sCnt[kBinSmallBins];
+    __shared__ int sStart[kBinSmallBins + 1];
+    __shared__ int sPlace[kBinSmallAtoms];
+    __shared__ int sWave[kBinSmallBlock / 64];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int total = c.total;
+    // every position load issued before any is used (clamped, unconditional: a load
+    // under a branch would be waited for before the next one is issued)
+    float p[kBinSmallPer][3];
+#pragma unroll
+    for (int j = 0; j < kBinSmallPer; ++j) {
+        const int64_t i = max(min(t + j * kBinSmallBlock, n - 1), 0);
+#pragma unroll
+        for (int d = 0; d < 3; ++d) p[j][d] = n > 0 ? pos[i * 3 + d] : 0.0f;
+    }
+    for (int k = t; k < kBinSmallBins; k += kBinSmallBlock) sCnt[k] = 0;
+    __syncthreads();
+    int bin[kBinSmallPer];
+#pragma unroll
+    for (int j = 0; j < kBinSmallPer; ++j) {
+        bin[j] = -1;
+        if (t + j * kBinSmallBlock < n) {
+            int b[3];
+            bin_coords(p[j][0], p[j][1], p[j][2], c, b);
+            bin[j] = b[0] + b[1] * c.nb[0] + b[2] * c.nb[0] * c.nb[1];
+            atomicAdd(&sCnt[bin[j]], 1);
+        }
+    }
+    __syncthreads();
+    // exclusive scan of the counts: four bins per thread, shuffles within a wave,
+    // then the wave totals
+    int v[4], sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        v[q] = sCnt[4 * t + q];
+        sum += v[q];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += u;
+    }
+    if (lane == 63) sWave[wv] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += sWave[w];
+    int run = base + incl - sum;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int k = 4 * t + q;
+        sStart[k] = run;
+        if (k < total) bin_start[k] = run;
+        sCnt[k] = 0;  // the placement cursor from here on
+        run += v[q];
+    }
+    if (t == 0) {
+        sStart[kBinSmallBins] = n;
+        bin_start[total] = n;
+    }
+    __syncthreads();
+    // every placement's atomic issued before the writes that use them
+    int slot[kBinSmallPer];
+#pragma unroll
+    for (int j = 0; j < kBinSmallPer; ++j)
+        slot[j] = bin[j] >= 0 ? sStart[bin[j]] + atomicAdd(&sCnt[bin[j]], 1) : 0;
+#pragma unroll
+    for (int j = 0; j < kBinSmallPer; ++j)
+        if (bin[j] >= 0) sPlace[slot[j]] = t + j * kBinSmallBlock;
+    __syncthreads();
+    // rank in the bin, four LDS reads in flight per step
+#pragma unroll
+    for (int j = 0; j < kBinSmallPer; ++j) {
+        if (bin[j] < 0) continue;
+        const int i = t + j * kBinSmallBlock;
+        const int b0 = sStart[bin[j]], b1 = sStart[bin[j] + 1];
+        int r = 0;
+        for (int u = b0; u < b1; u += 4) {
+            int x[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[q] = sPlace[min(u + q, b1 - 1)];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) r += (u + q < b1 && x[q] < i) ? 1 : 0;
+        }
+        order[b0 + r] = i;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Stencil passes (count, then write): one workgroup of kNlWaves waves per home
 // cell.  The atoms of the 27 cells around it (reference order: dz, dy, dx from
@@ -305,7 +408,8 @@ __global__ __launch_bounds__(64 * kNlWaves) void nl_cell_kernel(const float* __r
 // memory, 64 entries at a time: GRAPH writes each entry at its rank in the
 // output arrays; the in-place form keeps the ranks in esrc (the row's source
 // column, which holds the row index and is restored afterwards), and one lane
-// applies the permutation by following its cycles (one swap per entry).
+// applies the permutation by following its cycles (one swap per entry); a caller
+// that passes no source column gets an insertion sort by one lane instead.
 // GRAPH: the sorted row goes to the message-passing layout instead (int64
 // gsrc = j, gdst = i, gvec = the vector negated: edges grouped by destination
 // i, each with vector r_i - r_j), and edst / evec are left as they are.
@@ -389,6 +493,26 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
         for (int k = 0; k < kRowRegs; ++k)
             if (k * 64 + lane < len) put(s + rk[k], jk[k], xk[k], yk[k], zk[k]);
         return;
+    }
+    if constexpr (!GRAPH) {
+        if (esrc == nullptr) {  // no source column to hold the ranks: insertion by one lane
+            if (lane == 0)
+                for (int64_t a = s + 1; a < e; ++a) {
+                    const int v = edst[a];
+                    const float v0 = evec[a * 3], v1 = evec[a * 3 + 1], v2 = evec[a * 3 + 2];
+                    int64_t q = a - 1;
+                    for (; q >= s && edst[q] > v; --q) {
+                        edst[q + 1] = edst[q];
+#pragma unroll
+                        for (int d = 0; d < 3; ++d) evec[(q + 1) * 3 + d] = evec[q * 3 + d];
+                    }
+                    edst[q + 1] = v;
+                    evec[(q + 1) * 3] = v0;
+                    evec[(q + 1) * 3 + 1] = v1;
+                    evec[(q + 1) * 3 + 2] = v2;
+                }
+            return;
+        }
     }
     for (int base = 0; base < len; base += 64) {
         const int a = base + lane;
@@ -573,18 +697,26 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
     int64_t* counts = reinterpret_cast<int64_t*>(ws + L.counts);
     int64_t* offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
     const int B = 256;
-    nl_zero_i32_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_count, c.total);
-    if (N > 0)
-        nl_assign_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(positions, c, bin_of, bin_count,
-                                                                     N);
-    int rc = scan_i32(bin_count, bin_start, c.total, stream);
-    if (rc != BM_OK) return rc;
-    nl_zero_i32_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_count, c.total);
+    int rc = BM_OK;
+    if (N <= kBinSmallAtoms && c.total <= kBinSmallBins) {
+        nl_bin_small_kernel<<<1, kBinSmallBlock, 0, stream>>>(positions, c, (int)N, bin_start,
+                                                              order);
+    } else {
+        nl_zero_i32_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_count, c.total);
+        if (N > 0)
+            nl_assign_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(positions, c, bin_of,
+                                                                         bin_count, N);
+        rc = scan_i32(bin_count, bin_start, c.total, stream);
+        if (rc != BM_OK) return rc;
+        nl_zero_i32_kernel<<<(unsigned)ceil_div(c.total, B), B, 0, stream>>>(bin_count, c.total);
+        if (N > 0) {
+            nl_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(bin_of, bin_start,
+                                                                        bin_count, order, N);
+            nl_sort_bins_wave_kernel<<<(unsigned)c.total, 64, 0, stream>>>(bin_start, order,
+                                                                           bin_of, c.total);
+        }
+    }
     if (N > 0) {
-        nl_place_kernel<<<(unsigned)ceil_div(N, B), B, 0, stream>>>(bin_of, bin_start, bin_count,
-                                                                    order, N);
-        nl_sort_bins_wave_kernel<<<(unsigned)c.total, 64, 0, stream>>>(bin_start, order,
-                                                                         bin_of, c.total);
         nl_cell_kernel<false><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
             nullptr, nullptr);

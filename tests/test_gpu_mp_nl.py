@@ -158,6 +158,22 @@ def test_neighbor_list_bit_exact(bm, dev, n):
         np.testing.assert_array_equal(vec, bv)
 
 
+@pytest.mark.parametrize("n,box", [(8192, None), (8193, None), (500, 100.0), (0, 30.0)])
+def test_neighbor_list_binning_paths(bm, dev, n, box):
+    """Systems of up to 8192 atoms in up to 4096 bins are binned by one workgroup, larger
+    ones by the multi-kernel sequence: both sides of each limit, bit-exact."""
+    if box is None:
+        pos, cell = periodic_box(n, n)
+    else:
+        pos = torch.rand(n, 3, generator=gen(n + 1)) * box
+        cell = torch.diag(torch.tensor([box, box, box]))
+    ei, vec, off = _nl_gpu(bm, dev, pos, cell)
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
+    np.testing.assert_array_equal(ei, np.stack([s, d]))
+    np.testing.assert_array_equal(vec, v)
+    assert off.shape == (n + 1,) and off[0] == 0 and off[-1] == len(s)
+
+
 def test_neighbor_list_reference_cases(bm, dev):
     """The reference's correctness cases (tests/test_neighbor_list.cu:264-266: N = 100, 500,
     1000, density 0.05, cutoff 5, std::mt19937(42) positions from tests/golden/): bit-exact
