@@ -538,7 +538,7 @@ torch::Tensor spatial_order(const torch::Tensor& positions, const torch::Tensor&
 // rows_per_block) for sh_tp_scatter_scheduled.
 std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t> mp_schedule(
     const torch::Tensor& row_ptr, const torch::Tensor& order, int64_t C,
-    const c10::optional<torch::Tensor>& col_perm) {
+    const c10::optional<torch::Tensor>& col_perm, int64_t num_edges) {
     TORCH_CHECK(row_ptr.dim() == 1 && row_ptr.dtype() == torch::kInt64 && row_ptr.numel() >= 1,
                 "row_ptr must be int64 [N_dst + 1]");
     const int64_t N = row_ptr.numel() - 1;
@@ -549,7 +549,8 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, int64_t, int64_t> mp_sch
     check_device(order, "order");
     int nb = 0, rpb = 0;
     check_status(batteries_mp_schedule_shape(N, (int)C, &nb, &rpb), "mp_schedule");
-    const int64_t E = row_ptr[N].item<int64_t>();
+    // E from the caller when it knows it (no host sync), else from row_ptr[N]
+    const int64_t E = num_edges >= 0 ? num_edges : row_ptr[N].item<int64_t>();
     const int64_t* cp = nullptr;
     if (col_perm.has_value() && col_perm->defined()) {
         TORCH_CHECK(col_perm->dtype() == torch::kInt64 && col_perm->numel() == E,
@@ -641,13 +642,15 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
     torch::Tensor src = torch::empty({E}, i32);
     torch::Tensor dst = torch::empty({E}, i32);
     torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
-    torch::Tensor offsets = torch::empty({N + 1}, i64);
     check_status(batteries_neighbor_list_write(cptr<float>(positions, "positions"), box, N, rc,
                                                self_loops ? 1 : 0, ws.data_ptr(), wsb,
                                                src.data_ptr<int>(), dst.data_ptr<int>(),
-                                               vec.data_ptr<float>(), offsets.data_ptr<int64_t>(),
-                                               s),
+                                               vec.data_ptr<float>(), nullptr, s),
                  "neighbor_list");
+    // the row offsets read in place from the workspace (a view that keeps it alive)
+    const size_t at = batteries_neighbor_list_offsets_at(N, box, rc);
+    TORCH_CHECK(at > 0 && at % 8 == 0, "neighbor_list: workspace layout");
+    torch::Tensor offsets = ws.narrow(0, (int64_t)(at / 8), N + 1);
     torch::Tensor edge_index = torch::stack({src.to(torch::kInt64), dst.to(torch::kInt64)}, 0);
     return {edge_index, vec, offsets};
 }
@@ -686,14 +689,17 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor, torch::Te
     torch::Tensor src = torch::empty({E}, i64);
     torch::Tensor dst = torch::empty({E}, i64);
     torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
-    torch::Tensor offsets = torch::empty({N + 1}, i64);
     torch::Tensor order = torch::empty({N}, i64);
     check_status(batteries_neighbor_graph_write(
                      cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
                      ws.data_ptr(), wsb, tmp_j.data_ptr<int>(), tmp_vec.data_ptr<float>(),
                      src.data_ptr<int64_t>(), dst.data_ptr<int64_t>(), vec.data_ptr<float>(),
-                     offsets.data_ptr<int64_t>(), order.data_ptr<int64_t>(), s),
+                     nullptr, order.data_ptr<int64_t>(), s),
                  "neighbor_graph");
+    // the row offsets read in place from the workspace (a view that keeps it alive)
+    const size_t at = batteries_neighbor_list_offsets_at(N, box, rc);
+    TORCH_CHECK(at > 0 && at % 8 == 0, "neighbor_graph: workspace layout");
+    torch::Tensor offsets = ws.narrow(0, (int64_t)(at / 8), N + 1);
     return {src, dst, vec, offsets, order};
 }
 
@@ -943,11 +949,13 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("cutoff"), py::arg("self_loops") = false,
           "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], row_offsets)");
     m.def("spatial_order", &spatial_order, py::arg("positions"), py::arg("cell"),
-          "Atoms sorted by the Morton code of their cell (32^3 grid over the box)");
+          "Atoms sorted by the Morton code of their cell (2^b cells per axis, the largest "
+          "b <= 5 with 8^b <= N)");
     m.def("mp_schedule", &mp_schedule, py::arg("row_ptr"), py::arg("order"), py::arg("C"),
-          py::arg("col_perm") = py::none(),
+          py::arg("col_perm") = py::none(), py::arg("num_edges") = -1,
           "Spatial processing schedule for sh_tp_scatter_scheduled: "
-          "(row_ptr_s, edge_perm, row_dst, n_blocks, rows_per_block)");
+          "(row_ptr_s, edge_perm, row_dst, n_blocks, rows_per_block); num_edges = row_ptr[-1] "
+          "when the caller knows it (saves a host sync)");
     m.def("sh_tp_scatter_scheduled", &sh_tp_scatter_scheduled, py::arg("edge_vectors"),
           py::arg("node_features"), py::arg("source_idx"), py::arg("row_ptr_s"),
           py::arg("edge_perm"), py::arg("row_dst"), py::arg("n_blocks"),

@@ -573,7 +573,8 @@ constexpr int kScanPer = 16;
 template <typename TI>
 __global__ __launch_bounds__(kScanBlock) void scan_exclusive_kernel(const TI* __restrict__ in,
                                                                     int64_t* __restrict__ out,
-                                                                    int64_t n) {
+                                                                    int64_t n,
+                                                                    int64_t* __restrict__ total_out) {
     constexpr int kWaves = kScanBlock / 64;
     __shared__ int64_t wsum[kWaves];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -624,15 +625,19 @@ __global__ __launch_bounds__(kScanBlock) void scan_exclusive_kernel(const TI* __
         }
         carry += total;
     }
-    if (t == 0) out[n] = carry;
+    if (t == 0) {
+        out[n] = carry;
+        if (total_out) *total_out = carry;  // the total once more (a copy the caller skips)
+    }
 }
 
-static int scan_i64(const int64_t* in, int64_t* out, int64_t n, hipStream_t s) {
-    scan_exclusive_kernel<int64_t><<<1, kScanBlock, 0, s>>>(in, out, n);
+static int scan_i64(const int64_t* in, int64_t* out, int64_t n, hipStream_t s,
+                    int64_t* total_out = nullptr) {
+    scan_exclusive_kernel<int64_t><<<1, kScanBlock, 0, s>>>(in, out, n, total_out);
     return (int)hipGetLastError();
 }
 static int scan_i32(const int* in, int64_t* out, int64_t n, hipStream_t s) {
-    scan_exclusive_kernel<int><<<1, kScanBlock, 0, s>>>(in, out, n);
+    scan_exclusive_kernel<int><<<1, kScanBlock, 0, s>>>(in, out, n, nullptr);
     return (int)hipGetLastError();
 }
 
@@ -681,6 +686,12 @@ extern "C" size_t batteries_neighbor_list_workspace_bytes(int64_t N, const float
     return nl_layout(N, c.total).total_bytes;
 }
 
+extern "C" size_t batteries_neighbor_list_offsets_at(int64_t N, const float* box, float cutoff) {
+    if (N < 0 || !box || !valid_box(box, cutoff)) return 0;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    return nl_layout(N, c.total).offsets;
+}
+
 extern "C" int batteries_neighbor_list_count(const float* positions, const float* box, int64_t N,
                                              float cutoff, int self_loops, void* workspace,
                                              size_t workspace_bytes, int64_t* d_num_edges,
@@ -721,13 +732,8 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
             nullptr, nullptr);
     }
-    rc = scan_i64(counts, offsets, N, stream);
+    rc = scan_i64(counts, offsets, N, stream, d_num_edges);
     if (rc != BM_OK) return rc;
-    if (d_num_edges) {
-        hipError_t e = hipMemcpyAsync(d_num_edges, offsets + N, sizeof(int64_t),
-                                      hipMemcpyDeviceToDevice, stream);
-        if (e != hipSuccess) return (int)e;
-    }
     return (int)hipGetLastError();
 }
 

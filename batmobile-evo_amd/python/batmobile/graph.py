@@ -39,7 +39,8 @@ class Graph:
         self.channels = int(channels)
         self.order = order
         (self.row_ptr_s, self.edge_perm, self.row_dst, self.n_blocks,
-         self.rows_per_block) = _batmobile.mp_schedule(self.row_ptr, self.order, self.channels)
+         self.rows_per_block) = _batmobile.mp_schedule(self.row_ptr, self.order, self.channels,
+                                                       None, int(src.numel()))
 
     @property
     def num_edges(self):

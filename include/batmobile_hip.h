@@ -259,6 +259,13 @@ int batteries_exclusive_scan_i64(const int64_t* in, int64_t* out, int64_t n, hip
 /* Workspace for the two-phase build; box (host) = cell diagonal. 0 if invalid. */
 size_t batteries_neighbor_list_workspace_bytes(int64_t N, const float* box, float cutoff);
 
+/* Byte offset, inside that workspace, of the row offsets (int64 [N+1]) that phase 1
+ * leaves there: a caller may read them in place (until the workspace is reused)
+ * instead of a copy through row_offsets.  0 if invalid (a valid offset is never 0).
+ * No counterpart in the reference, whose offsets stay internal to
+ * batteries::neighbor_list_cuda. */
+size_t batteries_neighbor_list_offsets_at(int64_t N, const float* box, float cutoff);
+
 /* Phase 1: bins, per-atom counts, offsets; writes E to *d_num_edges (device,
  * may be NULL).  Steps :261-366 of batteries::neighbor_list_cuda,
  * src/neighbor_list/neighbor_list.cu. */
