@@ -639,19 +639,19 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
                                                total.data_ptr<int64_t>(), s),
                  "neighbor_list");
     const int64_t E = total.item<int64_t>();  // one host sync, as in the reference
-    torch::Tensor src = torch::empty({E}, i32);
-    torch::Tensor dst = torch::empty({E}, i32);
+    torch::Tensor tmp_j = torch::empty({E}, i32);
+    torch::Tensor tmp_vec = torch::empty({E, 3}, f32_like(positions));
+    torch::Tensor edge_index = torch::empty({2, E}, i64);
     torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
-    check_status(batteries_neighbor_list_write(cptr<float>(positions, "positions"), box, N, rc,
-                                               self_loops ? 1 : 0, ws.data_ptr(), wsb,
-                                               src.data_ptr<int>(), dst.data_ptr<int>(),
-                                               vec.data_ptr<float>(), nullptr, s),
+    check_status(batteries_neighbor_list_write_i64(
+                     cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
+                     ws.data_ptr(), wsb, E, tmp_j.data_ptr<int>(), tmp_vec.data_ptr<float>(),
+                     edge_index.data_ptr<int64_t>(), vec.data_ptr<float>(), nullptr, s),
                  "neighbor_list");
     // the row offsets read in place from the workspace (a view that keeps it alive)
     const size_t at = batteries_neighbor_list_offsets_at(N, box, rc);
     TORCH_CHECK(at > 0 && at % 8 == 0, "neighbor_list: workspace layout");
     torch::Tensor offsets = ws.narrow(0, (int64_t)(at / 8), N + 1);
-    torch::Tensor edge_index = torch::stack({src.to(torch::kInt64), dst.to(torch::kInt64)}, 0);
     return {edge_index, vec, offsets};
 }
 

@@ -410,9 +410,10 @@ __global__ __launch_bounds__(64 * kNlWaves) void nl_cell_kernel(const float* __r
 // column, which holds the row index and is restored afterwards), and one lane
 // applies the permutation by following its cycles (one swap per entry); a caller
 // that passes no source column gets an insertion sort by one lane instead.
-// GRAPH: the sorted row goes to the message-passing layout instead (int64
-// gsrc = j, gdst = i, gvec = the vector negated: edges grouped by destination
-// i, each with vector r_i - r_j), and edst / evec are left as they are.
+// GRAPH: the sorted row goes to int64 arrays instead, edst / evec are left as
+// they are: the message-passing layout (gsrc = j, gdst = i, gvec = the vector
+// negated: edges grouped by destination i, each with vector r_i - r_j), or with
+// ref the neighbor list's own (gsrc = i, gdst = j, gvec = the vector).
 constexpr int kRowRegs = 8;
 template <bool GRAPH>
 __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __restrict__ offsets,
@@ -421,7 +422,7 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
                                                            float* __restrict__ evec, int64_t n,
                                                            int64_t* __restrict__ gsrc,
                                                            int64_t* __restrict__ gdst,
-                                                           float* __restrict__ gvec) {
+                                                           float* __restrict__ gvec, int ref) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;  // uniform per wave
@@ -429,11 +430,19 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
     const int len = (int)(e - s);
     auto put = [&](int64_t at, int j, float v0, float v1, float v2) {
         if constexpr (GRAPH) {
-            gsrc[at] = j;
-            gdst[at] = row;
-            gvec[at * 3] = -v0;
-            gvec[at * 3 + 1] = -v1;
-            gvec[at * 3 + 2] = -v2;
+            if (ref) {  // uniform: the neighbor list itself with int64 indices
+                gsrc[at] = row;
+                gdst[at] = j;
+                gvec[at * 3] = v0;
+                gvec[at * 3 + 1] = v1;
+                gvec[at * 3 + 2] = v2;
+            } else {
+                gsrc[at] = j;
+                gdst[at] = row;
+                gvec[at * 3] = -v0;
+                gvec[at * 3 + 1] = -v1;
+                gvec[at * 3 + 2] = -v2;
+            }
         } else {
             edst[at] = j;
             evec[at * 3] = v0;
@@ -756,7 +765,7 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, edge_src,
             edge_dst, edge_vectors);
         nl_sort_rows_kernel<false><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
-            offsets, edge_src, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr);
+            offsets, edge_src, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr, 0);
     }
     if (row_offsets) {
         hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
@@ -813,12 +822,13 @@ __global__ __launch_bounds__(kSerpBlock) void nl_serpentine_order_kernel(
     }
 }
 
-extern "C" int batteries_neighbor_graph_write(const float* positions, const float* box, int64_t N,
-                                              float cutoff, int self_loops, void* workspace,
-                                              size_t workspace_bytes, int* tmp_j, float* tmp_vec,
-                                              int64_t* src, int64_t* dst, float* edge_vectors,
-                                              int64_t* row_offsets, int64_t* spatial_order,
-                                              hipStream_t stream) {
+// Phase 2 into int64 arrays: the message-passing layout (ref = 0) or the neighbor
+// list's own orientation (ref = 1).
+static int neighbor_write_i64(const float* positions, const float* box, int64_t N, float cutoff,
+                              int self_loops, void* workspace, size_t workspace_bytes, int* tmp_j,
+                              float* tmp_vec, int64_t* src, int64_t* dst, float* edge_vectors,
+                              int64_t* row_offsets, int64_t* spatial_order, int ref,
+                              hipStream_t stream) {
     if (N < 0 || !box || !valid_box(box, cutoff)) return BM_ERR_ARG;
     const BinCfg c = make_bin_cfg(box, cutoff);
     const NlLayout L = nl_layout(N, c.total);
@@ -832,7 +842,7 @@ extern "C" int batteries_neighbor_graph_write(const float* positions, const floa
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, nullptr,
             tmp_j, tmp_vec);
         nl_sort_rows_kernel<true><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
-            offsets, nullptr, tmp_j, tmp_vec, N, src, dst, edge_vectors);
+            offsets, nullptr, tmp_j, tmp_vec, N, src, dst, edge_vectors, ref);
         if (spatial_order)
             nl_serpentine_order_kernel<<<1, kSerpBlock, 0, stream>>>(bin_start, order, c,
                                                                      spatial_order);
@@ -843,6 +853,29 @@ extern "C" int batteries_neighbor_graph_write(const float* positions, const floa
         if (e != hipSuccess) return (int)e;
     }
     return (int)hipGetLastError();
+}
+
+extern "C" int batteries_neighbor_graph_write(const float* positions, const float* box, int64_t N,
+                                              float cutoff, int self_loops, void* workspace,
+                                              size_t workspace_bytes, int* tmp_j, float* tmp_vec,
+                                              int64_t* src, int64_t* dst, float* edge_vectors,
+                                              int64_t* row_offsets, int64_t* spatial_order,
+                                              hipStream_t stream) {
+    return neighbor_write_i64(positions, box, N, cutoff, self_loops, workspace, workspace_bytes,
+                              tmp_j, tmp_vec, src, dst, edge_vectors, row_offsets, spatial_order,
+                              0, stream);
+}
+
+extern "C" int batteries_neighbor_list_write_i64(const float* positions, const float* box,
+                                                 int64_t N, float cutoff, int self_loops,
+                                                 void* workspace, size_t workspace_bytes,
+                                                 int64_t num_edges, int* tmp_j, float* tmp_vec,
+                                                 int64_t* edge_index, float* edge_vectors,
+                                                 int64_t* row_offsets, hipStream_t stream) {
+    if (num_edges < 0 || (num_edges > 0 && !edge_index)) return BM_ERR_ARG;
+    return neighbor_write_i64(positions, box, N, cutoff, self_loops, workspace, workspace_bytes,
+                              tmp_j, tmp_vec, edge_index, edge_index + num_edges, edge_vectors,
+                              row_offsets, nullptr, 1, stream);
 }
 
 // ---------------------------------------------------------------------------

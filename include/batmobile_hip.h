@@ -301,6 +301,18 @@ int batteries_neighbor_graph_write(const float* positions, const float* box, int
                                    int64_t* row_offsets, int64_t* spatial_order,
                                    hipStream_t stream);
 
+/* Phase 2 with int64 indices in the neighbor list's own orientation (same
+ * workspace, after phase 1; num_edges = E from phase 1): edge_index [2, E] (row 0 =
+ * i, row 1 = j, sorted by (i, j)), edge_vectors [E, 3] = minimum-image pos[j] -
+ * pos[i], row_offsets [N+1] (may be NULL); tmp_j [E] and tmp_vec [E,3] are
+ * scratch.  The layout torch callers index with (int64); the reference's C ABI
+ * writes int32 (batteries_neighbor_list_write).  No counterpart in the reference. */
+int batteries_neighbor_list_write_i64(const float* positions, const float* box, int64_t N,
+                                      float cutoff, int self_loops, void* workspace,
+                                      size_t workspace_bytes, int64_t num_edges, int* tmp_j,
+                                      float* tmp_vec, int64_t* edge_index, float* edge_vectors,
+                                      int64_t* row_offsets, hipStream_t stream);
+
 /* Result of neighbor_list_cuda; same layout as include/neighbor_list.cuh:25-33. */
 typedef struct NeighborListResult {
     int* edge_index;      /* [2, num_edges] int32: row 0 = src i, row 1 = dst j */

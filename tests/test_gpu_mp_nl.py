@@ -211,9 +211,10 @@ def test_neighbor_list_bin_over_1024_atoms_and_rows_over_512(bm, dev):
     """1100 atoms packed into one 5 A cell of a 30 A box (6 bins per axis) among 1500
     spread over the box: that bin holds > 1024 atoms (the bin sort ranks them from
     memory instead of LDS) and its atoms' rows hold > 512 neighbours (ranked from
-    memory: permuted in place by cycles in the [2, E] layout, written out in the
-    message-passing layout), the rows of atoms near it 65..512 (ranked in registers).
-    Both layouts bit-exact against the C restatement and brute force."""
+    memory and written out to the int64 arrays of both torch layouts), the rows of
+    atoms near it 65..512 (ranked in registers).  Both layouts bit-exact against the C
+    restatement and brute force; the C ABI's in-place int32 sort of the same system is
+    test_neighbor_list_c_abi_long_rows_in_place."""
     g = gen(11)
     dense = torch.rand(1100, 3, generator=g) * 4.6 + 0.2
     spread = torch.rand(1500, 3, generator=g) * 30.0
@@ -269,31 +270,27 @@ def test_exclusive_scan_c_abi(bm, dev, n):
     np.testing.assert_array_equal(out.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("libpath", [NL_LIB, LIB])
-def test_neighbor_list_reference_c_abi(bm, dev, libpath):
-    """ctypes use as in reference benchmarks/benchmark_neighbor_list.py:18-47, through the
-    reference's library name (libbatteries_neighbor.so) and the full library."""
+class _NlResult(ctypes.Structure):
+    _fields_ = [("edge_index", ctypes.c_void_p), ("edge_vectors", ctypes.c_void_p),
+                ("num_edges", ctypes.c_int64), ("d_edge_index", ctypes.c_void_p),
+                ("d_edge_vectors", ctypes.c_void_p)]
 
-    class Result(ctypes.Structure):
-        _fields_ = [("edge_index", ctypes.c_void_p), ("edge_vectors", ctypes.c_void_p),
-                    ("num_edges", ctypes.c_int64), ("d_edge_index", ctypes.c_void_p),
-                    ("d_edge_vectors", ctypes.c_void_p)]
 
+def _nl_c_abi(libpath, dev, pos, cell, cutoff=5.0):
+    """neighbor_list_cuda through ctypes, as reference benchmarks/benchmark_neighbor_list.py:18-47
+    uses it: int32 edge_index [2, E] and vectors copied out of the library-owned buffers."""
     lib = ctypes.CDLL(libpath)
     lib.neighbor_list_cuda.restype = ctypes.c_int
     lib.neighbor_list_cuda.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
-                                       ctypes.c_bool, ctypes.POINTER(Result), ctypes.c_void_p]
-    lib.neighbor_list_free.argtypes = [ctypes.POINTER(Result)]
-    pos, cell = periodic_box(2000, 4)
+                                       ctypes.c_bool, ctypes.POINTER(_NlResult), ctypes.c_void_p]
+    lib.neighbor_list_free.argtypes = [ctypes.POINTER(_NlResult)]
+    n = pos.shape[0]
     pd, cd = pos.to(dev).contiguous(), cell.to(dev).contiguous()
     torch.cuda.synchronize()
-    res = Result()
-    rc = lib.neighbor_list_cuda(pd.data_ptr(), cd.data_ptr(), 2000, 5.0, False, ctypes.byref(res), None)
+    res = _NlResult()
+    rc = lib.neighbor_list_cuda(pd.data_ptr(), cd.data_ptr(), n, cutoff, False, ctypes.byref(res), None)
     assert rc == 0
     e = res.num_edges
-    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
-    assert e == len(s)
-    # copy the library-owned buffers out through torch
     ei = torch.empty(2 * e, dtype=torch.int32, device=dev)
     vv = torch.empty(e * 3, dtype=torch.float32, device=dev)
     hip = ctypes.CDLL("libamdhip64.so.7")
@@ -302,10 +299,36 @@ def test_neighbor_list_reference_c_abi(bm, dev, libpath):
     assert hip.hipMemcpy(vv.data_ptr(), res.d_edge_vectors, 12 * e, 3) == 0
     lib.neighbor_list_free(ctypes.byref(res))
     assert res.num_edges == 0 and not res.d_edge_index
-    ei = ei.cpu().numpy().reshape(2, e)
+    return ei.cpu().numpy().reshape(2, e), vv.cpu().numpy().reshape(e, 3)
+
+
+@pytest.mark.parametrize("libpath", [NL_LIB, LIB])
+def test_neighbor_list_reference_c_abi(bm, dev, libpath):
+    """ctypes use as in reference benchmarks/benchmark_neighbor_list.py:18-47, through the
+    reference's library name (libbatteries_neighbor.so) and the full library."""
+    pos, cell = periodic_box(2000, 4)
+    ei, vv = _nl_c_abi(libpath, dev, pos, cell)
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
     np.testing.assert_array_equal(ei[0], s)
     np.testing.assert_array_equal(ei[1], d)
-    np.testing.assert_array_equal(vv.cpu().numpy().reshape(e, 3), v)
+    np.testing.assert_array_equal(vv, v)
+
+
+def test_neighbor_list_c_abi_long_rows_in_place(bm, dev):
+    """The reference C ABI's int32 layout sorts rows in place: rows of 65..512 neighbours
+    ranked in registers, longer ones ranked from memory and permuted by cycles (ranks held
+    in the source column, which is restored).  The dense cluster of
+    test_neighbor_list_bin_over_1024_atoms_and_rows_over_512 through neighbor_list_cuda."""
+    g = gen(11)
+    dense = torch.rand(1100, 3, generator=g) * 4.6 + 0.2
+    spread = torch.rand(1500, 3, generator=g) * 30.0
+    pos = torch.cat([spread[:700], dense, spread[700:]])
+    cell = torch.diag(torch.tensor([30.0, 30.0, 30.0]))
+    ei, vv = _nl_c_abi(LIB, dev, pos, cell)
+    s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
+    assert np.bincount(s).max() > 512
+    np.testing.assert_array_equal(ei, np.stack([s, d]))
+    np.testing.assert_array_equal(vv, v)
 
 
 def test_config4_scatter_full_size(bm, dev):
