@@ -703,6 +703,54 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor, torch::Te
     return {src, dst, vec, offsets, order};
 }
 
+// The same with arrays of `capacity` edges and no host synchronisation: the edge
+// count stays on the device (offsets[N]); overflow [1] int32 is 1 when it exceeded
+// the capacity (then every row is empty).
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor>
+neighbor_graph_capacity(const torch::Tensor& positions, const torch::Tensor& cell, double cutoff,
+                        bool self_loops, int64_t capacity) {
+    TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
+    TORCH_CHECK(positions.dtype() == torch::kFloat32, "positions must be float32");
+    TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
+    TORCH_CHECK(capacity >= 0, "capacity must be >= 0");
+    check_device(positions, "positions");
+    const int64_t N = positions.size(0);
+    torch::Tensor cell_cpu = cell.detach().to(torch::kCPU, torch::kFloat32).contiguous();
+    const float* h = cell_cpu.data_ptr<float>();
+    const float box[3] = {h[0], h[4], h[8]};
+    const float rc = (float)cutoff;
+    const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, rc);
+    TORCH_CHECK(wsb > 0, "invalid cell or cutoff");
+    auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(positions.device());
+    auto i32 = torch::TensorOptions().dtype(torch::kInt32).device(positions.device());
+    const c10::DeviceGuard guard(positions.device());
+    hipStream_t s = current_stream(positions);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
+    check_status(batteries_neighbor_list_count(cptr<float>(positions, "positions"), box, N, rc,
+                                               self_loops ? 1 : 0, ws.data_ptr(), wsb, nullptr, s),
+                 "neighbor_graph_capacity");
+    torch::Tensor tmp_j = torch::empty({capacity}, i32);
+    torch::Tensor tmp_vec = torch::empty({capacity, 3}, f32_like(positions));
+    torch::Tensor src = torch::empty({capacity}, i64);
+    torch::Tensor dst = torch::empty({capacity}, i64);
+    torch::Tensor vec = torch::empty({capacity, 3}, f32_like(positions));
+    torch::Tensor order = torch::empty({N}, i64);
+    torch::Tensor overflow = torch::empty({1}, i32);
+    check_status(batteries_neighbor_graph_write_capacity(
+                     cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
+                     ws.data_ptr(), wsb, capacity, capacity ? tmp_j.data_ptr<int>() : nullptr,
+                     capacity ? tmp_vec.data_ptr<float>() : nullptr,
+                     capacity ? src.data_ptr<int64_t>() : nullptr,
+                     capacity ? dst.data_ptr<int64_t>() : nullptr,
+                     capacity ? vec.data_ptr<float>() : nullptr, nullptr,
+                     order.data_ptr<int64_t>(), overflow.data_ptr<int>(), s),
+                 "neighbor_graph_capacity");
+    const size_t at = batteries_neighbor_list_offsets_at(N, box, rc);
+    TORCH_CHECK(at > 0 && at % 8 == 0, "neighbor_graph_capacity: workspace layout");
+    torch::Tensor offsets = ws.narrow(0, (int64_t)(at / 8), N + 1);
+    return {src, dst, vec, offsets, order, overflow};
+}
+
 torch::Tensor selftest_mfma_16x16x4(const torch::Tensor& A, const torch::Tensor& B) {
     TORCH_CHECK(A.numel() == 64 && B.numel() == 64 && A.dtype() == torch::kFloat32 &&
                     B.dtype() == torch::kFloat32,
@@ -951,6 +999,12 @@ PYBIND11_MODULE(_batmobile, m) {
     m.def("spatial_order", &spatial_order, py::arg("positions"), py::arg("cell"),
           "Atoms sorted by the Morton code of their cell (2^b cells per axis, the largest "
           "b <= 5 with 8^b <= N)");
+    m.def("neighbor_graph_capacity", &neighbor_graph_capacity, py::arg("positions"),
+          py::arg("cell"), py::arg("cutoff"), py::arg("self_loops"), py::arg("capacity"),
+          "neighbor_graph with arrays of `capacity` edges and no host synchronisation: "
+          "(src, dst, edge_vectors, row_offsets, order, overflow); the edge count is "
+          "row_offsets[-1] on the device, overflow [1] is 1 (and every row empty) when it "
+          "exceeded the capacity");
     m.def("mp_schedule", &mp_schedule, py::arg("row_ptr"), py::arg("order"), py::arg("C"),
           py::arg("col_perm") = py::none(), py::arg("num_edges") = -1,
           "Spatial processing schedule for sh_tp_scatter_scheduled: "

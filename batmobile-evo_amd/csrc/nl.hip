@@ -292,7 +292,8 @@ __global__ __launch_bounds__(64 * kNlWaves) void nl_cell_kernel(const float* __r
                                                                 const int64_t* __restrict__ offsets,
                                                                 int* __restrict__ esrc,
                                                                 int* __restrict__ edst,
-                                                                float* __restrict__ evec) {
+                                                                float* __restrict__ evec,
+                                                                uint64_t cap) {
     __shared__ float4 sCand[kNlCap];
     __shared__ int sStart[27], sPre[28];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -351,8 +352,8 @@ __global__ __launch_bounds__(64 * kNlWaves) void nl_cell_kernel(const float* __r
             }
             const uint64_t m = __ballot(keep);
             if constexpr (WRITE) {
-                if (keep) {
-                    const int64_t at = w + __popcll(m & ((1ull << lane) - 1ull));
+                const int64_t at = w + __popcll(m & ((1ull << lane) - 1ull));
+                if (keep && (uint64_t)at < cap) {  // cap: the arrays' length (capacity mode)
                     if (esrc) esrc[at] = i;
                     edst[at] = j;
                     evec[at * 3 + 0] = d[0];
@@ -422,11 +423,13 @@ __global__ __launch_bounds__(256) void nl_sort_rows_kernel(const int64_t* __rest
                                                            float* __restrict__ evec, int64_t n,
                                                            int64_t* __restrict__ gsrc,
                                                            int64_t* __restrict__ gdst,
-                                                           float* __restrict__ gvec, int ref) {
+                                                           float* __restrict__ gvec, int ref,
+                                                           uint64_t cap) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;  // uniform per wave
     const int64_t s = offsets[row], e = offsets[row + 1];
+    if ((uint64_t)e > cap) return;  // capacity mode: a row past the arrays (flagged later)
     const int len = (int)(e - s);
     auto put = [&](int64_t at, int j, float v0, float v1, float v2) {
         if constexpr (GRAPH) {
@@ -739,7 +742,7 @@ extern "C" int batteries_neighbor_list_count(const float* positions, const float
     if (N > 0) {
         nl_cell_kernel<false><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, counts, nullptr, nullptr,
-            nullptr, nullptr);
+            nullptr, nullptr, ~0ull);
     }
     rc = scan_i64(counts, offsets, N, stream, d_num_edges);
     if (rc != BM_OK) return rc;
@@ -763,9 +766,9 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
     if (N > 0) {
         nl_cell_kernel<true><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, edge_src,
-            edge_dst, edge_vectors);
+            edge_dst, edge_vectors, ~0ull);
         nl_sort_rows_kernel<false><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
-            offsets, edge_src, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr, 0);
+            offsets, edge_src, edge_dst, edge_vectors, N, nullptr, nullptr, nullptr, 0, ~0ull);
     }
     if (row_offsets) {
         hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
@@ -794,7 +797,18 @@ __device__ __forceinline__ int serpentine_cell(int p, const BinCfg& c) {
 
 __global__ __launch_bounds__(kSerpBlock) void nl_serpentine_order_kernel(
     const int64_t* __restrict__ bin_start, const int* __restrict__ order, BinCfg c,
-    int64_t* __restrict__ out) {
+    int64_t* __restrict__ out, int64_t* __restrict__ offsets, int64_t n, uint64_t cap,
+    int* __restrict__ overflow) {
+    // capacity mode (after the passes that read the offsets): when the edges outgrew the
+    // arrays, every row is emptied, so that no later kernel reads past them, and the flag
+    // is raised; otherwise the flag is cleared
+    if (overflow) {
+        const bool over = (uint64_t)offsets[n] > cap;
+        __syncthreads();  // every thread has read the total before any is cleared
+        if (over)
+            for (int64_t i = threadIdx.x; i <= n; i += kSerpBlock) offsets[i] = 0;
+        if (threadIdx.x == 0) *overflow = over ? 1 : 0;
+    }
     __shared__ int64_t sWave[kSerpBlock / 64];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int per = (c.total + kSerpBlock - 1) / kSerpBlock;
@@ -816,10 +830,11 @@ __global__ __launch_bounds__(kSerpBlock) void nl_serpentine_order_kernel(
     int64_t base = 0;
     for (int i = 0; i < w; ++i) base += sWave[i];
     int64_t o = base + incl - sum;
-    for (int p = p0; p < p1; ++p) {
-        const int k = serpentine_cell(p, c);
-        for (int64_t a = bin_start[k]; a < bin_start[k + 1]; ++a) out[o++] = order[a];
-    }
+    if (out)
+        for (int p = p0; p < p1; ++p) {
+            const int k = serpentine_cell(p, c);
+            for (int64_t a = bin_start[k]; a < bin_start[k + 1]; ++a) out[o++] = order[a];
+        }
 }
 
 // Phase 2 into int64 arrays: the message-passing layout (ref = 0) or the neighbor
@@ -828,8 +843,9 @@ static int neighbor_write_i64(const float* positions, const float* box, int64_t 
                               int self_loops, void* workspace, size_t workspace_bytes, int* tmp_j,
                               float* tmp_vec, int64_t* src, int64_t* dst, float* edge_vectors,
                               int64_t* row_offsets, int64_t* spatial_order, int ref,
-                              hipStream_t stream) {
+                              int64_t capacity, int* overflow, hipStream_t stream) {
     if (N < 0 || !box || !valid_box(box, cutoff)) return BM_ERR_ARG;
+    const uint64_t cap = capacity < 0 ? ~0ull : (uint64_t)capacity;
     const BinCfg c = make_bin_cfg(box, cutoff);
     const NlLayout L = nl_layout(N, c.total);
     if (!workspace || workspace_bytes < L.total_bytes) return BM_ERR_WORKSPACE;
@@ -840,13 +856,14 @@ static int neighbor_write_i64(const float* positions, const float* box, int64_t 
     if (N > 0) {
         nl_cell_kernel<true><<<(unsigned)c.total, 64 * kNlWaves, 0, stream>>>(
             positions, c, cutoff * cutoff, self_loops, bin_start, order, nullptr, offsets, nullptr,
-            tmp_j, tmp_vec);
+            tmp_j, tmp_vec, cap);
         nl_sort_rows_kernel<true><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
-            offsets, nullptr, tmp_j, tmp_vec, N, src, dst, edge_vectors, ref);
-        if (spatial_order)
-            nl_serpentine_order_kernel<<<1, kSerpBlock, 0, stream>>>(bin_start, order, c,
-                                                                     spatial_order);
+            offsets, nullptr, tmp_j, tmp_vec, N, src, dst, edge_vectors, ref, cap);
     }
+    // the spatial order, and in capacity mode the overflow check (also for N = 0)
+    if ((N > 0 && spatial_order) || overflow)
+        nl_serpentine_order_kernel<<<1, kSerpBlock, 0, stream>>>(
+            bin_start, order, c, spatial_order, const_cast<int64_t*>(offsets), N, cap, overflow);
     if (row_offsets) {
         hipError_t e = hipMemcpyAsync(row_offsets, offsets, sizeof(int64_t) * (size_t)(N + 1),
                                       hipMemcpyDeviceToDevice, stream);
@@ -863,7 +880,18 @@ extern "C" int batteries_neighbor_graph_write(const float* positions, const floa
                                               hipStream_t stream) {
     return neighbor_write_i64(positions, box, N, cutoff, self_loops, workspace, workspace_bytes,
                               tmp_j, tmp_vec, src, dst, edge_vectors, row_offsets, spatial_order,
-                              0, stream);
+                              0, -1, nullptr, stream);
+}
+
+extern "C" int batteries_neighbor_graph_write_capacity(
+    const float* positions, const float* box, int64_t N, float cutoff, int self_loops,
+    void* workspace, size_t workspace_bytes, int64_t capacity, int* tmp_j, float* tmp_vec,
+    int64_t* src, int64_t* dst, float* edge_vectors, int64_t* row_offsets, int64_t* spatial_order,
+    int* overflow, hipStream_t stream) {
+    if (capacity < 0 || !overflow) return BM_ERR_ARG;
+    return neighbor_write_i64(positions, box, N, cutoff, self_loops, workspace, workspace_bytes,
+                              tmp_j, tmp_vec, src, dst, edge_vectors, row_offsets, spatial_order,
+                              0, capacity, overflow, stream);
 }
 
 extern "C" int batteries_neighbor_list_write_i64(const float* positions, const float* box,
@@ -875,7 +903,7 @@ extern "C" int batteries_neighbor_list_write_i64(const float* positions, const f
     if (num_edges < 0 || (num_edges > 0 && !edge_index)) return BM_ERR_ARG;
     return neighbor_write_i64(positions, box, N, cutoff, self_loops, workspace, workspace_bytes,
                               tmp_j, tmp_vec, edge_index, edge_index + num_edges, edge_vectors,
-                              row_offsets, nullptr, 1, stream);
+                              row_offsets, nullptr, 1, -1, nullptr, stream);
 }
 
 // ---------------------------------------------------------------------------

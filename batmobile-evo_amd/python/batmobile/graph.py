@@ -14,6 +14,12 @@ scatter) into GPU-resident tensors that the fused kernel consumes directly:
 The neighbor relation of a cell list is symmetric, so the neighbor list sorted
 by (i, j) read with roles swapped is exactly the edge list sorted by destination,
 with vectors negated (exactly, in fp32).
+
+With max_edges the edge arrays hold max_edges entries and the build runs without a
+host synchronisation (the edge count stays on the device, in row_ptr[-1]): the step
+of a simulation whose positions change every step then queues the graph build and
+the fused kernel back to back.  check() raises if the edges outgrew max_edges (the
+rows are then left empty, so the kernels that follow read nothing past the arrays).
 """
 import torch
 
@@ -21,11 +27,18 @@ import _batmobile
 
 
 class Graph:
-    def __init__(self, positions, cell, cutoff, channels, self_loops=False):
+    def __init__(self, positions, cell, cutoff, channels, self_loops=False, max_edges=None):
         # the neighbor list written directly in this layout (one pass, no torch glue),
         # with a spatial order of the atoms from its cells
-        src, dst, vec, off, order = _batmobile.neighbor_graph(positions, cell, float(cutoff),
-                                                              bool(self_loops))
+        if max_edges is None:
+            src, dst, vec, off, order = _batmobile.neighbor_graph(positions, cell, float(cutoff),
+                                                                  bool(self_loops))
+            self.overflow = None
+            self._num_edges = int(src.numel())
+        else:
+            src, dst, vec, off, order, self.overflow = _batmobile.neighbor_graph_capacity(
+                positions, cell, float(cutoff), bool(self_loops), int(max_edges))
+            self._num_edges = None
         self.cell = cell
         self.cutoff = float(cutoff)
         self.positions = positions
@@ -44,7 +57,27 @@ class Graph:
 
     @property
     def num_edges(self):
-        return int(self.src.numel())
+        """The number of edges (with max_edges: read back from the device, once)."""
+        if self._num_edges is None:
+            self.check()
+            self._num_edges = int(self.row_ptr[-1].item())
+        return self._num_edges
+
+    def check(self):
+        """Raise if the edges outgrew max_edges (a host synchronisation)."""
+        if self.overflow is not None and int(self.overflow.item()) != 0:
+            raise RuntimeError("batmobile.Graph: the neighbor list has more edges than "
+                               f"max_edges = {int(self.src.numel())}")
+
+    def exact(self):
+        """The edge arrays cut to the edge count (after check(); a no-op without
+        max_edges).  Consumers that take the edge count from the arrays' length (the
+        MACE layer, reverse_edges) call it first."""
+        e = self.num_edges
+        if self.src.numel() != e:
+            self.src, self.dst, self.vec = self.src[:e], self.dst[:e], self.vec[:e]
+            self.edge_perm = self.edge_perm[:e]
+        return self
 
     def fine_order(self):
         """Morton order of the atoms on a grid of 1 to 8 atoms per cell (spatial_order; built
@@ -57,6 +90,7 @@ class Graph:
     def reverse_edges(self):
         """rev[e]: index of the edge with source and destination swapped (built once)."""
         if self._rev is None:
+            self.exact()
             self._rev = _batmobile.mace_reverse_edges(self.row_ptr, self.src)
         return self._rev
 

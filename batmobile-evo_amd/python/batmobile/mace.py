@@ -50,6 +50,7 @@ class MaceLayerFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, positions, node_features, w1, b1, w2, graph, cutoff, save_edge_weights=True):
+        graph.exact()  # edge arrays of the edge count (a graph built with max_edges)
         pos = positions.detach().contiguous()
         x = node_features.detach().contiguous()
         # the per-edge weights R (34 C floats per edge) are kept for the backward when

@@ -301,6 +301,22 @@ int batteries_neighbor_graph_write(const float* positions, const float* box, int
                                    int64_t* row_offsets, int64_t* spatial_order,
                                    hipStream_t stream);
 
+/* batteries_neighbor_graph_write without knowing E on the host: the arrays hold
+ * `capacity` edges (tmp_j, tmp_vec, src, dst, edge_vectors), E stays on the device
+ * (row_offsets[N], or the workspace's offsets), and *overflow (device int) is set to
+ * 1 when E > capacity, in which case every row is left empty (row offsets all 0, so
+ * that no later kernel reads past the arrays), else to 0.  spatial_order as there.
+ * Lets a caller build the graph and launch its kernels with no host
+ * synchronisation.  No counterpart in the reference, whose neighbor list
+ * synchronises twice (neighbor_list.cu:262,363-366). */
+int batteries_neighbor_graph_write_capacity(const float* positions, const float* box, int64_t N,
+                                            float cutoff, int self_loops, void* workspace,
+                                            size_t workspace_bytes, int64_t capacity, int* tmp_j,
+                                            float* tmp_vec, int64_t* src, int64_t* dst,
+                                            float* edge_vectors, int64_t* row_offsets,
+                                            int64_t* spatial_order, int* overflow,
+                                            hipStream_t stream);
+
 /* Phase 2 with int64 indices in the neighbor list's own orientation (same
  * workspace, after phase 1; num_edges = E from phase 1): edge_index [2, E] (row 0 =
  * i, row 1 = j, sorted by (i, j)), edge_vectors [E, 3] = minimum-image pos[j] -

@@ -521,3 +521,57 @@ def test_graph_order_is_a_serpentine_cell_order(bm, dev, n):
     path = row * nb + px                      # serpentine position of each atom's cell
     key = path[order] * n + order             # path position, then atom index
     assert (np.diff(key) > 0).all()
+
+
+def test_graph_with_max_edges_matches_exact_build(bm, dev):
+    """Graph(max_edges=...) builds without a host synchronisation into arrays of max_edges
+    edges: the first E entries, the row pointers, the order and the schedule equal the exact
+    build's, and the fused kernels give bit-identical results."""
+    import batmobile
+    pos, cell = periodic_box(5000, 3)
+    pos = pos.to(dev)
+    ex = batmobile.Graph(pos, cell, 5.0, 64)
+    e = ex.num_edges
+    cap = batmobile.Graph(pos, cell, 5.0, 64, max_edges=e + 1000)
+    assert cap.src.numel() == e + 1000
+    assert cap.num_edges == e
+    cap.check()
+    for a, b in ((cap.src[:e], ex.src), (cap.dst[:e], ex.dst), (cap.vec[:e], ex.vec),
+                 (cap.row_ptr, ex.row_ptr), (cap.order, ex.order), (cap.row_ptr_s, ex.row_ptr_s),
+                 (cap.row_dst, ex.row_dst), (cap.edge_perm[:e], ex.edge_perm)):
+        assert torch.equal(a, b)
+    x = torch.randn(5000, 64, 16, generator=gen(40)).to(dev)
+    assert torch.equal(cap.sh_tp_scatter(x), ex.sh_tp_scatter(x))
+    w = (torch.randn(34, 64, 64, generator=gen(41)) / 8.0).to(dev)
+    assert torch.equal(cap.sh_tp_scatter(x, weights=w), ex.sh_tp_scatter(x, weights=w))
+    assert torch.equal(cap.sh_tp_scatter_index_order(x), ex.sh_tp_scatter_index_order(x))
+    cap.exact()
+    assert cap.src.numel() == e and torch.equal(cap.src, ex.src)
+    # exactly full
+    full = batmobile.Graph(pos, cell, 5.0, 64, max_edges=e)
+    full.check()
+    assert torch.equal(full.sh_tp_scatter(x), ex.sh_tp_scatter(x))
+
+
+@pytest.mark.parametrize("max_edges", [0, 1000, 150000])
+def test_graph_with_too_few_max_edges_flags_and_stays_in_bounds(bm, dev, max_edges):
+    """Edges beyond max_edges: check() raises, every row is empty (row pointers all zero), and
+    the kernels that follow read nothing past the arrays (zero outputs)."""
+    import batmobile
+    pos, cell = periodic_box(5000, 3)   # about 150,480 edges
+    g = batmobile.Graph(pos.to(dev), cell, 5.0, 64, max_edges=max_edges)
+    with pytest.raises(RuntimeError, match="max_edges"):
+        g.check()
+    assert int(g.row_ptr.abs().sum().item()) == 0
+    x = torch.randn(5000, 64, 16, generator=gen(42)).to(dev)
+    assert torch.count_nonzero(g.sh_tp_scatter(x)).item() == 0
+    w = (torch.randn(34, 64, 64, generator=gen(43)) / 8.0).to(dev)
+    assert torch.count_nonzero(g.sh_tp_scatter(x, weights=w)).item() == 0
+
+
+def test_graph_with_max_edges_and_no_atoms(bm, dev):
+    import batmobile
+    g = batmobile.Graph(torch.zeros(0, 3, device=dev), torch.diag(torch.tensor([20.0, 20.0, 20.0])),
+                        5.0, 16, max_edges=10)
+    g.check()
+    assert g.num_edges == 0 and g.row_ptr.cpu().tolist() == [0]
