@@ -40,3 +40,26 @@ def dst_sorted_edges(src_i, dst_j, vec_ij):
     Returns (src, dst, vec) with dst non-decreasing and src ascending per dst.
     """
     return dst_j, src_i, -vec_ij
+
+
+def random_rotation(seed):
+    """A proper rotation matrix (det +1), float64."""
+    q, _ = np.linalg.qr(np.random.default_rng(seed).normal(size=(3, 3)))
+    return q * np.sign(np.linalg.det(q))
+
+
+def wigner_d(rot, lmax=3, n=400, seed=0):
+    """Block-diagonal D(R) with Y(R r) = D Y(r) for the real SH of the oracle, fitted by least
+    squares per l from n random unit vectors (float64; exact to rounding)."""
+    from oracle import sh
+    rng = np.random.default_rng(seed)
+    r = rng.normal(size=(n, 3))
+    r /= np.linalg.norm(r, axis=1, keepdims=True)
+    y0 = sh.spherical_harmonics(r, lmax)
+    y1 = sh.spherical_harmonics(r @ rot.T, lmax)
+    d = np.zeros(((lmax + 1) ** 2, (lmax + 1) ** 2))
+    for l in range(lmax + 1):
+        s = slice(l * l, (l + 1) ** 2)
+        sol, *_ = np.linalg.lstsq(y0[:, s], y1[:, s], rcond=None)
+        d[s, s] = sol.T
+    return d
