@@ -476,6 +476,13 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const float* mh = mrow;
     float4 mr[kLdsAhead + 1];
     const int* th = sTgt;
+    const int* th2 = sTgt;  // the next half's first gather indices
+    // IDX: (gather index, lane offset) pairs, the vaddr pair of an index-mode
+    // load; pair j % 4 serves edge j and is refilled with the index of edge
+    // j + 4 once its load is issued, so that no index is waited for right after
+    // its LDS read
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    v2i_t tgp[4] = {v2i_t{0, voff}, v2i_t{0, voff}, v2i_t{0, voff}, v2i_t{0, voff}};
     int gsrc = 0, lsel = 0;
     uint32_t ends_h = 0;
     int64_t kh = e0;
@@ -486,25 +493,42 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     // waited for at once so that no store is pending where the paths meet
     auto edge = [&](auto jj, auto gather_c) {
         constexpr int j = decltype(jj)::value;
+        // IDX: one wait per pair of edges, at the even one, for both edges'
+        // gather slots, gather indices and the odd edge's operator fragment
+        // (all issued two or more edges earlier): the empty asm takes them as
+        // operands, so the compiler places a single s_waitcnt before it, and
+        // the odd edge needs none
+        if constexpr (IDX && decltype(gather_c)::value && (j & 1) == 0) {
+            constexpr int m1 = (j + 1) % (kLdsAhead + 1);
+            asm volatile("" ::"v"(tgp[j & 3].x), "v"(tgp[(j + 1) & 3].x), "v"(ring[j].x),
+                         "v"(ring[j].y), "v"(ring[j].z), "v"(ring[j].w), "v"(ring[j + 1].x),
+                         "v"(ring[j + 1].y), "v"(ring[j + 1].z), "v"(ring[j + 1].w), "v"(mr[m1].x),
+                         "v"(mr[m1].y), "v"(mr[m1].z), "v"(mr[m1].w));
+            __builtin_amdgcn_sched_barrier(0);
+        }
         mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
             *reinterpret_cast<const float4*>(mh + (j + kLdsAhead) * kMStride);
-        // IDX: the gather's source row, read before the MFMAs that cover its latency
-        int tg = 0;
-        if constexpr (IDX && decltype(gather_c)::value) tg = th[j];
         acc = mfma4(mr[j % (kLdsAhead + 1)], ring[j], acc);
         // the slot's next gather after the MFMAs that read it: hoisted above
         // them it would need a second register ring
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (decltype(gather_c)::value) {
             if constexpr (IDX) {
-                const v4i_t r = struct_buffer_load_b128(xs, tg, voff, 0, 0);
+                const v4i_t r = struct_buffer_load_b128(xs, tgp[j & 3].x, tgp[j & 3].y, 0, 0);
                 ring[j] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
                                       __int_as_float(r.w));
+                // the index of edge j + 4: past the half, the next half's (in
+                // the second half a valid address whose value is not used: the
+                // next batch reloads the pairs after its phase 1)
+                if constexpr (j + 4 < kRing) tgp[j & 3].x = th[j + 4];
+                else tgp[j & 3].x = th2[j + 4 - kRing];
             } else {
                 ring[j] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(gsrc, lsel + j), row_bytes);
             }
         }
-        if ((ends_h >> j) & 1u) {
+        // rare: laid out off the edge path, so that an edge that closes no row
+        // falls through (no taken branch, 54.2 -> 53.0 us at configs[3])
+        if (__builtin_expect((ends_h >> j) & 1u, 0)) {
             const float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
             if (direct == 0) {
                 sStage[w][k_ne - k_out][lane] = v;
@@ -560,6 +584,11 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             constexpr int q = decltype(qq)::value;
             mr[q] = *reinterpret_cast<const float4*>(mrow + q * kMStride);
         });
+        if constexpr (IDX)
+            static_for<4>([&](auto qq) {
+                constexpr int q = decltype(qq)::value;
+                tgp[q].x = sTgt[q + (voff >> 30)];
+            });
         // Phase 2 in two halves of kRing edges, a loop that is not unrolled:
         // each ring slot is then defined once per iteration (by the gather
         // kRing edges ahead) and stays in its registers.  Half h gathers the
@@ -577,6 +606,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             // not known to be uniform, so the address is not rebuilt from a
             // scalar register at every edge
             th = sTgt + jb + (voff >> 30);
+            th2 = sTgt + (h == 0 ? kRing : 0) + (voff >> 30);
             gsrc = h == 0 ? cur.src : nxt.src;
             lsel = h == 0 ? kRing : 0;
             ends_h = (uint32_t)(ends >> jb);
