@@ -1015,11 +1015,116 @@ __global__ void sched_groups_kernel(int64_t n_dst, int P, int Q, int R, int64_t*
     }
 }
 
+// The scan, sched_group_targets_kernel and sched_groups_kernel in one workgroup, for up
+// to kPrepMaxDst destinations, fewer than 2^31 edges and up to kPrepMaxGroups groups:
+// degm (from sched_degm_kernel, which spreads its scattered row_ptr reads over many
+// compute units) is read with coalesced loads into LDS, summed there in int32 (and
+// written out as cum, as the scan would), and the group targets and the clamp read the
+// sums from LDS.  The sums are exact in int32, and
+// the targets compare the same values in double as sched_group_targets_kernel, so gb is
+// the same as the three kernels'.
+constexpr int kPrepThreads = 1024;
+constexpr int kPrepPer = 16;
+constexpr int kPrepMaxDst = kPrepThreads * kPrepPer;
+constexpr int kPrepMaxGroups = 2048;
+__global__ __launch_bounds__(kPrepThreads) void sched_prep_kernel(
+    const int64_t* __restrict__ degm, int64_t n_dst, int P, int Q, int R, int64_t* __restrict__ cum,
+    int64_t* __restrict__ gb) {
+    constexpr int kWaves = kPrepThreads / 64;
+    __shared__ int sCum[kPrepMaxDst + 1];
+    __shared__ int sPos[kPrepMaxGroups];
+    __shared__ int wsum[kWaves];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int n = (int)n_dst;
+    // coalesced: element j * kPrepThreads + t, all loads issued together
+    {
+        int64_t dv[kPrepPer];
+#pragma unroll
+        for (int j = 0; j < kPrepPer; ++j) {
+            const int i = j * kPrepThreads + t;
+            dv[j] = i < n ? degm[i] : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < kPrepPer; ++j) {
+            const int i = j * kPrepThreads + t;
+            if (i < n) sCum[i] = (int)dv[j];
+        }
+    }
+    __syncthreads();
+    // thread t sums its run i0 .. i0 + 15
+    const int i0 = t * kPrepPer;
+    int v[kPrepPer];
+#pragma unroll
+    for (int j = 0; j < kPrepPer; ++j) v[j] = i0 + j < n ? sCum[i0 + j] : 0;
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < kPrepPer; ++j) s += v[j];
+    int x = s;  // inclusive scan of the thread sums within the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();  // also: every thread has read its run before the sums overwrite it
+    int before = 0, total = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+        const int ws = wsum[k];
+        before += k < w ? ws : 0;
+        total += ws;
+    }
+    int run = before + x - s;
+#pragma unroll
+    for (int j = 0; j < kPrepPer; ++j) {
+        if (i0 + j < n) sCum[i0 + j] = run;
+        run += v[j];
+    }
+    if (t == 0) sCum[n] = total;
+    __syncthreads();
+    // the sums to global memory for the balancing kernel (coalesced)
+    for (int i = t; i <= n; i += kPrepThreads) cum[i] = sCum[i];
+    // group ends where the cumulative edge count reaches each group's share
+    const int G = (P + Q - 1) / Q;
+    const double E = (double)total;
+    for (int gi = t; gi < 8 * G; gi += kPrepThreads) {
+        const int xg = gi / G, gen = gi - xg * G;
+        const int Qg = min(Q, P - gen * Q);
+        const int64_t w_end = (int64_t)xg * P + (int64_t)gen * Q + Qg;
+        const double target = E * (double)w_end / (8.0 * (double)P);
+        int lo = 0, hi = n;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((double)sCum[mid] < target) lo = mid + 1;
+            else hi = mid;
+        }
+        if (lo > 0 && target - (double)sCum[lo - 1] < (double)sCum[lo] - target) --lo;
+        sPos[gi] = lo;
+    }
+    __syncthreads();
+    // the clamp, in group order (every group fits its slots and leaves room for the rest)
+    if (t == 0) {
+        const int64_t total_wg = 8LL * P;
+        int64_t start = 0;
+        gb[0] = 0;
+        for (int gi = 0; gi < 8 * G; ++gi) {
+            const int gen = gi % G;
+            const int Qg = min(Q, P - gen * Q);
+            const int64_t w_end = (int64_t)(gi / G) * P + (int64_t)gen * Q + Qg;
+            const int64_t low = max(start, n_dst - (total_wg - w_end) * (int64_t)R);
+            const int64_t high = min(n_dst, start + (int64_t)Qg * R);
+            const int64_t pos = max(low, min(high, (int64_t)sPos[gi]));
+            gb[gi + 1] = pos;
+            start = pos;
+        }
+    }
+}
+
 // One block per group: deal the group's rows to its workgroups' slots.
 __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
     const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
-    const int64_t* __restrict__ gb, int64_t n_dst, int P, int Q, int R,
-    int64_t* __restrict__ row_dst, int64_t* __restrict__ slot_deg) {
+    const int64_t* __restrict__ gb, const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
+    int R, int64_t* __restrict__ row_dst, int64_t* __restrict__ row_ptr_s) {
     __shared__ int64_t sLoad[kSchedMaxQ];
     __shared__ int64_t sA[kScatterRows][kSchedMaxQ];   // degree in (slot, workgroup)
     __shared__ int sPos[kScatterRows][kSchedMaxQ];     // row (offset in the group) or -1
@@ -1033,6 +1138,7 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
     const int64_t s0 = gb[gi], s1 = gb[gi + 1];
     const int n = (int)(s1 - s0);
     const int T = (n + Qg - 1) / Qg;  // <= R: a group holds at most Qg * R rows
+    if (gi == 0 && k == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];  // all the edges
     sLoad[k] = 0;
     for (int t = 0; t < kScatterRows; ++t) {
         sA[t][k] = 0;
@@ -1111,8 +1217,23 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
         }
         __syncthreads();
     }
+    // slot offsets: the group's slots follow the edges of the earlier groups (cum at
+    // the group's first position) in workgroup order, slot order within a workgroup
+    int64_t wl = 0;
+    if (k < Qg)
+        for (int t = 0; t < T; ++t) {
+            const int p = sPos[t][k];
+            if (p >= 0) {
+                const int64_t o = order[s0 + p];
+                if (o >= 0 && o < n_dst) wl += sA[t][k];
+            }
+        }
+    sLoad[k] = wl;
+    __syncthreads();
     if (k < Qg) {
         const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
+        int64_t off = cum[s0];
+        for (int l = 0; l < k; ++l) off += sLoad[l];
         for (int t = 0; t < R; ++t) {
             const int p = t < T ? sPos[t][k] : -1;
             int64_t d = -1, dg = 0;
@@ -1124,7 +1245,8 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
                 }
             }
             row_dst[b * R + t] = d;
-            slot_deg[b * R + t] = dg;
+            row_ptr_s[b * R + t] = off;
+            off += dg;
         }
     }
 }
@@ -1142,8 +1264,8 @@ __global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
 constexpr int kBalWaves = 4;
 __global__ __launch_bounds__(64 * kBalWaves) void sched_balance_wave_kernel(
     const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
-    const int64_t* __restrict__ gb, int64_t n_dst, int P, int Q, int R,
-    int64_t* __restrict__ row_dst, int64_t* __restrict__ slot_deg) {
+    const int64_t* __restrict__ gb, const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
+    int R, int64_t* __restrict__ row_dst, int64_t* __restrict__ row_ptr_s) {
     __shared__ __attribute__((aligned(16))) int sRk[kScatterRows][64];  // row keys per slice
     __shared__ __attribute__((aligned(16))) int sKey[64];               // workgroup load keys
     __shared__ int sPart[kBalWaves][64];      // partial load ranks
@@ -1161,12 +1283,14 @@ __global__ __launch_bounds__(64 * kBalWaves) void sched_balance_wave_kernel(
     const int64_t s0 = gb[gi], s1 = gb[gi + 1];
     const int n = (int)(s1 - s0);
     const int T = (n + Qg - 1) / Qg;  // <= R: a group holds at most Qg * R rows
-    if (n <= 0) {  // no rows: every slot empty
+    if (gi == 0 && threadIdx.x == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];  // all the edges
+    if (n <= 0) {  // no rows: every slot empty, at the group's edge offset
         if (v == 0 && k < Qg) {
             const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
+            const int64_t base = cum[s0];
             for (int t = 0; t < R; ++t) {
                 row_dst[b * R + t] = -1;
-                slot_deg[b * R + t] = 0;
+                row_ptr_s[b * R + t] = base;
             }
         }
         return;
@@ -1306,26 +1430,46 @@ __global__ __launch_bounds__(64 * kBalWaves) void sched_balance_wave_kernel(
             wave_sync();
         }
     }
-    if (v == 0 && k < Qg) {
+    if (v == 0) {
         const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
+        const bool live = k < Qg;
         int64_t od[kScatterRows];  // destinations of the slots, loaded together
         static_for<kScatterRows>([&](auto tt) {
             constexpr int t = decltype(tt)::value;
-            od[t] = order[s0 + (pos[t] >= 0 ? pos[t] : 0)];
+            od[t] = order[s0 + (live && pos[t] >= 0 ? pos[t] : 0)];
         });
+        int64_t dd[kScatterRows];
+        int sd[kScatterRows];
+        int wl = 0;  // edges of workgroup k
         static_for<kScatterRows>([&](auto tt) {
             constexpr int t = decltype(tt)::value;
-            if (t < R) {
-                const int p = t < T ? pos[t] : -1;
-                int64_t d = -1, sd = 0;
-                if (p >= 0 && od[t] >= 0 && od[t] < n_dst) {
-                    d = od[t];
-                    sd = a[t];
-                }
-                row_dst[b * R + t] = d;
-                slot_deg[b * R + t] = sd;
+            const int p = live && t < T ? pos[t] : -1;
+            dd[t] = -1;
+            sd[t] = 0;
+            if (p >= 0 && od[t] >= 0 && od[t] < n_dst) {
+                dd[t] = od[t];
+                sd[t] = a[t];
             }
+            wl += sd[t];
         });
+        // slot offsets: the group's slots follow the edges of the earlier groups (cum at
+        // the group's first position), in workgroup order: an exclusive scan over lanes
+        int xs = wl;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(xs, off, 64);
+            if (k >= off) xs += y;
+        }
+        int64_t off = cum[s0] + (xs - wl);
+        if (live)
+            static_for<kScatterRows>([&](auto tt) {
+                constexpr int t = decltype(tt)::value;
+                if (t < R) {
+                    row_dst[b * R + t] = dd[t];
+                    row_ptr_s[b * R + t] = off;
+                    off += sd[t];
+                }
+            });
     }
 }
 
@@ -1364,12 +1508,12 @@ extern "C" int batteries_mp_schedule_shape(int64_t N_dst, int C, int* n_blocks,
     return BM_OK;
 }
 
-// degm [N_dst], cum [N_dst + 1], group bounds [8 G + 1] (G <= n_blocks / 8),
-// slot degrees [n_blocks * rows_per_block]; N_dst <= n_blocks * rows_per_block.
+// degm [N_dst], cum [N_dst + 1], group bounds [8 G + 1] (G <= n_blocks / 8);
+// N_dst <= n_blocks * rows_per_block.
 extern "C" size_t batteries_mp_schedule_workspace_bytes(int n_blocks, int rows_per_block) {
     if (n_blocks <= 0 || rows_per_block <= 0) return 0;
     const size_t ns = (size_t)n_blocks * (size_t)rows_per_block;
-    return sizeof(int64_t) * (3 * ns + (size_t)n_blocks + 2);
+    return sizeof(int64_t) * (2 * ns + (size_t)n_blocks + 2);
 }
 
 extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_perm,
@@ -1391,22 +1535,25 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
     int64_t* degm = static_cast<int64_t*>(workspace);
     int64_t* cum = degm + N_dst;
     int64_t* gb = cum + N_dst + 1;
-    int64_t* slot_deg = gb + 8 * (int64_t)G + 1;
+    int rc = BM_OK;
     if (N_dst > 0)
         sched_degm_kernel<<<(unsigned)ceil_div(N_dst, B), B, 0, stream>>>(row_ptr, order, degm, N_dst);
-    int rc = batteries_exclusive_scan_i64(degm, cum, N_dst, stream);
-    if (rc != BM_OK) return rc;
-    sched_group_targets_kernel<<<(unsigned)ceil_div(8 * (int64_t)G, 64), 64, 0, stream>>>(cum, N_dst,
-                                                                                         P, Q, gb);
-    sched_groups_kernel<<<1, 64, 0, stream>>>(N_dst, P, Q, rows_per_block, gb);
+    if (N_dst <= kPrepMaxDst && N_edges < INT32_MAX && 8 * (int64_t)G <= kPrepMaxGroups) {
+        sched_prep_kernel<<<1, kPrepThreads, 0, stream>>>(degm, N_dst, P, Q, rows_per_block, cum,
+                                                          gb);
+    } else {
+        rc = batteries_exclusive_scan_i64(degm, cum, N_dst, stream);
+        if (rc != BM_OK) return rc;
+        sched_group_targets_kernel<<<(unsigned)ceil_div(8 * (int64_t)G, 64), 64, 0, stream>>>(
+            cum, N_dst, P, Q, gb);
+        sched_groups_kernel<<<1, 64, 0, stream>>>(N_dst, P, Q, rows_per_block, gb);
+    }
     if (Q <= 64 && N_edges < ((int64_t)1 << 25))
         sched_balance_wave_kernel<<<(unsigned)(8 * G), 64 * kBalWaves, 0, stream>>>(
-            degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
+            degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst, row_ptr_s);
     else
         sched_balance_kernel<<<(unsigned)(8 * G), kSchedMaxQ, 0, stream>>>(
-            degm, order, gb, N_dst, P, Q, rows_per_block, row_dst, slot_deg);
-    rc = batteries_exclusive_scan_i64(slot_deg, row_ptr_s, n_sched, stream);
-    if (rc != BM_OK) return rc;
+            degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst, row_ptr_s);
     sched_edges_kernel<<<(unsigned)ceil_div(n_sched, 4), 256, 0, stream>>>(row_ptr, col_perm, row_dst,
                                                                           row_ptr_s, edge_perm, n_sched);
     return (int)hipGetLastError();

@@ -441,6 +441,100 @@ def test_schedule_with_skewed_degrees(bm, dev, c):
     assert torch.equal(torch.sort(rdst[rdst >= 0].cpu()).values, torch.arange(n))
 
 
+def _schedule_groups_expected(deg, P, Q, R):
+    """Group bounds of the spatial schedule from the degrees in processing order: each
+    group ends where the cumulative edge count reaches its share of the edges (or one
+    position earlier when that is closer), then the ends are clamped in order so that
+    every group fits its Qg * R slots and leaves room for the groups after it."""
+    n = len(deg)
+    cum = np.concatenate([[0], np.cumsum(deg, dtype=np.int64)])
+    G = (P + Q - 1) // Q
+    gb = np.zeros(8 * G + 1, dtype=np.int64)
+    start = 0
+    for gi in range(8 * G):
+        x, gen_ = divmod(gi, G)
+        qg = min(Q, P - gen_ * Q)
+        w_end = x * P + gen_ * Q + qg
+        target = float(cum[n]) * float(w_end) / (8.0 * float(P))
+        lo = int(np.searchsorted(cum[:n].astype(np.float64), target, side="left"))
+        if lo > 0 and target - float(cum[lo - 1]) < float(cum[lo]) - target:
+            lo -= 1
+        low = max(start, n - (8 * P - w_end) * R)
+        high = min(n, start + qg * R)
+        gb[gi + 1] = max(low, min(high, lo))
+        start = int(gb[gi + 1])
+    return gb
+
+
+@pytest.mark.parametrize("case", ["box5000", "box16384", "box16385", "box20000", "skewed", "empty"])
+def test_schedule_groups_through_c_abi(bm, dev, case):
+    """batteries_mp_schedule's processing-order degrees, their running sums and the group
+    bounds (read from its workspace: degm [N], cum [N + 1], gb [8 G + 1]) against a numpy
+    restatement, and its slot offsets against the running sums of the slot degrees, on both
+    sides of the one-workgroup preparation's limit of 16,384 destinations."""
+    import batmobile
+    c = 64
+    if case.startswith("box"):
+        n = int(case[3:])
+        pos, cell = periodic_box(n, 5 + n % 97)
+        g = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+        row_ptr, order, e = g.row_ptr, g.order, g.num_edges
+    elif case == "skewed":
+        n = 3000
+        dst = torch.cat([torch.zeros(900, dtype=torch.int64), torch.arange(1, 600),
+                         torch.randint(600, 2000, (40000,), generator=gen(71))])
+        src = torch.randint(0, n, (dst.numel(),), generator=gen(72))
+        row_ptr, _ = bm.edge_index_to_csr(torch.stack([src, dst]).to(dev), n)
+        order = torch.randperm(n, generator=gen(73)).to(dev)
+        e = dst.numel()
+    else:
+        n, e = 0, 0
+        row_ptr = torch.zeros(1, dtype=torch.int64, device=dev)
+        order = torch.zeros(1, dtype=torch.int64, device=dev)
+    lib = ctypes.CDLL(LIB)
+    nb, rpb = ctypes.c_int(), ctypes.c_int()
+    assert lib.batteries_mp_schedule_shape(ctypes.c_int64(n), ctypes.c_int(c), ctypes.byref(nb),
+                                           ctypes.byref(rpb)) == 0
+    nb, rpb = nb.value, rpb.value
+    lib.batteries_mp_schedule_workspace_bytes.restype = ctypes.c_size_t
+    wsb = lib.batteries_mp_schedule_workspace_bytes(ctypes.c_int(nb), ctypes.c_int(rpb))
+    ws = torch.full((wsb // 8,), -7, dtype=torch.int64, device=dev)
+    ns = nb * rpb
+    rps = torch.empty(ns + 1, dtype=torch.int64, device=dev)
+    rdst = torch.empty(ns, dtype=torch.int64, device=dev)
+    ep = torch.empty(max(e, 1), dtype=torch.int64, device=dev)
+    P = nb // 8
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Q = min(P, max(1, 2 * cus // ((c + 63) // 64) // 8), 256)
+    G = (P + Q - 1) // Q
+    stream = torch.cuda.current_stream().cuda_stream
+    lib.batteries_mp_schedule.restype = ctypes.c_int
+    rc = lib.batteries_mp_schedule(
+        ctypes.c_void_p(row_ptr.data_ptr()), None, ctypes.c_void_p(order.data_ptr()),
+        ctypes.c_int64(n), ctypes.c_int64(e), ctypes.c_int(c), ctypes.c_int(nb), ctypes.c_int(rpb),
+        ctypes.c_void_p(rps.data_ptr()), ctypes.c_void_p(rdst.data_ptr()),
+        ctypes.c_void_p(ep.data_ptr()), ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(wsb),
+        ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    assert rc == 0
+    w = ws.cpu().numpy()
+    rp = row_ptr.cpu().numpy()
+    od = order.cpu().numpy()[:n]
+    deg = (rp[1:] - rp[:-1])[od] if n else np.zeros(0, dtype=np.int64)
+    assert np.array_equal(w[:n], deg)
+    assert np.array_equal(w[n:2 * n + 1], np.concatenate([[0], np.cumsum(deg)]))
+    gb = w[2 * n + 1: 2 * n + 1 + 8 * G + 1]
+    assert np.array_equal(gb, _schedule_groups_expected(deg, P, Q, rpb))
+    # and the schedule built on them covers every destination once, its slot offsets
+    # the running sums of the scheduled rows' degrees
+    r = rdst.cpu()
+    assert torch.equal(torch.sort(r[r >= 0]).values, torch.arange(n))
+    slot_deg = torch.zeros(ns, dtype=torch.int64)
+    slot_deg[r >= 0] = torch.from_numpy(rp[1:] - rp[:-1])[r[r >= 0]]
+    assert torch.equal(rps.cpu(), torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(slot_deg, 0)]))
+    assert int(rps[-1]) == e
+
+
 def test_schedule_with_col_perm_matches_fused_message_passing_simple(bm, dev):
     n, e, c = 900, 20000, 32
     vec, x, src, dst = _random_graph(n, e, c, 51)
