@@ -107,6 +107,34 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(const float* __res
     lds_to_block<K, KS>(sy, Y + base * K, rows, vec4);
 }
 
+// Small inputs (at most kShDirectRows rows, one round of workgroups): each lane its own
+// vector and row straight from global memory, no LDS and no barriers (with a single
+// round there is no other workgroup to cover the staged kernel's barriers).
+constexpr int64_t kShDirectRows = 65536;
+template <int L, bool NORM>
+__global__ __launch_bounds__(kShBlock) void sh_forward_direct_kernel(const float* __restrict__ v,
+                                                                       float* __restrict__ Y,
+                                                                       int64_t n, bool vec4) {
+    constexpr int K = sh_dim(L);
+    const int64_t r = (int64_t)blockIdx.x * kShBlock + threadIdx.x;
+    if (r >= n) return;
+    float x = v[r * 3 + 0], y = v[r * 3 + 1], z = v[r * 3 + 2];
+    if constexpr (NORM) normalize3(x, y, z);
+    float out[K];
+    sh_forward<L>(x, y, z, out);
+    if constexpr (K % 4 == 0) {
+        if (vec4) {
+            float4* y4 = reinterpret_cast<float4*>(Y + r * K);
+#pragma unroll
+            for (int q = 0; q < K / 4; ++q)
+                y4[q] = make_float4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+            return;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) Y[r * K + k] = out[k];
+}
+
 // grad_xyz = sum_k g_k dY_k/d(x,y,z).  With NORM the input is the raw vector v,
 // Y is taken at u = v/|v| and the result is chained through the normalisation:
 // (g_u - u (u . g_u)) / |v|   (reference python/batmobile/autograd.py:62-92).
@@ -163,6 +191,19 @@ template <bool NORM>
 static int launch_sh_forward(const float* v, float* Y, int64_t n, int L, hipStream_t s) {
     const dim3 grid((unsigned)ceil_div(n, kShBlock));
     const bool vec4 = al16(v) && al16(Y);
+    if (n <= kShDirectRows) {
+        switch (L) {
+            case 0: sh_forward_direct_kernel<0, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            case 1: sh_forward_direct_kernel<1, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            case 2: sh_forward_direct_kernel<2, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            case 3: sh_forward_direct_kernel<3, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            case 4: sh_forward_direct_kernel<4, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            case 5: sh_forward_direct_kernel<5, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            case 6: sh_forward_direct_kernel<6, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
+            default: return BM_ERR_ARG;
+        }
+        return (int)hipGetLastError();
+    }
     switch (L) {
         case 0: sh_forward_kernel<0, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;
         case 1: sh_forward_kernel<1, NORM><<<grid, kShBlock, 0, s>>>(v, Y, n, vec4); break;

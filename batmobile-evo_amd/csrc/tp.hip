@@ -130,6 +130,54 @@ __global__ __launch_bounds__(kTpBlock) void tp_simple_kernel(const float* __rest
     store_rows16(sb, out, base, rows);
 }
 
+// Small inputs (at most kTpDirectRows rows: one round of at most 256 workgroups): each
+// lane its own rows straight from global memory, the next row's loads issued before
+// this row's products, no LDS and no barriers.  With a single round there is no other
+// workgroup to cover the LDS kernel's barriers: 3.7 us against 4.35 us at configs[0]
+// (20,000 rows).  From about 10^5 rows up the coalesced LDS-staged kernel above is
+// faster (31.7 us against 34.4 us at 10^6: lanes reading 64-byte rows 64 bytes apart
+// use the memory pipeline less well).
+constexpr int64_t kTpDirectRows = 65536;
+__global__ __launch_bounds__(kTpBlock) void tp_simple_direct_kernel(const float* __restrict__ x,
+                                                                    const float* __restrict__ y,
+                                                                    float* __restrict__ out,
+                                                                    int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kTpBlock;
+    int64_t r = (int64_t)blockIdx.x * kTpBlock + threadIdx.x;
+    if (r >= n) return;
+    float4 ux[4], uy[4];
+    auto ld = [&](int64_t row) {
+        const float4* x4 = reinterpret_cast<const float4*>(x + row * 16);
+        const float4* y4 = reinterpret_cast<const float4*>(y + row * 16);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            ux[k] = x4[k];
+            uy[k] = y4[k];
+        }
+    };
+    ld(r);
+    for (; r < n; r += stride) {
+        float a[16], b[16], o[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a[4 * k] = ux[k].x;
+            a[4 * k + 1] = ux[k].y;
+            a[4 * k + 2] = ux[k].z;
+            a[4 * k + 3] = ux[k].w;
+            b[4 * k] = uy[k].x;
+            b[4 * k + 1] = uy[k].y;
+            b[4 * k + 2] = uy[k].z;
+            b[4 * k + 3] = uy[k].w;
+        }
+        ld(r + stride < n ? r + stride : r);  // the last row re-reads itself (in bounds)
+        tp_simple_rows(a, b, o);
+        float4* o4 = reinterpret_cast<float4*>(out + r * 16);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            o4[k] = make_float4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+    }
+}
+
 __global__ __launch_bounds__(kTpBlock) void tp_simple_backward_kernel(
     const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ g,
     float* __restrict__ gx, float* __restrict__ gy, int64_t n) {
@@ -969,8 +1017,12 @@ extern "C" int batteries_tensor_product_simple_l3(const float* input1, const flo
     if (N < 0) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
     if (!aligned16(input1) || !aligned16(input2) || !aligned16(output)) return BM_ERR_ARG;
-    tp_simple_kernel<<<(unsigned)ceil_div(N, kTpBlock), kTpBlock, 0, stream>>>(input1, input2,
-                                                                              output, N);
+    if (N <= kTpDirectRows)
+        tp_simple_direct_kernel<<<(unsigned)ceil_div(N, kTpBlock), kTpBlock, 0, stream>>>(
+            input1, input2, output, N);
+    else
+        tp_simple_kernel<<<(unsigned)ceil_div(N, kTpBlock), kTpBlock, 0, stream>>>(input1, input2,
+                                                                                  output, N);
     return (int)hipGetLastError();
 }
 

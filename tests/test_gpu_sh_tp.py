@@ -100,7 +100,7 @@ def test_sh_normalized_backward(bm, dev, lmax):
     assert normwise_err(got, want) <= 1e-4
 
 
-@pytest.mark.parametrize("n", [1, 257, 20000])
+@pytest.mark.parametrize("n", [1, 257, 20000, 65536, 65537, 100003])
 def test_tp_simple_forward(bm, dev, n):
     # configs[0] workload at n = 20000: Y of unit Gaussian vectors, x ~ N(0,1)
     v = unit_vectors(n, 0)
@@ -110,6 +110,20 @@ def test_tp_simple_forward(bm, dev, n):
     want = otp.tensor_product_simple(x.cpu().double().numpy(), y.cpu().double().numpy())
     assert normwise_err(out, want) <= 1e-5
     np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
+
+
+def test_tp_simple_small_and_large_kernels_agree(bm, dev):
+    """Up to 65,536 rows the product runs one row per lane from global memory, above that
+    through LDS-staged coalesced rows: the same rows give the same bits either way."""
+    n = 65537
+    v = unit_vectors(n, 5)
+    y = bm.spherical_harmonics(v.to(dev), 3)
+    x = torch.randn(n, 16, generator=gen(11)).to(dev)
+    big = bm.tensor_product_simple(x, y)
+    small = bm.tensor_product_simple(x[:n - 1].contiguous(), y[:n - 1].contiguous())
+    assert torch.equal(big[:n - 1], small)
+    last = bm.tensor_product_simple(x[n - 1:].contiguous(), y[n - 1:].contiguous())
+    assert torch.equal(big[n - 1:], last)
 
 
 def test_tp_simple_backward(bm, dev):
