@@ -11,7 +11,7 @@ Workload (one "step" = one pass of the hot path over the whole system):
   (batmobile.sh_tp_scatter: one kernel, inputs resident in HBM).
 
 Prints ONE JSON line (rank 0).  value = edges/s over the timed region.
-`roofline` uses the survey's algorithmic byte count for this path,
+`roofline` uses the algorithmic byte count of this path,
   B = E * (12 + 8 + 64 C) + N * (64 C + 8)
 (edge vector, source index, gathered source row; output row and row pointer),
 divided by the kernel's average duration from HIP events on the launch stream;
@@ -138,8 +138,9 @@ def event_ms(torch, fn, reps, settle_s=0.03):
 
 
 def other_configs(torch, bm, dev):
-    """configs[0..2] of the survey, timed on this GPU (parity cases; reported beside the
-    headline).  Inputs as the survey states (seeds 0, 1, 2); algorithmic work per unit:
+    """configs[0..2] of the benchmark configurations, timed on this GPU (parity cases;
+    reported beside the headline).  Inputs as those configurations state (seeds 0, 1, 2);
+    algorithmic work per unit:
     SH 76 B/edge, TP simple 192 B/row, weighted TP fwd E(312 Ci Co + 1222 Ci) flop,
     weighted TP bwd E(624 Ci Co + 3666 Ci) flop."""
     res = {}
@@ -212,14 +213,15 @@ def weighted_config3(torch, bm, dev, w, wt, reps=200, settle=SETTLE_STEPS // 2):
     kernel (mp_weighted_fused_kernel), HIP events on the launch stream.
     Flop models: the one this kernel executes, E (512 C) + N (1222 C + 312 C^2) (edge sums
     of X Y^T on MFMA, CG contraction and per-path mixing once per destination), which the
-    roofline uses; and the survey's E (1222 C) + N (312 C^2), reported beside it.
+    roofline uses; and E (1222 C) + N (312 C^2) (the CG contraction per edge, the mixing per
+    destination, no edge sums), reported beside it.
     Compulsory bytes: edge vector, source index, X row once, W, output row, row pointer."""
     graph, x = w["graph"], w["x"]
     for _ in range(settle):     # clock settle under this kernel's own load
         out = graph.sh_tp_scatter(x, weights=wt)
     t = event_ms(torch, lambda: graph.sh_tp_scatter(x, weights=wt), reps)
     e, n, c = graph.num_edges, N_ATOMS, CHANNELS
-    f_survey = e * 1222 * c + n * 312 * c * c
+    f_cg_edge = e * 1222 * c + n * 312 * c * c
     f_exec = e * 512 * c + n * (1222 * c + 312 * c * c)
     b_comp = e * (12 + 8) + n * (64 * c + 64 * c + 8) + 34 * c * c * 4
     tf = f_exec / (t * 1e-3) / 1e12
@@ -241,8 +243,8 @@ def weighted_config3(torch, bm, dev, w, wt, reps=200, settle=SETTLE_STEPS // 2):
             "frac": tf / MFMA_FP32_PEAK_TFLOPS, "traffic": traffic,
             "flop_model": "executed: E*512*C + N*(1222*C + 312*C^2)",
             "flops_per_launch": f_exec,
-            "survey_model_flops_per_launch": f_survey,
-            "survey_model_TFLOPs": f_survey / (t * 1e-3) / 1e12,
+            "cg_per_edge_model_flops_per_launch": f_cg_edge,
+            "cg_per_edge_model_TFLOPs": f_cg_edge / (t * 1e-3) / 1e12,
             "traffic_source": note,
         },
         "roofline_hbm": {
@@ -564,7 +566,7 @@ def main():
             "traffic_source": traffic_note,
         },
         # HBM side: the fraction is of the measured traffic (rocprofv3 counters), the
-        # bytes that actually cross HBM.  The survey's algorithmic byte count charges
+        # bytes that actually cross HBM.  The algorithmic byte count charges
         # every gathered source row to HBM although L2 serves most of them; its rate is
         # reported as an effective rate, not as a roofline fraction.
         "roofline_hbm": {
