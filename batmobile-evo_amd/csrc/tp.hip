@@ -787,17 +787,19 @@ __device__ __forceinline__ void bwd_w_group(const float* __restrict__ x, const f
             const int co = co0 + i16;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                // rows past the segment must not count; co >= cout is a discarded column
+                // rows past the segment meet T = 0 (below); co >= cout is a discarded column
                 const int64_t rw = rc + 4 * r + g4;
-                load16_mask(g, (min<int64_t>(rw, n - 1) * cout + min(co, cout - 1)) * 16, rw < r1,
-                            gv[r]);
+                load16(g, (min<int64_t>(rw, n - 1) * cout + min(co, cout - 1)) * 16, gv[r]);
             }
         }
         __syncthreads();
         {
             float xa[16], yb[16], t[NS];
-            // T rows past the segment meet g = 0; channels >= cin are discarded rows
-            load16(x, (min<int64_t>(rc + t_row, n - 1) * cin + min(t_ci, cin - 1)) * 16, xa);
+            // rows past the segment must not count: their T is zero (x masked: 16 selects
+            // per thread, against 64 for masking the thread's g values); channels >= cin
+            // are discarded rows
+            load16_mask(x, (min<int64_t>(rc + t_row, n - 1) * cin + min(t_ci, cin - 1)) * 16,
+                        rc + t_row < r1, xa);
 #pragma unroll
             for (int k = 0; k < 16; ++k) yb[k] = sY[t_row * 16 + k];
 #pragma unroll
