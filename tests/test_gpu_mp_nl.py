@@ -548,6 +548,46 @@ def test_schedule_with_col_perm_matches_fused_message_passing_simple(bm, dev):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_scheduled_scatter_random_degree_patterns(bm, dev, seed):
+    """Random graphs whose row lengths mix empty rows, one-edge rows, rows around the
+    32- and 64-edge boundaries and long rows, in random orders: the scheduled kernel
+    (gather indices read ahead across halves and batches) equals the index-order kernel
+    bit for bit, and the oracle within 1e-5 on every fourth case."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    n = int(torch.randint(1, 600, (1,), generator=g))
+    c = [16, 64, 24, 80][seed % 4]
+    kind = torch.randint(0, 6, (n,), generator=g)
+    deg = torch.where(kind == 0, torch.zeros(n, dtype=torch.int64),
+          torch.where(kind == 1, torch.ones(n, dtype=torch.int64),
+          torch.where(kind == 2, torch.randint(28, 37, (n,), generator=g),
+          torch.where(kind == 3, torch.randint(60, 69, (n,), generator=g),
+          torch.where(kind == 4, torch.randint(2, 20, (n,), generator=g),
+                      torch.randint(100, 300, (n,), generator=g))))))
+    if seed % 3 == 0:
+        deg[torch.rand(n, generator=g) < 0.5] = 0        # long runs of empty rows
+    dst = torch.repeat_interleave(torch.arange(n), deg)
+    e = int(dst.numel())
+    src = torch.randint(0, n, (e,), generator=g)
+    perm = torch.randperm(e, generator=g)                # edges in random order
+    src, dst = src[perm], dst[perm]
+    vec = unit_vectors(e, 2000 + seed) * (0.5 + torch.rand(e, 1, generator=g)) if e else torch.zeros(0, 3)
+    x = torch.randn(n, c, 16, generator=g)
+    ei = torch.stack([src, dst]).to(dev)
+    rp, ci = bm.edge_index_to_csr(ei, n)
+    order = torch.randperm(n, generator=g).to(dev)
+    rps, ep, rdst, nb, rpb = bm.mp_schedule(rp, order, c, ci)
+    out = bm.sh_tp_scatter_scheduled(vec.to(dev), x.to(dev), ei[0].contiguous(), rps, ep, rdst, nb, rpb,
+                                     n, True)
+    idx = bm.sh_tp_scatter(vec.to(dev), x.to(dev), ei[0].contiguous(), rp, ci, True)
+    assert torch.equal(out, idx)
+    assert out[deg.to(dev) == 0].abs().sum().item() == 0.0
+    if seed % 4 == 0 and e:
+        want = omp.sh_tp_scatter(vec.double().numpy(), x.double().numpy(), src.numpy(), dst.numpy(), n,
+                                 normalize=True)
+        assert normwise_err(out.cpu(), want) <= 1e-5
+
+
 def test_scatter_batch_boundaries(bm, dev):
     """Index order with 11 destinations per workgroup (n = 512 * 11, C = 16) and
     degree patterns that put row ends on both sides of the 32- and 64-edge
