@@ -88,6 +88,36 @@ def test_weighted_scatter_empty_rows_long_rows_and_no_edges(bm, dev):
     assert z.shape == (0, co, 16)
 
 
+@pytest.mark.parametrize("ci,co", [(32, 64), (20, 70)])
+def test_weighted_scatter_step_and_segment_boundaries(bm, dev, ci, co):
+    """Destinations whose edge counts sit on both sides of the kernel's boundaries: the
+    4-edge k-steps (padded to an even number), the 12-step (48-edge) staging segments,
+    and several segments; in a shuffled processing order, against the oracle, and the
+    same bits as with the edges stored in CSR order."""
+    degs = [0, 1, 2, 3, 4, 5, 7, 8, 9, 47, 48, 49, 52, 95, 96, 97, 100, 143, 144, 145]
+    n = len(degs)
+    dst = torch.repeat_interleave(torch.arange(n), torch.tensor(degs))
+    e = dst.numel()
+    perm = torch.randperm(e, generator=gen(80))
+    dst = dst[perm]
+    src = torch.randint(0, n, (e,), generator=gen(81))
+    vec = unit_vectors(e, 82) * (0.5 + torch.rand(e, 1, generator=gen(83)))
+    x = torch.randn(n, ci, 16, generator=gen(84))
+    w = _weights(ci, co, 85)
+    order, rp = _csr(dst, n)
+    shuffle = torch.randperm(n, generator=gen(86))
+    out = bm.sh_tp_scatter_weighted(vec.to(dev), x.to(dev), w.to(dev), src.to(dev), rp.to(dev),
+                                    order.to(dev), shuffle.to(dev), True)
+    want = omp.weighted_message_passing(vec.double().numpy(), x.double().numpy(),
+                                        w.double().numpy(), src.numpy(), dst.numpy(), n,
+                                        normalize=True)
+    assert normwise_err(out.cpu(), want) <= 1e-5
+    assert torch.count_nonzero(out[0]).item() == 0
+    out2 = bm.sh_tp_scatter_weighted(vec[order].to(dev), x.to(dev), w.to(dev), src[order].to(dev),
+                                     rp.to(dev), None, None, True)
+    assert torch.equal(out, out2)
+
+
 def test_weighted_scatter_matches_reference_composition_on_gpu(bm, dev):
     """SH -> tensor_product(X[src], Y, W) -> index_add_, the reference's own calls, on this GPU."""
     n, e, c = 300, 5000, 32
