@@ -254,8 +254,6 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> tensor_product_backward(
     TORCH_CHECK(input1.dtype() == torch::kFloat32 && input2.dtype() == torch::kFloat32 &&
                     weights.dtype() == torch::kFloat32 && grad_output.dtype() == torch::kFloat32,
                 "inputs must be float32");
-    TORCH_CHECK(C_in <= 1023 || C_out <= 128,
-                "tensor_product_backward: C_in must be <= 1023 when C_out > 128");
     auto opt = f32_like(input1);
     torch::Tensor g1, g2, gW;
     if (needs_input1_grad) g1 = torch::empty({N, C_in, 16}, opt);
@@ -648,10 +646,11 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
                      ws.data_ptr(), wsb, E, tmp_j.data_ptr<int>(), tmp_vec.data_ptr<float>(),
                      edge_index.data_ptr<int64_t>(), vec.data_ptr<float>(), nullptr, s),
                  "neighbor_list");
-    // the row offsets read in place from the workspace (a view that keeps it alive)
+    // the row offsets copied out of the workspace, so the result owns its own [N+1]
+    // tensor (neighbor_graph, below, keeps the zero-copy view for batmobile.Graph)
     const size_t at = batteries_neighbor_list_offsets_at(N, box, rc);
     TORCH_CHECK(at > 0 && at % 8 == 0, "neighbor_list: workspace layout");
-    torch::Tensor offsets = ws.narrow(0, (int64_t)(at / 8), N + 1);
+    torch::Tensor offsets = ws.narrow(0, (int64_t)(at / 8), N + 1).clone();
     return {edge_index, vec, offsets};
 }
 

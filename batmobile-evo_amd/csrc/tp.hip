@@ -867,11 +867,14 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_bwd_w_mfma_kernel(
 
 // grad_x and grad_y for C_out above the LDS tile of the MFMA kernel (128):
 // h[n,ci,q] = sum_co W[path(q),ci,co] g[n,co,out(q)], gx = CG^T(h, y),
-// gy = sum_ci CG^T(h, x).  One thread per (row, ci); per-ci gy partials are
+// gy = sum_ci CG^T(h, x).  One thread per (row, ci); the per-ci gy partials are
 // reduced in a fixed order.
-// STAGE_G: the rows' g is staged in LDS (kBRows rows per workgroup); otherwise
-// (C_out too large for that) one row per workgroup reads g from memory, where
-// the row's C_out x 64 bytes stay in cache for the workgroup's threads.
+// STAGE_G: the rows' g is staged in LDS (kBRows rows per workgroup) beside every
+// (row, ci) partial of gy.  Otherwise (C_out or C_in too large for that) one row
+// per workgroup reads g from memory, where the row's C_out x 64 bytes stay in
+// cache for the workgroup's threads; thread t sums the partials of its channels
+// t, t + 256, ... in registers, and the 256 sums meet in LDS (16 KB whatever
+// C_in is), so neither C_in nor C_out is bounded.
 constexpr int kBRows = 2;
 template <bool STAGE_G>
 __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
@@ -880,8 +883,10 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
     int cout) {
     constexpr int kRows = STAGE_G ? kBRows : 1;
     extern __shared__ float smem[];
-    float* sgy = smem;                         // [kRows][cin][16]
-    float* sy = sgy + kRows * cin * 16;        // [kRows][16]
+    // gy partials: [kRows][cin][16] when STAGE_G, else [kTpBlock][16]
+    const int npart = STAGE_G ? kRows * cin : kTpBlock;
+    float* sgy = smem;
+    float* sy = sgy + npart * 16;              // [kRows][16]
     float* sg = sy + kRows * 16;               // [kRows][cout][16] when STAGE_G
     const int64_t row0 = (int64_t)blockIdx.x * kRows;
     const int rows = (int)min<int64_t>(kRows, n - row0);
@@ -890,6 +895,9 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
         for (int i = tid; i < rows * cout * 16; i += kTpBlock) sg[i] = g[row0 * cout * 16 + i];
     for (int i = tid; i < rows * 16; i += kTpBlock) sy[i] = y[row0 * 16 + i];
     __syncthreads();
+    float gyacc[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gyacc[k] = 0.0f;
     for (int it = tid; it < rows * cin; it += kTpBlock) {
         const int r = it / cin, ci = it - r * cin;
         float h[kNumSlots];
@@ -927,16 +935,41 @@ __global__ __launch_bounds__(kTpBlock) void tp_weighted_backward_xy_kernel(
 #pragma unroll
             for (int k = 0; k < 16; ++k) o[k] = ga[k];
         }
+        if constexpr (STAGE_G) {
 #pragma unroll
-        for (int k = 0; k < 16; ++k) sgy[(r * cin + ci) * 16 + k] = gb[k];
+            for (int k = 0; k < 16; ++k) sgy[(r * cin + ci) * 16 + k] = gb[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) gyacc[k] += gb[k];
+        }
+    }
+    if constexpr (!STAGE_G) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) sgy[tid * 16 + k] = gyacc[k];
     }
     __syncthreads();
-    if (gy) {
+    if (!gy) return;
+    if constexpr (STAGE_G) {
         for (int i = tid; i < rows * 16; i += kTpBlock) {
             const int r = i >> 4, k = i & 15;
             float s = 0.0f;
             for (int ci = 0; ci < cin; ++ci) s += sgy[(r * cin + ci) * 16 + k];
             gy[(row0 + r) * 16 + k] = s;
+        }
+    } else {
+        // 16 groups of 16 partials per component, then the 16 group sums, in order
+        const int k = tid & 15, grp = tid >> 4;
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += sgy[(grp * 16 + j) * 16 + k];
+        __syncthreads();
+        sgy[grp * 16 + k] = s;
+        __syncthreads();
+        if (tid < 16) {
+            float t = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t += sgy[j * 16 + tid];
+            gy[row0 * 16 + tid] = t;
         }
     }
 }
@@ -1043,23 +1076,33 @@ extern "C" int batteries_tensor_product_simple_backward_l3(const float* input1,
     return (int)hipGetLastError();
 }
 
+// Rows per launch of the weighted forward: keeps grid.x * blockDim.x (at most
+// 512 work-items per 16-row tile and group) below 2^32 - 1, the dispatch limit;
+// larger N runs as consecutive launches over row ranges.
+constexpr int64_t kFwdMaxRowsPerLaunch = int64_t(1) << 24;
+
 extern "C" int batteries_tensor_product_l3(const float* input1, const float* input2,
                                            const float* weights, float* output, int64_t N,
                                            int C_in, int C_out, hipStream_t stream) {
     if (N < 0 || C_in <= 0 || C_out <= 0) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
-    const int64_t ntile = ceil_div(N, kTile);
-    if (ceil_div(ntile, 8) * 8 * kFwdGroups > INT32_MAX || ceil_div(C_out, 64) > 65535)
-        return BM_ERR_ARG;
+    if (ceil_div(C_out, 64) > 65535) return BM_ERR_ARG;
     if ((int64_t)kNumPaths * C_in * C_out * 4 > INT32_MAX) return BM_ERR_ARG;  // W via 32-bit offsets
     if ((reinterpret_cast<uintptr_t>(input1) | reinterpret_cast<uintptr_t>(output)) & 15)
         return BM_ERR_ARG;
-    // (row tile, group) pairs: tiles rounded up to 8, four groups each
-    dim3 grid((unsigned)(ceil_div(ntile, 8) * 8 * kFwdGroups), (unsigned)ceil_div(C_out, 64), 1);
     const int halves = C_in > 16 ? 2 : 1;  // input-channel chunks split over two wave halves
-    tp_weighted_fwd_mfma_kernel<<<grid, halves * kTpBlock, 0, stream>>>(
-        input1, input2, weights, output, N, C_in, C_out, (int)ntile);
-    return (int)hipGetLastError();
+    for (int64_t r0 = 0; r0 < N; r0 += kFwdMaxRowsPerLaunch) {
+        const int64_t rows = std::min(kFwdMaxRowsPerLaunch, N - r0);
+        const int64_t ntile = ceil_div(rows, kTile);
+        // (row tile, group) pairs: tiles rounded up to 8, four groups each
+        dim3 grid((unsigned)(ceil_div(ntile, 8) * 8 * kFwdGroups), (unsigned)ceil_div(C_out, 64), 1);
+        tp_weighted_fwd_mfma_kernel<<<grid, halves * kTpBlock, 0, stream>>>(
+            input1 + r0 * C_in * 16, input2 + r0 * 16, weights, output + r0 * C_out * 16, rows,
+            C_in, C_out, (int)ntile);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+    }
+    return BM_OK;
 }
 
 // Workspace of the weighted backward: grad_W partials of the row segments
@@ -1110,14 +1153,14 @@ static int tp_backward_run(const float* input1, const float* input2, const float
             // above that one row per workgroup with g read from memory (no bound on C_out)
             const size_t staged = sizeof(float) * ((size_t)kBRows * C_out * 16 +
                                                    (size_t)kBRows * C_in * 16 + kBRows * 16);
-            const size_t unstaged = sizeof(float) * ((size_t)C_in * 16 + 16);
+            const size_t unstaged = sizeof(float) * ((size_t)kTpBlock * 16 + 16);
             if (staged <= 64 * 1024) {
                 tp_weighted_backward_xy_kernel<true>
                     <<<(unsigned)ceil_div(N, kBRows), kTpBlock, staged, stream>>>(
                         input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in,
                         C_out);
             } else {
-                if (unstaged > 64 * 1024 || N > INT32_MAX) return BM_ERR_ARG;  // C_in > 1023
+                if (N > UINT32_MAX) return BM_ERR_ARG;  // one row per workgroup
                 tp_weighted_backward_xy_kernel<false><<<(unsigned)N, kTpBlock, unstaged, stream>>>(
                     input1, input2, weights, grad_output, grad_input1, grad_input2, N, C_in, C_out);
             }

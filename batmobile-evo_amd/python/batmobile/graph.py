@@ -20,6 +20,14 @@ host synchronisation (the edge count stays on the device, in row_ptr[-1]): the s
 of a simulation whose positions change every step then queues the graph build and
 the fused kernel back to back.  check() raises if the edges outgrew max_edges (the
 rows are then left empty, so the kernels that follow read nothing past the arrays).
+Such an overflow is silent until check() runs: every kernel queued on the graph then
+returns all-zero sums (no messages, no forces).  A loop that builds with max_edges
+must call check() (one host synchronisation) before it trusts a result, e.g. once
+every few steps with max_edges sized with headroom, and rebuild larger on an error.
+
+row_ptr is a view into the neighbor list's device workspace (no copy on the hot
+path): it keeps that workspace alive, and saving it serialises the workspace too;
+take row_ptr.clone() to keep the offsets alone.
 """
 import torch
 
@@ -82,7 +90,10 @@ class Graph:
     def fine_order(self):
         """Morton order of the atoms on a grid of 1 to 8 atoms per cell (spatial_order; built
         on first use).  The MACE layer walks its destination rows in this order, 1.5% faster
-        at configs[4] than in the cell list's order."""
+        at configs[4] than in the cell list's order.  It is computed from the values that
+        the positions tensor given to the constructor holds at the first call (a caller
+        that updates positions in place before then gets the order of the new values);
+        results never depend on the order, only the speed does."""
         if self._fine_order is None:
             self._fine_order = _batmobile.spatial_order(self.positions, self.cell)
         return self._fine_order
@@ -99,7 +110,10 @@ class Graph:
 
         With weights [34, C_in, C_out]: out[d] = sum_{e -> d} tensor_product(X[src_e],
         Y_lm(v_e), weights), the per-path sums over each destination's edges mixed once
-        per destination (destinations processed in the spatial order)."""
+        per destination (destinations processed in the spatial order).
+
+        A graph built with max_edges whose edges outgrew it gives all-zero sums here
+        without an error: call check() before trusting the result."""
         if weights is not None:
             return _batmobile.sh_tp_scatter_weighted(self.vec, node_features, weights, self.src,
                                                      self.row_ptr, None, self.order, normalize)

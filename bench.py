@@ -380,6 +380,117 @@ def scatter_sweep(torch, bm, dev, sizes=(5000, 20000, 50000), reps=200):
     return res
 
 
+def create_edge_index_like(n_atoms, avg_neighbors, seed):
+    """The reference benchmarks' random graph (benchmarks/benchmark_fused_sh_tp.py:16-31,
+    benchmark_fused_mp.py): per target, randint(1, 2 avg) sources uniform over all atoms,
+    self pairs dropped, duplicates removed, and the edges left in the scrambled order of
+    list(set(edges)) (here: a seeded random permutation).  Returns edge_index [2, E]."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randint(1, 2 * avg_neighbors, (n_atoms,), generator=g)
+    tgt = torch.repeat_interleave(torch.arange(n_atoms), k)
+    src = torch.randint(0, n_atoms, (tgt.numel(),), generator=g)
+    keep = src != tgt
+    key = torch.unique(src[keep] * n_atoms + tgt[keep])
+    key = key[torch.randperm(key.numel(), generator=g)]
+    return torch.stack([key // n_atoms, key % n_atoms])
+
+
+def reference_workloads(torch, bm, dev, reps=200):
+    """The reference's own benchmark workloads, on this GPU (parity-tested entry points):
+      rw_*   benchmarks/benchmark_fused_sh_tp.py's largest config: create_edge_index(5000, 30)
+             (sources uniform over all atoms, edges scrambled), random unit vectors,
+             X [5000, 64, 16] ~ N(0, 1).  Timed: the reference's pipeline on these kernels
+             (fused_sh_tp_simple -> zeros -> index_add_, :103-109); the CSR single kernel
+             fused_message_passing_simple after edge_index_to_csr; and the scheduled kernel
+             after mp_schedule over the CSR (col_perm), destinations in index order.
+             Flops E (512 C + 1222) against the fp32 MFMA peak.
+      msg_*  the messages kernel fused_sh_tp_simple at configs[3] (the headline graph),
+             HBM roofline on E (12 + 8 + 64 C) read + E 64 C written.
+      fmp_*  benchmarks/benchmark_fused_mp.py's config: create_edge_index(1000, 20),
+             C_in = C_out = 32, W [32, 32] / sqrt(32): fused_message_passing_simple and
+             fused_message_passing."""
+    res = {}
+    n, c = N_ATOMS, CHANNELS
+    ei = create_edge_index_like(n, 30, SEED + 200).to(dev)
+    e = int(ei.shape[1])
+    g = torch.Generator().manual_seed(SEED + 201)
+    v = torch.randn(e, 3, generator=g)
+    v = (v / v.norm(dim=1, keepdim=True)).to(dev)
+    x = torch.randn(n, c, 16, generator=g).to(dev)
+    src, tgt = ei[0].contiguous(), ei[1].contiguous()
+    f = e * (2 * 256 * c + 2 * 611)
+
+    def pipeline():
+        m = bm.fused_sh_tp_simple(v, x, src)
+        return torch.zeros(n, c, 16, device=dev).index_add_(0, tgt, m)
+
+    res["rw_E"] = e
+    t = event_ms(torch, pipeline, 20)
+    res["rw_reference_pipeline_ms"] = round(t, 5)
+    res["rw_reference_pipeline_edges_per_s"] = round(e / (t * 1e-3), 1)
+    res["rw_edge_index_to_csr_ms"] = round(time_call(torch, lambda: bm.edge_index_to_csr(ei, n), 20), 5)
+    rp, col = bm.edge_index_to_csr(ei, n)
+    for _ in range(SETTLE_STEPS // 2):
+        out_csr = bm.fused_message_passing_simple(x, v, ei, rp, col)
+    t = event_ms(torch, lambda: bm.fused_message_passing_simple(x, v, ei, rp, col), reps)
+    res["rw_csr_kernel_ms"] = round(t, 5)
+    res["rw_csr_kernel_edges_per_s"] = round(e / (t * 1e-3), 1)
+    res["rw_csr_kernel_mfma_frac"] = round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+    order = torch.arange(n, device=dev)
+    res["rw_mp_schedule_ms"] = round(time_call(torch, lambda: bm.mp_schedule(rp, order, c, col, e), 20), 5)
+    rps, ep, rdst, nb, rpb = bm.mp_schedule(rp, order, c, col, e)
+
+    def sched():
+        return bm.sh_tp_scatter_scheduled(v, x, src, rps, ep, rdst, nb, rpb, n, False)
+
+    out_s = sched()
+    assert torch.equal(out_s, out_csr), "scheduled and CSR kernels disagree"
+    for _ in range(SETTLE_STEPS // 2):
+        sched()
+    t = event_ms(torch, sched, reps)
+    res["rw_scheduled_kernel_ms"] = round(t, 5)
+    res["rw_scheduled_kernel_edges_per_s"] = round(e / (t * 1e-3), 1)
+    res["rw_scheduled_kernel_mfma_frac"] = round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+    del x, v, ei, src, tgt, rp, col, rps, ep, rdst
+
+    # the messages kernel on the headline graph (one [E, C, 16] store per edge)
+    w = make_workload(torch, bm, dev)
+    vn = w["vec"] / w["vec"].norm(dim=1, keepdim=True)
+    e3 = int(w["src"].numel())
+    for _ in range(50):
+        bm.fused_sh_tp_simple(vn, w["x"], w["src"])
+    t = event_ms(torch, lambda: bm.fused_sh_tp_simple(vn, w["x"], w["src"]), 50)
+    b = e3 * (12 + 8 + 64 * c) + e3 * 64 * c
+    res["msg_cfg3_kernel_ms"] = round(t, 5)
+    res["msg_cfg3_algorithmic_bytes"] = b
+    res["msg_cfg3_GBs"] = round(b / (t * 1e-3) / 1e9, 1)
+    res["msg_cfg3_hbm_frac"] = round(b / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    res["msg_cfg3_write_only_hbm_frac"] = round(e3 * 64 * c / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    del w, vn
+
+    # benchmarks/benchmark_fused_mp.py: N = 1000, C_in = C_out = 32, ~20 neighbours
+    n2, c2 = 1000, 32
+    ei2 = create_edge_index_like(n2, 20, SEED + 300).to(dev)
+    e2 = int(ei2.shape[1])
+    g = torch.Generator().manual_seed(SEED + 301)
+    v2 = torch.randn(e2, 3, generator=g)
+    v2 = (v2 / v2.norm(dim=1, keepdim=True)).to(dev)
+    x2 = torch.randn(n2, c2, 16, generator=g).to(dev)
+    w2 = (torch.randn(c2, c2, generator=g) / math.sqrt(c2)).to(dev)
+    rp2, col2 = bm.edge_index_to_csr(ei2, n2)
+    res["fmp_E"] = e2
+    t = event_ms(torch, lambda: bm.fused_message_passing_simple(x2, v2, ei2, rp2, col2), reps)
+    f2 = e2 * (2 * 256 * c2 + 2 * 611)
+    res["fmp_simple_ms"] = round(t, 5)
+    res["fmp_simple_edges_per_s"] = round(e2 / (t * 1e-3), 1)
+    res["fmp_simple_mfma_frac"] = round(f2 / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+    t = event_ms(torch, lambda: bm.fused_message_passing(x2, v2, w2, rp2, col2), reps)
+    res["fmp_dense_w_ms"] = round(t, 5)
+    res["fmp_dense_w_edges_per_s"] = round(e2 / (t * 1e-3), 1)
+    return res
+
+
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     passes recorded in profiles/hbm_traffic.txt (scaled by the copy calibration)."""
@@ -419,6 +530,10 @@ def main():
     ap.add_argument("--scatter-sweep", action="store_true",
                     help="time only the headline kernel at N = 5000, 20000, 50000 (C = 64) and "
                          "print the figures")
+    ap.add_argument("--reference-workloads-only", action="store_true",
+                    help="time only the reference benchmarks' own workloads (random graph of "
+                         "benchmark_fused_sh_tp.py, messages kernel, benchmark_fused_mp.py) and "
+                         "print the figures")
     ap.add_argument("--graph-only", action="store_true",
                     help="build the configs[3] graph --steps times, then run as many end-to-end "
                          "steps, and print the times (for kernel traces of the build)")
@@ -448,6 +563,9 @@ def main():
         return
     if a.scatter_sweep:
         print(json.dumps(scatter_sweep(torch, bm, dev, reps=max(a.steps, 1))), flush=True)
+        return
+    if a.reference_workloads_only:
+        print(json.dumps(reference_workloads(torch, bm, dev, reps=max(a.steps, 1))), flush=True)
         return
     if a.mace_only:
         print(json.dumps(mace_config4(torch, bm, dev, reps=max(min(a.steps, 10), 1))), flush=True)
@@ -532,6 +650,7 @@ def main():
         extra["reference_pipeline_on_this_gpu_ms"] = round(time_reference_composition(torch, bm, dev, w), 4)
         weighted, w_out = weighted_config3(torch, bm, dev, w, wt)
         extra.update(other_configs(torch, bm, dev))
+        extra.update(reference_workloads(torch, bm, dev))
         extra.update(mace_config4(torch, bm, dev))
 
     res = {

@@ -57,6 +57,35 @@ def test_noalloc_backward_rejects_oversize_before_any_device_call():
     assert f(one, one, one, one, None, None, one, 100000, 1024, 1024, None) == -4
 
 
+def test_noalloc_scratch_holds_every_claimed_shape():
+    """The header's claim: the no-allocation backward's grad_W partials fit its 24 MiB
+    scratch for every N whenever 3 * ceil(C_in/16) * ceil(C_out/64) <= 512.  Swept over N
+    from 1 to 10^7 and channel pairs across and at the corners of that region, with the
+    host-only workspace-size function (no GPU)."""
+    lib = ctypes.CDLL(LIB)
+    f = lib.batteries_tensor_product_backward_workspace_bytes
+    f.restype = ctypes.c_size_t
+    f.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int]
+    scratch = 24 << 20
+    ns = sorted(set([1, 2, 15, 16, 17, 100, 255, 256, 257, 1000, 4095, 4096, 4097, 20000,
+                     65535, 65536, 100003, 10 ** 6, 1234567, 10 ** 7]
+                    + [int(round(10 ** (k / 4))) for k in range(29)]))
+    pairs = [(256, 256), (16, 10880), (208, 832), (10880, 16), (2720, 64), (16, 64), (1, 1),
+             (32, 64), (64, 64), (128, 128), (170, 640), (255, 255), (512, 128), (96, 1088)]
+    pairs += [(ci, co) for ci in (1, 7, 16, 31, 48, 100, 160) for co in (1, 33, 64, 65, 500, 1000)]
+    checked = 0
+    for ci, co in pairs:
+        combos = 3 * -(-ci // 16) * -(-co // 64)
+        if combos > 512:
+            continue
+        for n in ns:
+            assert f(n, ci, co) <= scratch, (n, ci, co, f(n, ci, co))
+            checked += 1
+    assert checked > 500
+    # just outside the region the partials can exceed it
+    assert f(10 ** 6, 1024, 1024) > scratch
+
+
 def test_host_only_entry_points():
     lib = ctypes.CDLL(LIB)
     assert lib.batteries_get_num_paths_l3() == 34
