@@ -77,8 +77,7 @@ def build_lib(force=False, jobs=4):
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, todo))
     if force or todo or _stale(LIB, objs):
-        _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", LIB] + objs
-             + ["-L" + os.path.join(ROCM, "lib"), "-lrocblas"])
+        _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", LIB] + objs)
     nl_obj = os.path.join(BUILD, "nl.o")
     if force or todo or _stale(NL_LIB, [nl_obj]):
         _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", NL_LIB, nl_obj])

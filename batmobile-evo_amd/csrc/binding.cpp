@@ -47,7 +47,6 @@ void check_status(int rc, const char* what) {
     if (rc == BATMOBILE_HIP_OK) return;
     if (rc == BATMOBILE_HIP_ERR_ARG) TORCH_CHECK(false, what, ": invalid argument");
     if (rc == BATMOBILE_HIP_ERR_WORKSPACE) TORCH_CHECK(false, what, ": workspace too small");
-    if (rc == BATMOBILE_HIP_ERR_BLAS) TORCH_CHECK(false, what, ": rocBLAS call failed");
     if (rc == BATMOBILE_HIP_ERR_SCRATCH) TORCH_CHECK(false, what, ": larger than the static scratch");
     TORCH_CHECK(false, "HIP error in ", what, ": ", hipGetErrorString(static_cast<hipError_t>(rc)));
 }
@@ -859,40 +858,24 @@ torch::Tensor mace_forward(const torch::Tensor& positions, const torch::Tensor& 
                            const torch::Tensor& b1, const torch::Tensor& w2,
                            const torch::Tensor& src, const torch::Tensor& dst,
                            const torch::Tensor& row_ptr, double cutoff,
-                           const c10::optional<torch::Tensor>& edge_weights,
                            const c10::optional<torch::Tensor>& order) {
     const MaceArgs a = mace_check(positions, cell, node_features, w1, b1, w2, src, dst, row_ptr);
     torch::Tensor x = aligned16(node_features);
     torch::Tensor out = torch::empty({a.N, a.C, 16}, f32_like(x));
     if (a.N == 0) return out;
     const int64_t* ord = mace_order(order, a.N, x);
-    float* ew = nullptr;
-    if (edge_weights.has_value() && edge_weights->defined()) {
-        TORCH_CHECK(edge_weights->dtype() == torch::kFloat32 &&
-                        edge_weights->numel() ==
-                            batteries_mace_edge_weight_rows(a.E, (int)a.C) * 34 * a.C,
-                    "edge_weights must be float32 [mace_edge_weight_rows(E, C), 34 C]");
-        torch::Tensor t = *edge_weights;  // shares the storage
-        ew = mptr<float>(t, "edge_weights");
-    }
     const c10::DeviceGuard guard(x.device());
-    const size_t wsb = batteries_mace_workspace_bytes(a.E, (int)a.C, 0, ew != nullptr);
+    const size_t wsb = batteries_mace_workspace_bytes(a.N, a.E, (int)a.C, 0);
     torch::Tensor ws = torch::empty({(int64_t)((wsb + 3) / 4)}, f32_like(x));
     check_status(batteries_mace_forward(cptr<float>(positions, "positions"), a.box,
                                         cptr<float>(x, "node_features"), cptr<float>(w1, "W1"),
                                         cptr<float>(b1, "b1"), cptr<float>(w2, "W2"),
                                         cptr<int64_t>(src, "src"), cptr<int64_t>(dst, "dst"),
                                         cptr<int64_t>(row_ptr, "row_ptr"), ord,
-                                        mptr<float>(out, "out"), ew, a.N, a.E, (int)a.C,
-                                        (float)cutoff, ws.data_ptr(), wsb,
-                                        current_stream(x)),
+                                        mptr<float>(out, "out"), a.N, a.E, (int)a.C,
+                                        (float)cutoff, ws.data_ptr(), wsb, current_stream(x)),
                  "mace_forward");
     return out;
-}
-
-int64_t mace_edge_weight_rows(int64_t E, int64_t C) {
-    TORCH_CHECK(E >= 0 && C > 0, "E must be >= 0 and C > 0");
-    return batteries_mace_edge_weight_rows(E, (int)C);
 }
 
 torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor& cell,
@@ -901,7 +884,6 @@ torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor&
                             const torch::Tensor& src, const torch::Tensor& dst,
                             const torch::Tensor& row_ptr, const torch::Tensor& rev,
                             const torch::Tensor& grad_out, double cutoff,
-                            const c10::optional<torch::Tensor>& edge_weights,
                             const c10::optional<torch::Tensor>& order) {
     const MaceArgs a = mace_check(positions, cell, node_features, w1, b1, w2, src, dst, row_ptr);
     TORCH_CHECK(rev.numel() == a.E && rev.dtype() == torch::kInt64, "rev must be int64 [E]");
@@ -913,16 +895,8 @@ torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor&
     torch::Tensor gpos = torch::empty({a.N, 3}, f32_like(x));
     if (a.N == 0) return gpos;
     const int64_t* ord = mace_order(order, a.N, x);
-    const float* ew = nullptr;
-    if (edge_weights.has_value() && edge_weights->defined()) {
-        TORCH_CHECK(edge_weights->dtype() == torch::kFloat32 &&
-                        edge_weights->numel() ==
-                            batteries_mace_edge_weight_rows(a.E, (int)a.C) * 34 * a.C,
-                    "edge_weights must be float32 [mace_edge_weight_rows(E, C), 34 C]");
-        ew = cptr<float>(*edge_weights, "edge_weights");
-    }
     const c10::DeviceGuard guard(x.device());
-    const size_t wsb = batteries_mace_workspace_bytes(a.E, (int)a.C, 1, ew != nullptr);
+    const size_t wsb = batteries_mace_workspace_bytes(a.N, a.E, (int)a.C, 1);
     torch::Tensor ws = torch::empty({(int64_t)((wsb + 3) / 4)}, f32_like(x));
     check_status(batteries_mace_backward(cptr<float>(positions, "positions"), a.box,
                                          cptr<float>(x, "node_features"), cptr<float>(w1, "W1"),
@@ -930,7 +904,7 @@ torch::Tensor mace_backward(const torch::Tensor& positions, const torch::Tensor&
                                          cptr<int64_t>(src, "src"), cptr<int64_t>(dst, "dst"),
                                          cptr<int64_t>(row_ptr, "row_ptr"), ord,
                                          cptr<int64_t>(rev, "rev"), cptr<float>(g, "grad_out"),
-                                         ew, mptr<float>(gpos, "grad_pos"), a.N, a.E, (int)a.C,
+                                         mptr<float>(gpos, "grad_pos"), a.N, a.E, (int)a.C,
                                          (float)cutoff, ws.data_ptr(), wsb, current_stream(x)),
                  "mace_backward");
     return gpos;
@@ -1020,20 +994,16 @@ PYBIND11_MODULE(_batmobile, m) {
           "index of every edge's reverse in a symmetric destination-grouped edge list (extension)");
     m.def("mace_forward", &mace_forward, py::arg("positions"), py::arg("cell"),
           py::arg("node_features"), py::arg("W1"), py::arg("b1"), py::arg("W2"), py::arg("src"),
-          py::arg("dst"), py::arg("row_ptr"), py::arg("cutoff"),
-          py::arg("edge_weights") = py::none(), py::arg("order") = py::none(),
-          "MACE-style layer with per-edge radial weights, forward (extension); edge_weights "
-          "[mace_edge_weight_rows(E, C), 34 C] receives the per-edge weights for the backward; "
-          "order [N], a permutation of 0..N-1, is the processing order of the destination rows "
-          "(results do not depend on it)");
-    m.def("mace_edge_weight_rows", &mace_edge_weight_rows, py::arg("E"), py::arg("C"),
-          "rows of the buffer that keeps the per-edge weights of all E edges (whole chunks)");
+          py::arg("dst"), py::arg("row_ptr"), py::arg("cutoff"), py::arg("order") = py::none(),
+          "MACE-style layer with per-edge radial weights, forward (extension; one fused kernel, "
+          "the per-edge weights stay on chip); order [N], a permutation of 0..N-1, is the "
+          "processing order of the destinations (results do not depend on it)");
     m.def("mace_backward", &mace_backward, py::arg("positions"), py::arg("cell"),
           py::arg("node_features"), py::arg("W1"), py::arg("b1"), py::arg("W2"), py::arg("src"),
           py::arg("dst"), py::arg("row_ptr"), py::arg("rev"), py::arg("grad_out"),
-          py::arg("cutoff"), py::arg("edge_weights") = py::none(), py::arg("order") = py::none(),
-          "gradient of the MACE-style layer w.r.t. positions (extension); with the forward's "
-          "edge_weights the per-edge weights are not recomputed; order as for mace_forward");
+          py::arg("cutoff"), py::arg("order") = py::none(),
+          "gradient of the MACE-style layer w.r.t. positions (extension); order as for "
+          "mace_forward");
     m.def("selftest_mfma_16x16x4", &selftest_mfma_16x16x4, py::arg("A"), py::arg("B"),
           "D = A @ B through one v_mfma_f32_16x16x4f32 (lane-layout self test)");
     m.def("selftest_mfma_4x4x1_bcast", &selftest_mfma_4x4x1_bcast, py::arg("A"), py::arg("B"),

@@ -333,4 +333,3 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t v) {
 #define BM_OK 0
 #define BM_ERR_ARG -1
 #define BM_ERR_WORKSPACE -2
-#define BM_ERR_BLAS -3

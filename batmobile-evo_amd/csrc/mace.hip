@@ -13,17 +13,15 @@
 //   out[d, c, o] = sum_{e -> d} sum_p R[e,c,p] sum_{(a,b) in p -> o} CG x[src_e,c,a] Y_e[b]
 //
 // Work per edge: the MLP's second layer is a GEMM [edges x 64] x [64 x 34C]
-// (557 kflop per edge at C = 128) and runs on MFMA over edge chunks; the CG
-// work (611 products with a coefficient, 256 bilinear products and 156 path
-// weightings per edge and channel) runs on the VALU, thread per
-// (destination row, channel), so every output row is written by one thread in
-// a fixed edge order (deterministic, no atomics).  Forces are gathered per
-// atom from per-edge gradients through the reverse-edge map of the symmetric
-// edge list.
-#include <mutex>
-
-#include <rocblas/rocblas.h>
-
+// (557 kflop per edge at C = 128).  One kernel per pass runs it on MFMA and
+// consumes each tile of per-edge weights R straight from the accumulators in
+// the channel-wise CG product on the VALU (611 products with a coefficient,
+// 256 bilinear products and 156 path weightings per edge and channel), so R
+// (26 GB at configs[4]) never reaches memory.  The backward runs the same
+// tiles with the MLP's transpose GEMM on MFMA fed by the path gradients, and
+// ends in per-edge position gradients; forces are gathered per atom through
+// the reverse-edge map of the symmetric edge list.  Every sum runs in a fixed
+// order (deterministic, no atomics).
 #include "common.h"
 #include "batmobile_hip.h"
 
@@ -31,20 +29,6 @@ namespace bmhip {
 
 constexpr int kNBasis = 8;
 constexpr int kHidden = 64;
-// Edges per chunk (R and its gradient live per chunk): up to kMaceChunkMax, and
-// all chunks of a graph equally long (multiples of 256, the last one shorter by
-// less than 256 per chunk), so the GEMMs run every chunk at one height.  Larger
-// chunks run faster on MI355X (configs[4], forward / backward: 8192 edges
-// 36.3 / 88.7 ms, 65536 19.3 / 34.5 ms, 131072 16.6 / 32.0 ms, 262144 16.2 /
-// 31.3 ms); R is 17 KB per edge at C = 128, 4.6 GB for a chunk of 262144.
-constexpr int64_t kMaceChunkMax = 262144;
-static int64_t mace_chunk(int64_t E, int C) {
-    // R offsets within a chunk stay below 2^31 (32-bit GEMM and kernel offsets)
-    const int64_t cap = std::min<int64_t>(kMaceChunkMax, INT32_MAX / ((int64_t)C * 34) / 256 * 256);
-    const int64_t e = std::max<int64_t>(E, 1);
-    const int64_t n = (e + cap - 1) / cap;
-    return ((e + n - 1) / n + 255) / 256 * 256;
-}
 
 #pragma clang fp contract(off)
 // v = pos[dst] - pos[src] with the minimum image of an orthorhombic box, in the
@@ -92,57 +76,6 @@ __device__ __forceinline__ void radial_basis(float r, float rc, float* B, float*
 }
 
 __device__ __forceinline__ float sigmoidf(float z) { return 1.0f / (1.0f + expf(-z)); }
-
-
-// ---------------------------------------------------------------------------
-// edge vectors from positions (grid over edges)
-// ---------------------------------------------------------------------------
-__global__ void mace_edge_vectors_kernel(const float* __restrict__ pos, MaceBox bx,
-                                         const int64_t* __restrict__ src,
-                                         const int64_t* __restrict__ dst, float* __restrict__ vec,
-                                         int64_t n_edges) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= n_edges) return;
-    float v[3];
-    edge_vector(pos, src[e], dst[e], bx.box, bx.inv, v);
-    vec[e * 3 + 0] = v[0];
-    vec[e * 3 + 1] = v[1];
-    vec[e * 3 + 2] = v[2];
-}
-
-// ---------------------------------------------------------------------------
-// h[e, :] = silu(B(r_e) W1 + b1), edges [e0, e1) of the chunk (row e - e0 of h)
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void mace_radial_kernel(const float* __restrict__ vec,
-                                                          const float* __restrict__ w1,
-                                                          const float* __restrict__ b1,
-                                                          float* __restrict__ h, int64_t e0,
-                                                          int64_t e1, float rc) {
-    __shared__ float sW[kNBasis * kHidden + kHidden];
-    for (int i = threadIdx.x; i < kNBasis * kHidden + kHidden; i += blockDim.x)
-        sW[i] = i < kNBasis * kHidden ? w1[i] : b1[i - kNBasis * kHidden];
-    __syncthreads();
-    const int64_t e = e0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= e1) return;
-    float vx = vec[e * 3], vy = vec[e * 3 + 1], vz = vec[e * 3 + 2];
-    const float r = normalize3(vx, vy, vz);
-    float B[kNBasis];
-    radial_basis(r, rc, B, nullptr);
-    float4* out = reinterpret_cast<float4*>(h + (e - e0) * kHidden);
-#pragma unroll
-    for (int j4 = 0; j4 < kHidden / 4; ++j4) {
-        float z[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int j = j4 * 4 + t;
-            float acc = sW[kNBasis * kHidden + j];
-#pragma unroll
-            for (int k = 0; k < kNBasis; ++k) acc = fmaf(B[k], sW[k * kHidden + j], acc);
-            z[t] = acc * sigmoidf(acc);
-        }
-        out[j4] = make_float4(z[0], z[1], z[2], z[3]);
-    }
-}
 
 // ---------------------------------------------------------------------------
 // fp32 GEMM on MFMA: C[M, N] = A[M, K] B, with B = [K, N] (row-major) or, when
@@ -249,39 +182,6 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
                 if (m < M) C[m * N + n] = acc[mi][ni][r];
             }
     }
-}
-
-// ---------------------------------------------------------------------------
-// Product kernels.  Threads are the channels of one edge at a time; a
-// workgroup walks the destination rows that have edges in the chunk [e0, e1).
-// Per path, T_p[e, c, o] = sum over the path's CG entries of c Y[b] x[a] is
-// formed per thread from registers.  (Building K_p[o][a] = sum_b CG Y[b] once
-// per edge and reading it as a broadcast operand measured slower here: from
-// LDS each broadcast read still moves 1 KB per wave, from memory the scalar
-// loads stall.)
-// ---------------------------------------------------------------------------
-// grid of the product kernels: at most chunk / 4 destination rows hold edges of
-// a chunk when every row has 4 or more (grid-stride loop over the rows beyond)
-static unsigned mace_row_blocks(int64_t chunk) { return (unsigned)(chunk / 4); }
-
-// rows[2i], rows[2i+1]: first and one-past-last destination with an edge in
-// chunk i = [i * chunk, min(E, (i + 1) * chunk)).
-__global__ void mace_chunk_rows_kernel(const int64_t* __restrict__ row_ptr, int64_t N, int64_t E,
-                                       int64_t chunk, int n_chunks, int64_t* __restrict__ rows) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_chunks) return;
-    const int64_t e0 = (int64_t)i * chunk, e1 = min(E, e0 + chunk);
-    auto row_of = [&](int64_t k) {  // the row holding edge k: largest d with row_ptr[d] <= k
-        int64_t lo = 0, hi = N - 1;
-        while (lo < hi) {
-            const int64_t mid = (lo + hi + 1) >> 1;
-            if (row_ptr[mid] <= k) lo = mid;
-            else hi = mid - 1;
-        }
-        return lo;
-    };
-    rows[2 * i] = row_of(e0);
-    rows[2 * i + 1] = row_of(e1 - 1) + 1;
 }
 
 // One past the last path of the (l1, l2) block that starts at path p0 (the path
@@ -445,13 +345,6 @@ __device__ __forceinline__ void mace_grad_y(const float* xs, const float* g, con
     });
 }
 
-// Y of edge k (unit vector of vec[k]).
-__device__ __forceinline__ void mace_edge_sh(const float* __restrict__ vec, int64_t k, float* Y) {
-    float ux = vec[k * 3], uy = vec[k * 3 + 1], uz = vec[k * 3 + 2];
-    normalize3(ux, uy, uz);
-    sh_forward<3>(ux, uy, uz, Y);
-}
-
 __device__ __forceinline__ void load_row16(const float* __restrict__ p, float* v) {
     const float4* q = reinterpret_cast<const float4*>(p);
 #pragma unroll
@@ -462,256 +355,6 @@ __device__ __forceinline__ void load_row16(const float* __restrict__ p, float* v
         v[4 * i + 2] = t.z;
         v[4 * i + 3] = t.w;
     }
-}
-
-// First row and step of a workgroup's walk over the chunk's destination rows
-// [d_lo, d_hi).  Without `order`: rows d_lo + blockIdx.x, + gridDim.x, ...  With
-// `order` (n_pos positions, e.g. a spatial order): workgroup b takes position
-// (b % 8) * gridDim.x / 8 + b / 8 (consecutive positions on one XCD, whose L2 then
-// holds the source rows that neighbouring destinations share) and its row when that
-// row is in the chunk; gridDim.x is a multiple of 8.
-__device__ __forceinline__ void mace_row_walk(const int64_t* __restrict__ order, int64_t n_pos,
-                                              int64_t d_lo, int64_t d_hi, int64_t& first,
-                                              int64_t& step) {
-    if (!order) {
-        first = d_lo + blockIdx.x;
-        step = gridDim.x;
-        return;
-    }
-    const int64_t per_xcd = gridDim.x >> 3;
-    const int64_t p = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    const int64_t d = p < n_pos ? order[p] : -1;
-    first = (d >= d_lo && d < d_hi) ? d : d_hi;
-    step = d_hi - d_lo + 1;  // one row
-}
-
-// Forward: out[d, c, :] += sum over the chunk's edges of row d of
-// sum_p R[e, p, c] T_p[e, c, :] (R row e - e0 of the chunk, path-major).
-__global__ __launch_bounds__(256) void mace_tp_scatter_kernel(
-    const float* __restrict__ vec, const float* __restrict__ x, const int64_t* __restrict__ src,
-    const int64_t* __restrict__ row_ptr, const float* __restrict__ R,
-    const int64_t* __restrict__ rows, const int64_t* __restrict__ order, int64_t n_pos, int64_t e0,
-    int64_t e1, float* __restrict__ out, int C) {
-    const int c = blockIdx.y * blockDim.x + threadIdx.x;
-    const bool live = c < C;
-    const int cc = live ? c : C - 1;
-    const int64_t d_lo = rows[0], d_hi = rows[1];
-    int64_t d0, dstep;
-    mace_row_walk(order, n_pos, d_lo, d_hi, d0, dstep);
-    for (int64_t d = d0; d < d_hi; d += dstep) {
-        const int64_t s = max(row_ptr[d], e0), e = min(row_ptr[d + 1], e1);
-        float m[16];
-#pragma unroll
-        for (int o = 0; o < 16; ++o) m[o] = 0.0f;
-        // operands of edge k: its R row (path offsets in a scalar register, no
-        // per-load address math) and the source row
-        auto load = [&](int64_t k, float* rr, float* xs) {
-            const auto rs = buffer_rsrc(R + (k - e0) * C * kNumPaths, (uint32_t)C * kNumPaths * 4u);
-#pragma unroll
-            for (int p = 0; p < kNumPaths; ++p) rr[p] = buffer_ld(rs, cc * 4, p * C * 4);
-            load_row16(x + (src[k] * C + cc) * 16, xs);
-        };
-        auto message = [&](int64_t k, const float* rr, const float* xs) {
-            float Y[16];
-            mace_edge_sh(vec, k, Y);
-            mace_message(Y, xs, rr, m);
-        };
-        // two edges per step, each edge's loads issued one edge ahead (the
-        // loads past the row's last edge re-read that edge: always in bounds)
-        float rA[kNumPaths], xA[16], rB[kNumPaths], xB[16];
-        if (s < e) load(s, rA, xA);
-        int64_t k = s;
-        for (; k + 1 < e; k += 2) {
-            load(k + 1, rB, xB);
-            message(k, rA, xA);
-            load(min(k + 2, e - 1), rA, xA);
-            message(k + 1, rB, xB);
-        }
-        if (k < e) message(k, rA, xA);
-        if (live) {
-            float4* op = reinterpret_cast<float4*>(out + (d * C + c) * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float4 t = op[q];
-                t.x += m[4 * q];
-                t.y += m[4 * q + 1];
-                t.z += m[4 * q + 2];
-                t.w += m[4 * q + 3];
-                op[q] = t;
-            }
-        }
-    }
-}
-
-// Sum of v[0..15] over the 64 lanes of a wave by recursive halving (each step
-// halves the values a lane carries), in a fixed order.  Lane l with
-// (l & 3) == 0 returns the total for b = 8 bit5 + 4 bit4 + 2 bit3 + bit2 of l.
-__device__ __forceinline__ float wave_sum16(const float* v) {
-    const int lane = threadIdx.x & 63;
-    float a[8];
-    {
-        const bool hi = lane & 32;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float keep = hi ? v[8 + i] : v[i], send = hi ? v[i] : v[8 + i];
-            a[i] = keep + __shfl_xor(send, 32, 64);
-        }
-    }
-    float b4[4];
-    {
-        const bool hi = lane & 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float keep = hi ? a[4 + i] : a[i], send = hi ? a[i] : a[4 + i];
-            b4[i] = keep + __shfl_xor(send, 16, 64);
-        }
-    }
-    float c2[2];
-    {
-        const bool hi = lane & 8;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float keep = hi ? b4[2 + i] : b4[i], send = hi ? b4[i] : b4[2 + i];
-            c2[i] = keep + __shfl_xor(send, 8, 64);
-        }
-    }
-    float t;
-    {
-        const bool hi = lane & 4;
-        const float keep = hi ? c2[1] : c2[0], send = hi ? c2[0] : c2[1];
-        t = keep + __shfl_xor(send, 4, 64);
-    }
-    t += __shfl_xor(t, 2, 64);
-    t += __shfl_xor(t, 1, 64);
-    return t;
-}
-
-// ---------------------------------------------------------------------------
-// Backward, per edge of the chunk (threads = channels; the workgroup walks the
-// destination rows with edges in the chunk):
-//   gR[e, p, c] = sum_{m_out} g[d, c, o] T_p[e, c, m_out]
-//   gY[e, b]    = sum_c sum_{(p, o, a)} CG[a, b, o] x[src, c, a] R[e, p, c] g[d, c, o]
-// gY is summed over the channels in a fixed order: within a wave by
-// recursive halving, then over the waves through LDS once per batch.
-// ---------------------------------------------------------------------------
-constexpr int kMaceEB = 8;  // edges per gY reduction batch of the backward
-
-__global__ __launch_bounds__(256) void mace_tp_backward_kernel(
-    const float* __restrict__ vec, const float* __restrict__ x, const int64_t* __restrict__ src,
-    const int64_t* __restrict__ row_ptr, const float* __restrict__ R,
-    const float* __restrict__ gout, const int64_t* __restrict__ rows,
-    const int64_t* __restrict__ order, int64_t n_pos, int64_t e0, int64_t e1,
-    float* __restrict__ gR, float* __restrict__ gY, int C) {
-    __shared__ float sRed[4][kMaceEB][16];
-    const int c = threadIdx.x;
-    const bool live = c < C;
-    const int cc = live ? c : C - 1;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int my_b = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1) + 2 * ((lane >> 3) & 1) +
-                     ((lane >> 2) & 1);
-    const int64_t d_lo = rows[0], d_hi = rows[1];
-    int64_t d0, dstep;
-    mace_row_walk(order, n_pos, d_lo, d_hi, d0, dstep);
-    for (int64_t d = d0; d < d_hi; d += dstep) {
-        const int64_t s = max(row_ptr[d], e0), e = min(row_ptr[d + 1], e1);
-        float g[16];
-        load_row16(gout + (d * C + cc) * 16, g);
-        if (!live) {
-#pragma unroll
-            for (int o = 0; o < 16; ++o) g[o] = 0.0f;
-        }
-        for (int64_t kb = s; kb < e; kb += kMaceEB) {
-            const int nb = (int)min<int64_t>(kMaceEB, e - kb);
-            __syncthreads();  // the previous batch's sums have been read from sRed
-            for (int j = 0; j < nb; ++j) {
-                const int64_t k = kb + j;
-                float rr[kNumPaths];
-                const auto rs = buffer_rsrc(R + (k - e0) * C * kNumPaths, (uint32_t)C * kNumPaths * 4u);
-#pragma unroll
-                for (int p = 0; p < kNumPaths; ++p) rr[p] = buffer_ld(rs, cc * 4, p * C * 4);
-                float Y[16];
-                mace_edge_sh(vec, k, Y);
-                float xs[16];
-                load_row16(x + (src[k] * C + cc) * 16, xs);
-                const auto gs = buffer_rsrc(gR + (k - e0) * C * kNumPaths, (uint32_t)C * kNumPaths * 4u);
-                // gR[p] = g . T_p (path-major: lanes write consecutive addresses)
-                for_blocks<0>([&](auto b0, auto b1) {
-                    block_products<decltype(b0)::value, decltype(b1)::value>(
-                        Y, xs, [&](auto pp, const float* tq) {
-                            constexpr int p = decltype(pp)::value;
-                            constexpr int lo = kPathL[p][2];
-                            float gr = 0.0f;
-#pragma unroll
-                            for (int q = 0; q < 2 * lo + 1; ++q) gr = fmaf(g[lo * lo + q], tq[q], gr);
-                            if (live)
-                                __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(gr), gs, c * 4,
-                                                                      p * C * 4, 0);
-                        });
-                });
-                // gy[b] = sum over the entries (a, b, o) of c x[a] R_p g[o]
-                float gy[16];
-                mace_grad_y(xs, g, rr, gy);
-                const float t = wave_sum16(gy);
-                if ((lane & 3) == 0) sRed[wv][j][my_b] = t;
-            }
-            __syncthreads();
-            for (int i = threadIdx.x; i < nb * 16; i += blockDim.x) {
-                const int j = i >> 4, b = i & 15;
-                float t = 0.0f;
-                for (int w = 0; w < nw; ++w) t += sRed[w][j][b];
-                gY[(kb + j - e0) * 16 + b] = t;
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Backward through the radial MLP, the normalisation and SH, per edge:
-//   g_v = g_r u + (g_u - u (u . g_u)) / r
-// with g_r = sum_k (sum_j W1[k, j] g_h[j] silu'(z_j)) dB_k/dr and
-// g_u = SH backward of gY at u.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void mace_radial_backward_kernel(
-    const float* __restrict__ vec, const float* __restrict__ w1, const float* __restrict__ b1,
-    const float* __restrict__ gh, const float* __restrict__ gY, int64_t e0, int64_t e1, float rc,
-    float* __restrict__ gv) {
-    __shared__ float sW[kNBasis * kHidden + kHidden];
-    for (int i = threadIdx.x; i < kNBasis * kHidden + kHidden; i += blockDim.x)
-        sW[i] = i < kNBasis * kHidden ? w1[i] : b1[i - kNBasis * kHidden];
-    __syncthreads();
-    const int64_t e = e0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= e1) return;
-    float ux = vec[e * 3], uy = vec[e * 3 + 1], uz = vec[e * 3 + 2];
-    const float r = normalize3(ux, uy, uz);
-    float B[kNBasis], dB[kNBasis];
-    radial_basis(r, rc, B, dB);
-    float gB[kNBasis];
-#pragma unroll
-    for (int k = 0; k < kNBasis; ++k) gB[k] = 0.0f;
-    const float* ghr = gh + (e - e0) * kHidden;
-    for (int j = 0; j < kHidden; ++j) {
-        float z = sW[kNBasis * kHidden + j];
-#pragma unroll
-        for (int k = 0; k < kNBasis; ++k) z = fmaf(B[k], sW[k * kHidden + j], z);
-        const float sg = sigmoidf(z);
-        const float gz = ghr[j] * sg * (1.0f + z * (1.0f - sg));
-#pragma unroll
-        for (int k = 0; k < kNBasis; ++k) gB[k] = fmaf(sW[k * kHidden + j], gz, gB[k]);
-    }
-    float gr = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kNBasis; ++k) gr = fmaf(gB[k], dB[k], gr);
-    float Y[16], gyv[16];
-    sh_forward<3>(ux, uy, uz, Y);
-#pragma unroll
-    for (int b = 0; b < 16; ++b) gyv[b] = gY[(e - e0) * 16 + b];
-    float gux, guy, guz;
-    sh_backward<3>(ux, uy, uz, Y, gyv, gux, guy, guz);
-    const float dot = ux * gux + uy * guy + uz * guz;
-    const float ir = 1.0f / r;
-    gv[e * 3 + 0] = gr * ux + (gux - ux * dot) * ir;
-    gv[e * 3 + 1] = gr * uy + (guy - uy * dot) * ir;
-    gv[e * 3 + 2] = gr * uz + (guz - uz * dot) * ir;
 }
 
 // ---------------------------------------------------------------------------
@@ -763,6 +406,460 @@ __global__ void mace_reverse_edges_kernel(const int64_t* __restrict__ row_ptr,
     if (!ok) atomicAdd(missing, 1);
 }
 
+// ---------------------------------------------------------------------------
+// Fused layer kernels.
+//
+// Edges are taken in "positions": the destinations in the given order (a
+// spatial order keeps shared source rows in cache), each destination's edges
+// consecutive and ascending.  A prepass writes per position the unit vector and
+// length, the source and destination, and the radial MLP's hidden layer h
+// [E][64] (the backward also s[E][64], below).
+//
+// A workgroup owns one quad of 4 channels c0..c0+3 and keeps that quad's slice
+// of W2 in LDS as sW[g][4 ch + j][k] = W2[k][(4g + j) C + c0 + ch] (paths in 9
+// groups of 4, the last two slots zero; rows of 68 floats).  Each of its 4
+// waves walks its own range of positions (ranges end at destination
+// boundaries) in tiles of 16 edges.  Per tile, v_mfma_f32_16x16x4f32 gives
+//   D[4 ch + j][e] = sum_k W2[k][(4g + j) C + c0 + ch] h[e][k]  = R[e, c0 + ch, 4g + j]
+// (A = the W2 rows from LDS, B = h of the tile, K = 64 in 16 steps, 9 groups:
+// 144 MFMAs), and by the accumulator layout lane l = 16 ch + e holds the 34
+// weights of its own (edge e, channel c0 + ch) pair.  The lane then forms the
+// message of that pair, sum_p R_p T_p(x[src, c], Y(u)), on the VALU.
+// R never leaves the registers.
+//
+// Each destination's messages are summed in ascending edge order by one lane
+// after another along the tile (lane e adds lane e - 1's running sum when both
+// belong to the same destination), the running sum of a destination that
+// continues into the next tile carried in LDS.  The sum is therefore the same
+// sequence of additions whatever the tiling, the order of the destinations or
+// the launch shape; each output row is written once, with no atomics.
+// ---------------------------------------------------------------------------
+constexpr int kMaceWaves = 4;                        // waves (position ranges) per workgroup
+constexpr int kPG = 9;                               // groups of 4 paths (36 slots)
+constexpr int kW2Row = kHidden + 4;                  // LDS row of sW, in floats
+constexpr int kW2Floats = kPG * 16 * kW2Row;         // 39,168 bytes per channel quad
+constexpr int kMaceMaxWorkers = 8192;                // position ranges (wstart entries - 1)
+
+// sW for the channel quad c0..c0+3 (zeros past path 33 and past channel C - 1)
+__device__ __forceinline__ void mace_fill_w2(const float* __restrict__ w2, int C, int c0,
+                                             float* sW) {
+    for (int i = threadIdx.x; i < kHidden * 36 * 4; i += blockDim.x) {
+        const int ch = i & 3, p = (i >> 2) % 36, k = i / 144;
+        const int c = c0 + ch;
+        float v = 0.0f;
+        if (p < kNumPaths && c < C) v = w2[(int64_t)k * kNumPaths * C + p * C + c];
+        sW[((p >> 2) * 16 + 4 * ch + (p & 3)) * kW2Row + k] = v;
+    }
+}
+
+// The 34 weights of the lane's pair: sA = sW + (lane % 16) row + 4 (lane / 16),
+// hb[j] = h[e][16 j + 4 (lane / 16) .. + 3] (k-step s of block j is
+// k = 16 j + 4 (lane / 16) + s for both operands).
+__device__ __forceinline__ void mace_tile_weights(const float* sA, const float4* hb, float* rr) {
+    // the W2 operands are the same for every tile: read them from LDS per tile (an
+    // opaque base keeps the compiler from hoisting all 36 reads, 144 registers, out
+    // of the tile loop)
+    int base = 0;
+    asm volatile("" : "+v"(base));
+    sA += base;
+    v4f acc[kPG];
+#pragma unroll
+    for (int g = 0; g < kPG; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int g = 0; g < kPG; ++g) {
+            const float4 a = *reinterpret_cast<const float4*>(sA + g * 16 * kW2Row + 16 * j);
+            acc[g] = mfma4(a, hb[j], acc[g]);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < kNumPaths; ++p) rr[p] = acc[p >> 2][p & 3];
+}
+
+__device__ __forceinline__ float dpp_prev(float v) {  // lane e - 1 of the 16-lane row
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int dpp_prev_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int dpp_next_i(int v) {  // lane e + 1 of the 16-lane row
+    return __builtin_amdgcn_update_dpp(0, v, 0x101, 0xF, 0xF, false);
+}
+
+// One tile's per-position operands (pos clamped into the range by the caller).
+struct MaceTileIn {
+    float4 hb[4];
+    float4 u;  // unit vector, length
+    int s, d;
+};
+
+__device__ __forceinline__ void mace_load_tile(const float4* __restrict__ u4,
+                                               const int* __restrict__ srcp,
+                                               const int* __restrict__ dstp,
+                                               const float* __restrict__ h, int64_t pos, int kk,
+                                               MaceTileIn& t) {
+    const float4* hr = reinterpret_cast<const float4*>(h + pos * kHidden + 4 * kk);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t.hb[j] = hr[4 * j];
+    t.u = u4[pos];
+    t.s = srcp[pos];
+    t.d = dstp[pos];
+}
+
+// Sum of the rows' messages v over each destination in ascending edge order
+// along the 16-lane row, with the carried running sum of a destination that
+// continues from the previous tile; writes every destination that closes in
+// the tile, and keeps the last one's running sum in sCarry.
+__device__ __forceinline__ void mace_scatter_tile(float* v, int d, bool valid, int e16, int kk,
+                                                  bool cok, int64_t c, int C, float* sCarry,
+                                                  int& carry_d, float* __restrict__ out) {
+    const int d0 = __builtin_amdgcn_readfirstlane(d);  // lane 0 of the tile is always valid
+    if (carry_d >= 0) {
+        float* cs = sCarry + kk * 16;
+        if (d0 == carry_d) {
+            if (e16 == 0) {
+#pragma unroll
+                for (int o = 0; o < 16; ++o) v[o] = cs[o] + v[o];
+            }
+        } else if (e16 == 0 && cok) {
+            float4* op = reinterpret_cast<float4*>(out + ((int64_t)carry_d * C + c) * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) op[q] = make_float4(cs[4 * q], cs[4 * q + 1], cs[4 * q + 2], cs[4 * q + 3]);
+        }
+    }
+    // the lane reads must run on every lane (a short-circuit || would put them in a
+    // branch that lane 0 skips, and a lane reading a skipped lane gets no value)
+    const int dp = dpp_prev_i(d);
+    const bool head = (e16 == 0) | (dp != d);
+#pragma unroll
+    for (int t = 1; t < 16; ++t) {
+        const bool take = e16 == t && !head;
+#pragma unroll
+        for (int o = 0; o < 16; ++o) {
+            const float pv = dpp_prev(v[o]);
+            v[o] = take ? v[o] + pv : v[o];
+        }
+    }
+    const int dn = dpp_next_i(d);
+    if (valid & (e16 < 15) & (dn != d) & cok) {
+        float4* op = reinterpret_cast<float4*>(out + ((int64_t)d * C + c) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) op[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+    const int d15 = __builtin_amdgcn_readlane(d, 15);
+    if (d15 >= 0 && e16 == 15) {
+        float* cs = sCarry + kk * 16;
+#pragma unroll
+        for (int o = 0; o < 16; ++o) cs[o] = v[o];
+    }
+    carry_d = d15;  // -1: the tile's last lane is past the range (nothing to carry)
+}
+
+// Workgroup -> (channel quad, position range): consecutive workgroup ids go to
+// consecutive XCDs, so (bid % 8, bid / 8) puts all quads of a position range on one
+// XCD, whose L2 then serves the range's h rows to every quad.
+struct MaceWg {
+    int quad, wave_range;
+};
+__device__ __forceinline__ MaceWg mace_wg(int n_quads, int ranges_per_xcd) {
+    const int bid = blockIdx.x, xcd = bid & 7, k = bid >> 3;
+    MaceWg w;
+    w.quad = k % n_quads;
+    w.wave_range = ((xcd * ranges_per_xcd + k / n_quads) * kMaceWaves) + (threadIdx.x >> 6);
+    return w;
+}
+
+// out[d, c, :] = sum_{e -> d} sum_p R[e, c, p] T_p(x[src_e, c], Y(u_e)) for every
+// destination with an edge (out of the others is zeroed by the caller).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void mace_fused_forward_kernel(
+    const float4* __restrict__ u4, const int* __restrict__ srcp, const int* __restrict__ dstp,
+    const float* __restrict__ h, const float* __restrict__ w2, const float* __restrict__ x,
+    const int64_t* __restrict__ wstart, float* __restrict__ out, int C, int n_quads,
+    int ranges_per_xcd) {
+    __shared__ __attribute__((aligned(16))) float sW[kW2Floats];
+    __shared__ __attribute__((aligned(16))) float sCarryAll[kMaceWaves * 4 * 16];
+    const MaceWg wg = mace_wg(n_quads, ranges_per_xcd);
+    const int lane = threadIdx.x & 63, e16 = lane & 15, kk = lane >> 4;
+    const int c0 = wg.quad * 4;
+    mace_fill_w2(w2, C, c0, sW);
+    __syncthreads();
+    float* sCarry = sCarryAll + (threadIdx.x >> 6) * 64;
+    const int64_t p0 = wstart[wg.wave_range], p1 = wstart[wg.wave_range + 1];
+    const int c = c0 + kk;
+    const bool cok = c < C;
+    const int cc = cok ? c : C - 1;
+    const float* sA = sW + (lane & 15) * kW2Row + 4 * kk;
+    int carry_d = -1;
+    MaceTileIn cur;
+    if (p0 < p1) mace_load_tile(u4, srcp, dstp, h, min(p0 + e16, p1 - 1), kk, cur);
+    for (int64_t t0 = p0; t0 < p1; t0 += 16) {
+        const bool valid = t0 + e16 < p1;
+        // source row of the pair (issued first: the MFMAs below hide its latency)
+        float xs[16];
+        load_row16(x + ((int64_t)cur.s * C + cc) * 16, xs);
+        if (!valid) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cur.hb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float rr[kNumPaths];
+        mace_tile_weights(sA, cur.hb, rr);
+        // the next tile's operands, in flight during this tile's products
+        MaceTileIn nxt;
+        const int64_t t1 = t0 + 16;
+        mace_load_tile(u4, srcp, dstp, h, t1 < p1 ? min(t1 + e16, p1 - 1) : p1 - 1, kk, nxt);
+        float Y[16];
+        sh_forward<3>(cur.u.x, cur.u.y, cur.u.z, Y);
+        float m[16];
+#pragma unroll
+        for (int o = 0; o < 16; ++o) m[o] = 0.0f;
+        mace_message(Y, xs, rr, m);
+        mace_scatter_tile(m, valid ? cur.d : -1, valid, e16, kk, cok, c, C, sCarry, carry_d,
+                          out);
+        cur = nxt;
+    }
+    if (carry_d >= 0 && e16 == 0 && cok) {
+        const float* cs = sCarry + kk * 16;
+        float4* op = reinterpret_cast<float4*>(out + ((int64_t)carry_d * C + c) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) op[q] = make_float4(cs[4 * q], cs[4 * q + 1], cs[4 * q + 2], cs[4 * q + 3]);
+    }
+}
+
+// Backward: per pair, gR_p = sum_o g[d, c, o] T_p[o] feeds the MLP's transpose GEMM
+//   D[k][e] += sum_{ch} W2[k][p C + c0 + ch] gR[e, c0 + ch, p]   (K = the quad's 4
+// channels, one MFMA per path and 16-row block of k: A = W2 from LDS, B = the lane's
+// own gR_p), and gY[b] = sum c x[a] R_p g[o] is summed over the quad's channels.
+// The quad's share of the edge's position gradient,
+//   g_v = g_r u + (g_u - u (u . g_u)) / r,  g_r = sum_k D[k][e] s[e][k],
+//   g_u = SH backward of gY at u,
+// with s[e][k] = silu'(z_k) sum_b W1[b][k] dB_b/dr, goes to gv_part[quad][position].
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mace_fused_backward_kernel(
+    const float4* __restrict__ u4, const int* __restrict__ srcp, const int* __restrict__ dstp,
+    const float* __restrict__ h, const float* __restrict__ sg, const float* __restrict__ w2,
+    const float* __restrict__ x, const float* __restrict__ gout,
+    const int64_t* __restrict__ wstart, float* __restrict__ gv_part, int64_t n_pos, int C,
+    int n_quads, int ranges_per_xcd) {
+    __shared__ __attribute__((aligned(16))) float sW[kW2Floats];
+    const MaceWg wg = mace_wg(n_quads, ranges_per_xcd);
+    const int lane = threadIdx.x & 63, e16 = lane & 15, kk = lane >> 4;
+    const int c0 = wg.quad * 4;
+    mace_fill_w2(w2, C, c0, sW);
+    __syncthreads();
+    const int64_t p0 = wstart[wg.wave_range], p1 = wstart[wg.wave_range + 1];
+    const int c = c0 + kk;
+    const bool cok = c < C;
+    const int cc = cok ? c : C - 1;
+    const float* sA = sW + (lane & 15) * kW2Row + 4 * kk;
+    float* gvq = gv_part + (int64_t)wg.quad * n_pos * 3;
+    MaceTileIn cur;
+    if (p0 < p1) mace_load_tile(u4, srcp, dstp, h, min(p0 + e16, p1 - 1), kk, cur);
+    for (int64_t t0 = p0; t0 < p1; t0 += 16) {
+        const int64_t pos = t0 + e16;
+        const bool valid = pos < p1;
+        const int64_t pc = valid ? pos : p1 - 1;
+        float xs[16], g[16];
+        load_row16(x + ((int64_t)cur.s * C + cc) * 16, xs);
+        load_row16(gout + ((int64_t)cur.d * C + cc) * 16, g);
+        if (!valid) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cur.hb[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float rr[kNumPaths];
+        mace_tile_weights(sA, cur.hb, rr);
+        if (!(valid && cok)) {
+#pragma unroll
+            for (int o = 0; o < 16; ++o) g[o] = 0.0f;
+        }
+        MaceTileIn nxt;
+        const int64_t t1 = t0 + 16;
+        mace_load_tile(u4, srcp, dstp, h, t1 < p1 ? min(t1 + e16, p1 - 1) : p1 - 1, kk, nxt);
+        const float4* sr = reinterpret_cast<const float4*>(sg + pc * kHidden + 4 * kk);
+        float4 sv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sv[j] = sr[4 * j];
+        float Y[16];
+        sh_forward<3>(cur.u.x, cur.u.y, cur.u.z, Y);
+        // gR_p = g . T_p per path, straight into the transpose GEMM
+        v4f gh[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gh[j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for_blocks<0>([&](auto b0, auto b1) {
+            block_products<decltype(b0)::value, decltype(b1)::value>(
+                Y, xs, [&](auto pp, const float* tq) {
+                    constexpr int p = decltype(pp)::value;
+                    constexpr int lo = kPathL[p][2];
+                    float gr = g[lo * lo] * tq[0];
+#pragma unroll
+                    for (int q = 1; q < 2 * lo + 1; ++q) gr = fmaf(g[lo * lo + q], tq[q], gr);
+                    const float* a = sW + ((p >> 2) * 16 + 4 * kk + (p & 3)) * kW2Row + e16;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) gh[j] = mfma1(a[16 * j], gr, gh[j]);
+                });
+        });
+        // gY of the pair, summed over the quad's channels (rows of the wave)
+        float gy[16];
+        mace_grad_y(xs, g, rr, gy);
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            gy[b] += __shfl_xor(gy[b], 16, 64);
+            gy[b] += __shfl_xor(gy[b], 32, 64);
+        }
+        float gux, guy, guz;
+        sh_backward<3>(cur.u.x, cur.u.y, cur.u.z, Y, gy, gux, guy, guz);
+        // g_r: D[k][e] of the lane's k = 16 j + 4 (lane / 16) + r against s[e][k]
+        float gr = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            gr = fmaf(gh[j][0], sv[j].x, gr);
+            gr = fmaf(gh[j][1], sv[j].y, gr);
+            gr = fmaf(gh[j][2], sv[j].z, gr);
+            gr = fmaf(gh[j][3], sv[j].w, gr);
+        }
+        gr += __shfl_xor(gr, 16, 64);
+        gr += __shfl_xor(gr, 32, 64);
+        if (valid && kk == 0) {
+            const float ux = cur.u.x, uy = cur.u.y, uz = cur.u.z, ir = 1.0f / cur.u.w;
+            const float dot = ux * gux + uy * guy + uz * guz;
+            float* o = gvq + pos * 3;
+            o[0] = gr * ux + (gux - ux * dot) * ir;
+            o[1] = gr * uy + (guy - uy * dot) * ir;
+            o[2] = gr * uz + (guz - uz * dot) * ir;
+        }
+        cur = nxt;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Positions: deg[i] = degree of order[i] (then an exclusive scan gives pos0[i]),
+// perm[pos0[i] + j] = row_ptr[order[i]] + j.  Writes past n_edges are dropped
+// (order must be a permutation of the rows for the layer to be correct; a
+// malformed one cannot make these kernels read or write out of bounds).
+// ---------------------------------------------------------------------------
+__global__ void mace_order_degrees_kernel(const int64_t* __restrict__ row_ptr,
+                                          const int64_t* __restrict__ order, int64_t n,
+                                          int64_t* __restrict__ deg) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t d = order ? order[i] : i;
+    d = d < 0 ? 0 : (d >= n ? n - 1 : d);
+    deg[i] = row_ptr[d + 1] - row_ptr[d];
+}
+
+__global__ void mace_positions_kernel(const int64_t* __restrict__ row_ptr,
+                                      const int64_t* __restrict__ order,
+                                      const int64_t* __restrict__ pos0, int64_t n,
+                                      int64_t n_edges, int64_t* __restrict__ perm) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t d = order ? order[i] : i;
+    d = d < 0 ? 0 : (d >= n ? n - 1 : d);
+    const int64_t e0 = row_ptr[d], k = row_ptr[d + 1] - e0, p = pos0[i];
+    for (int64_t j = 0; j < k && p + j < n_edges; ++j) perm[p + j] = e0 + j;
+}
+
+// wstart[w] = the first position of the first destination that starts at or after
+// w * n_edges / n_workers (positions of whole destinations per worker), wstart[n_workers]
+// = n_edges.
+__global__ void mace_worker_starts_kernel(const int64_t* __restrict__ pos0, int64_t n,
+                                          int64_t n_edges, int n_workers,
+                                          int64_t* __restrict__ wstart) {
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w > n_workers) return;
+    if (w == n_workers) {
+        wstart[w] = n_edges;
+        return;
+    }
+    const int64_t target = n_edges * w / n_workers;
+    int64_t lo = 0, hi = n;  // smallest i in [0, n] with pos0[i] >= target (pos0[n] = total)
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (pos0[mid] < target) lo = mid + 1;
+        else hi = mid;
+    }
+    wstart[w] = min(pos0[lo], n_edges);
+}
+
+// Per position p (edge e = perm[p]): unit vector and length, source, destination,
+// h = silu(B(r) W1 + b1); with sg, also s[k] = silu'(z_k) sum_b W1[b][k] dB_b/dr.
+__global__ __launch_bounds__(256) void mace_prep_kernel(
+    const float* __restrict__ pos, MaceBox bx, const int64_t* __restrict__ src,
+    const int64_t* __restrict__ dst, const int64_t* __restrict__ perm,
+    const float* __restrict__ w1, const float* __restrict__ b1, float rc, int64_t n_edges,
+    float4* __restrict__ u4, int* __restrict__ srcp, int* __restrict__ dstp,
+    float* __restrict__ h, float* __restrict__ sg) {
+    __shared__ float sW[kNBasis * kHidden + kHidden];
+    for (int i = threadIdx.x; i < kNBasis * kHidden + kHidden; i += blockDim.x)
+        sW[i] = i < kNBasis * kHidden ? w1[i] : b1[i - kNBasis * kHidden];
+    __syncthreads();
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n_edges) return;
+    int64_t e = perm[p];
+    e = e < 0 ? 0 : (e >= n_edges ? n_edges - 1 : e);
+    const int64_t s = src[e], d = dst[e];
+    float v[3];
+    edge_vector(pos, s, d, bx.box, bx.inv, v);
+    const float r = normalize3(v[0], v[1], v[2]);
+    u4[p] = make_float4(v[0], v[1], v[2], r);
+    srcp[p] = (int)s;
+    dstp[p] = (int)d;
+    float B[kNBasis], dB[kNBasis];
+    radial_basis(r, rc, B, sg ? dB : nullptr);
+    float4* ho = reinterpret_cast<float4*>(h + p * kHidden);
+    float4* so = sg ? reinterpret_cast<float4*>(sg + p * kHidden) : nullptr;
+#pragma unroll
+    for (int j4 = 0; j4 < kHidden / 4; ++j4) {
+        float z[4], sd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int j = j4 * 4 + t;
+            float acc = sW[kNBasis * kHidden + j];
+#pragma unroll
+            for (int k = 0; k < kNBasis; ++k) acc = fmaf(B[k], sW[k * kHidden + j], acc);
+            const float sgm = sigmoidf(acc);
+            z[t] = acc * sgm;
+            if (sg) {
+                float q = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kNBasis; ++k) q = fmaf(sW[k * kHidden + j], dB[k], q);
+                sd[t] = sgm * (1.0f + acc * (1.0f - sgm)) * q;
+            }
+        }
+        ho[j4] = make_float4(z[0], z[1], z[2], z[3]);
+        if (sg) so[j4] = make_float4(sd[0], sd[1], sd[2], sd[3]);
+    }
+}
+
+// out rows of destinations without edges (the fused kernel writes the others)
+__global__ void mace_zero_empty_rows_kernel(const int64_t* __restrict__ row_ptr, int64_t n,
+                                            int C, float4* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per = (int64_t)C * 4;
+    if (i >= n * per) return;
+    const int64_t d = i / per;
+    if (row_ptr[d + 1] == row_ptr[d]) out[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// g_v[perm[p]] = sum over the channel quads, in order, of gv_part[quad][p]
+__global__ void mace_gv_reduce_kernel(const float* __restrict__ gv_part,
+                                      const int64_t* __restrict__ perm, int64_t n_edges,
+                                      int n_quads, float* __restrict__ gv) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n_edges) return;
+    float a = 0.f, b = 0.f, c = 0.f;
+    for (int q = 0; q < n_quads; ++q) {
+        const float* s = gv_part + ((int64_t)q * n_edges + p) * 3;
+        a += s[0];
+        b += s[1];
+        c += s[2];
+    }
+    int64_t e = perm[p];
+    e = e < 0 ? 0 : (e >= n_edges ? n_edges - 1 : e);
+    gv[e * 3 + 0] = a;
+    gv[e * 3 + 1] = b;
+    gv[e * 3 + 2] = c;
+}
+
 __global__ void mace_fill_zero_kernel(float* __restrict__ p, int64_t count) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < count) p[i] = 0.0f;
@@ -770,37 +867,42 @@ __global__ void mace_fill_zero_kernel(float* __restrict__ p, int64_t count) {
 
 __global__ void mace_zero_int_kernel(int* __restrict__ p) { *p = 0; }
 
+// Workspace of one pass (per-position arrays; the backward adds s, the quads'
+// gradient shares and the per-edge gradient).
 struct MaceWs {
-    float *vec, *h, *R, *gR, *gh, *gY, *gv;
-    int64_t* rows;  // destination range of every chunk
+    int64_t *deg, *pos0, *perm, *wstart;
+    float4* u4;
+    int *srcp, *dstp;
+    float *h, *sg, *gv_part, *gv;
     size_t bytes;
 };
 
 static size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// external: the per-edge weights of all edges live in a caller buffer
-// (batteries_mace_edge_weight_rows rows of 34 C), so the workspace holds no R chunk.
-static MaceWs mace_ws(void* base, int64_t E, int C, bool backward, bool external = false) {
-    const int64_t chunk = mace_chunk(E, C);
-    const int64_t eb = std::min<int64_t>(std::max<int64_t>(E, 1), chunk);
+static int mace_quads(int C) { return (int)ceil_div(C, 4); }
+
+static MaceWs mace_ws(void* base, int64_t N, int64_t E, int C, bool backward) {
     char* p = static_cast<char*>(base);
     size_t o = 0;
     MaceWs w{};
     auto take = [&](size_t bytes) {
-        float* r = p ? reinterpret_cast<float*>(p + o) : nullptr;
+        void* r = p ? static_cast<void*>(p + o) : nullptr;
         o = a256(o + bytes);
         return r;
     };
-    w.vec = take(sizeof(float) * 3 * (size_t)E);
-    w.rows = reinterpret_cast<int64_t*>(
-        take(sizeof(int64_t) * 2 * (size_t)ceil_div(std::max<int64_t>(E, 1), chunk)));
-    w.h = take(sizeof(float) * (size_t)eb * kHidden);
-    w.R = external ? nullptr : take(sizeof(float) * (size_t)eb * C * kNumPaths);
+    const size_t e = (size_t)std::max<int64_t>(E, 1);
+    w.deg = static_cast<int64_t*>(take(sizeof(int64_t) * (size_t)std::max<int64_t>(N, 1)));
+    w.pos0 = static_cast<int64_t*>(take(sizeof(int64_t) * (size_t)(N + 1)));
+    w.perm = static_cast<int64_t*>(take(sizeof(int64_t) * e));
+    w.wstart = static_cast<int64_t*>(take(sizeof(int64_t) * (kMaceMaxWorkers + 1)));
+    w.u4 = static_cast<float4*>(take(sizeof(float4) * e));
+    w.srcp = static_cast<int*>(take(sizeof(int) * e));
+    w.dstp = static_cast<int*>(take(sizeof(int) * e));
+    w.h = static_cast<float*>(take(sizeof(float) * kHidden * e));
     if (backward) {
-        w.gR = take(sizeof(float) * (size_t)eb * C * kNumPaths);
-        w.gh = take(sizeof(float) * (size_t)eb * kHidden);
-        w.gY = take(sizeof(float) * (size_t)eb * 16);
-        w.gv = take(sizeof(float) * 3 * (size_t)E);
+        w.sg = static_cast<float*>(take(sizeof(float) * kHidden * e));
+        w.gv_part = static_cast<float*>(take(sizeof(float) * 3 * e * (size_t)mace_quads(C)));
+        w.gv = static_cast<float*>(take(sizeof(float) * 3 * e));
     }
     w.bytes = o;
     return w;
@@ -823,45 +925,55 @@ static int gemm_launch(const float* A, const float* B, float* Cm, int64_t M, int
     return (int)hipGetLastError();
 }
 
-// The layer's two GEMMs (R = h W2 and g_h = gR W2^T) are plain fp32 GEMMs and
-// go to rocBLAS, which runs these shapes faster than gemm_f32_kernel (65536 x
-// 64 x 4352: 478 vs 525 us; 65536 x 4352 x 64: 361 vs 659 us on one MI355X).
-// One handle per device, bound to the caller's stream on every call.
-static rocblas_handle blas_handle() {
-    static std::mutex mu;
-    static rocblas_handle handles[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success)
-        handles[dev] = nullptr;
-    return handles[dev];
+// Compute units of the current device.
+static int mace_cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    return n;
 }
 
-// Row-major C[M x N] = A[M x K] B[K x N] (tb: B given as [N x K], C = A B^T),
-// as the column-major product C^T = B^T A^T.
-static int blas_gemm(const float* A, const float* B, float* Cm, int64_t M, int N, int K, bool tb,
-                     hipStream_t s) {
-    if (M <= 0 || N <= 0 || K <= 0) return BM_OK;
-    if (M > INT32_MAX) return BM_ERR_ARG;
-    rocblas_handle h = blas_handle();
-    if (!h || rocblas_set_stream(h, s) != rocblas_status_success) return BM_ERR_BLAS;
-    const float one = 1.0f, zero = 0.0f;
-    const rocblas_status st =
-        tb ? rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, N, (int)M, K,
-                           &one, B, K, A, K, &zero, Cm, N)
-           : rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, N, (int)M, K, &one,
-                           B, N, A, K, &zero, Cm, N);
-    return st == rocblas_status_success ? BM_OK : BM_ERR_BLAS;
+// Launch shape of a fused kernel: every quad of a position range on one XCD, as
+// many ranges per XCD as fill one round of resident workgroups (occupancy from the
+// runtime for this kernel), so no second, partly idle round follows.
+struct MaceShape {
+    int n_quads, ranges_per_xcd, n_workers;
+    unsigned grid;
+};
+
+template <typename K>
+static int mace_shape(K kernel, int C, MaceShape* sh) {
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess || occ < 1)
+        occ = 1;
+    const int per_xcd = std::max(1, mace_cu_count() / 8);
+    sh->n_quads = mace_quads(C);
+    sh->ranges_per_xcd = std::max(1, per_xcd * occ / sh->n_quads);
+    sh->n_workers = 8 * sh->ranges_per_xcd * kMaceWaves;
+    if (sh->n_workers > kMaceMaxWorkers) return BM_ERR_ARG;
+    sh->grid = (unsigned)(8 * sh->ranges_per_xcd * sh->n_quads);
+    return BM_OK;
 }
 
-// Rows of a chunk's GEMMs: a graph of more than one chunk runs every chunk's
-// GEMMs at the full chunk height (the workspace holds a chunk's rows; rows
-// past the chunk's last edge hold the previous chunk's finite values and their
-// results are never read), so that rocBLAS picks the same kernel for the last,
-// shorter chunk (65536 x 64 x 4352 at 323 us; 57844 rows picked a 992 us one).
-static int64_t gemm_rows(int64_t n_edges, int64_t eb, int64_t chunk) {
-    return n_edges > chunk ? chunk : eb;
+// Positions (destinations in `order`, each destination's edges ascending), the
+// workers' ranges, and the per-position operands.
+static int mace_prepare(const float* positions, const MaceBox& bx, const float* w1,
+                        const float* b1, const int64_t* src, const int64_t* dst,
+                        const int64_t* row_ptr, const int64_t* order, int64_t N, int64_t E,
+                        float cutoff, const MaceShape& sh, const MaceWs& w, bool backward,
+                        hipStream_t stream) {
+    const unsigned nb = (unsigned)ceil_div(N, 256);
+    mace_order_degrees_kernel<<<nb, 256, 0, stream>>>(row_ptr, order, N, w.deg);
+    int rc = batteries_exclusive_scan_i64(w.deg, w.pos0, N, stream);
+    if (rc != BM_OK) return rc;
+    mace_positions_kernel<<<nb, 256, 0, stream>>>(row_ptr, order, w.pos0, N, E, w.perm);
+    mace_worker_starts_kernel<<<(unsigned)ceil_div(sh.n_workers + 1, 256), 256, 0, stream>>>(
+        w.pos0, N, E, sh.n_workers, w.wstart);
+    mace_prep_kernel<<<(unsigned)ceil_div(E, 256), 256, 0, stream>>>(
+        positions, bx, src, dst, w.perm, w1, b1, cutoff, E, w.u4, w.srcp, w.dstp, w.h,
+        backward ? w.sg : nullptr);
+    return (int)hipGetLastError();
 }
 
 }  // namespace bmhip
@@ -874,18 +986,9 @@ extern "C" int batteries_gemm_f32(const float* A, const float* B, float* C, int6
     return gemm_launch(A, B, C, M, N, K, trans_b != 0, stream);
 }
 
-extern "C" size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward,
-                                                 int external_weights) {
-    if (N_edges < 0 || C <= 0) return 0;
-    return mace_ws(nullptr, N_edges, C, backward != 0, external_weights != 0).bytes;
-}
-
-// Rows of a caller buffer for the per-edge weights of all edges: whole chunks
-// (every chunk's GEMM writes a full chunk of rows; rows past N_edges are padding).
-extern "C" int64_t batteries_mace_edge_weight_rows(int64_t N_edges, int C) {
-    if (N_edges <= 0 || C <= 0) return 0;
-    const int64_t chunk = mace_chunk(N_edges, C);
-    return ceil_div(N_edges, chunk) * chunk;
+extern "C" size_t batteries_mace_workspace_bytes(int64_t N, int64_t N_edges, int C, int backward) {
+    if (N < 0 || N_edges < 0 || C <= 0) return 0;
+    return mace_ws(nullptr, N, N_edges, C, backward != 0).bytes;
 }
 
 extern "C" int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src,
@@ -901,10 +1004,10 @@ extern "C" int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_
 
 static bool mace_args_ok(const float* box, int64_t N, int64_t E, int C, float cutoff) {
     if (!box || N < 0 || E < 0 || C <= 0 || C > 256 || !(cutoff > 0.0f)) return false;
-    if (ceil_div(N, 8) * 8 > INT32_MAX) return false;  // one workgroup per position
+    if (N > INT32_MAX || E > INT32_MAX) return false;  // int32 indices per position
     for (int k = 0; k < 3; ++k)
         if (!(box[k] > 0.0f)) return false;
-    return true;  // chunk offsets are kept within 32 bits by mace_chunk
+    return true;
 }
 
 static MaceBox mace_box(const float* box) {
@@ -920,40 +1023,28 @@ extern "C" int batteries_mace_forward(const float* positions, const float* box,
                                       const float* node_features, const float* w1,
                                       const float* b1, const float* w2, const int64_t* src,
                                       const int64_t* dst, const int64_t* row_ptr,
-                                      const int64_t* order, float* out,
-                                      float* edge_weights, int64_t N, int64_t N_edges, int C,
-                                      float cutoff, void* workspace, size_t workspace_bytes,
-                                      hipStream_t stream) {
+                                      const int64_t* order, float* out, int64_t N,
+                                      int64_t N_edges, int C, float cutoff, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream) {
     if (!mace_args_ok(box, N, N_edges, C, cutoff)) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
-    const MaceWs w = mace_ws(workspace, N_edges, C, false, edge_weights != nullptr);
+    if ((reinterpret_cast<uintptr_t>(node_features) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return BM_ERR_ARG;
+    const MaceWs w = mace_ws(workspace, N, N_edges, C, false);
     if (!workspace || workspace_bytes < w.bytes) return BM_ERR_WORKSPACE;
-    const int64_t count = N * (int64_t)C * 16;
-    mace_fill_zero_kernel<<<(unsigned)ceil_div(count, 256), 256, 0, stream>>>(out, count);
+    const int64_t n4 = N * (int64_t)C * 4;
+    mace_zero_empty_rows_kernel<<<(unsigned)ceil_div(n4, 256), 256, 0, stream>>>(
+        row_ptr, N, C, reinterpret_cast<float4*>(out));
     if (N_edges == 0) return (int)hipGetLastError();
-    const MaceBox bx = mace_box(box);
-    mace_edge_vectors_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
-        positions, bx, src, dst, w.vec, N_edges);
-    const int nthr = C >= 256 ? 256 : (int)ceil_div(C, 64) * 64;
-    const int64_t chunk = mace_chunk(N_edges, C);
-    const int n_chunks = (int)ceil_div(N_edges, chunk);
-    mace_chunk_rows_kernel<<<(unsigned)ceil_div(n_chunks, 64), 64, 0, stream>>>(
-        row_ptr, N, N_edges, chunk, n_chunks, w.rows);
-    for (int64_t e0 = 0; e0 < N_edges; e0 += chunk) {
-        const int64_t e1 = std::min(N_edges, e0 + chunk), eb = e1 - e0;
-        // this chunk's R: the workspace chunk, or rows e0.. of the caller's buffer
-        float* R = edge_weights ? edge_weights + e0 * (int64_t)C * kNumPaths : w.R;
-        mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h, e0,
-                                                                             e1, cutoff);
-        int rc = blas_gemm(w.h, w2, R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden, false,
-                           stream);
-        if (rc != BM_OK) return rc;
-        dim3 grid(order ? (unsigned)(ceil_div(N, 8) * 8) : mace_row_blocks(chunk),
-                  (unsigned)ceil_div(C, nthr));
-        mace_tp_scatter_kernel<<<grid, nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, R,
-                                                          w.rows + 2 * (e0 / chunk), order, N,
-                                                          e0, e1, out, C);
-    }
+    MaceShape sh;
+    int rc = mace_shape(mace_fused_forward_kernel, C, &sh);
+    if (rc != BM_OK) return rc;
+    rc = mace_prepare(positions, mace_box(box), w1, b1, src, dst, row_ptr, order, N, N_edges,
+                      cutoff, sh, w, false, stream);
+    if (rc != BM_OK) return rc;
+    mace_fused_forward_kernel<<<sh.grid, 256, 0, stream>>>(w.u4, w.srcp, w.dstp, w.h, w2,
+                                                            node_features, w.wstart, out, C,
+                                                            sh.n_quads, sh.ranges_per_xcd);
     return (int)hipGetLastError();
 }
 
@@ -962,47 +1053,30 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
                                        const float* b1, const float* w2, const int64_t* src,
                                        const int64_t* dst, const int64_t* row_ptr,
                                        const int64_t* order, const int64_t* rev,
-                                       const float* grad_out,
-                                       const float* edge_weights, float* grad_pos, int64_t N,
+                                       const float* grad_out, float* grad_pos, int64_t N,
                                        int64_t N_edges, int C, float cutoff, void* workspace,
                                        size_t workspace_bytes, hipStream_t stream) {
     if (!mace_args_ok(box, N, N_edges, C, cutoff)) return BM_ERR_ARG;
     if (N == 0) return BM_OK;
-    const MaceWs w = mace_ws(workspace, N_edges, C, true, edge_weights != nullptr);
+    if ((reinterpret_cast<uintptr_t>(node_features) | reinterpret_cast<uintptr_t>(grad_out)) & 15)
+        return BM_ERR_ARG;
+    const MaceWs w = mace_ws(workspace, N, N_edges, C, true);
     if (!workspace || workspace_bytes < w.bytes) return BM_ERR_WORKSPACE;
     if (N_edges == 0) {
         mace_fill_zero_kernel<<<(unsigned)ceil_div(N * 3, 256), 256, 0, stream>>>(grad_pos, N * 3);
         return (int)hipGetLastError();
     }
-    const MaceBox bx = mace_box(box);
-    mace_edge_vectors_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
-        positions, bx, src, dst, w.vec, N_edges);
-    const int nthr = (int)ceil_div(C, 64) * 64;
-    const int64_t chunk = mace_chunk(N_edges, C);
-    const int n_chunks = (int)ceil_div(N_edges, chunk);
-    mace_chunk_rows_kernel<<<(unsigned)ceil_div(n_chunks, 64), 64, 0, stream>>>(
-        row_ptr, N, N_edges, chunk, n_chunks, w.rows);
-    for (int64_t e0 = 0; e0 < N_edges; e0 += chunk) {
-        const int64_t e1 = std::min(N_edges, e0 + chunk), eb = e1 - e0;
-        // R: the forward's saved weights (rows e0..), or recomputed into the workspace
-        const float* R = edge_weights ? edge_weights + e0 * (int64_t)C * kNumPaths : w.R;
-        int rc = BM_OK;
-        if (!edge_weights) {
-            mace_radial_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(w.vec, w1, b1, w.h,
-                                                                                 e0, e1, cutoff);
-            rc = blas_gemm(w.h, w2, w.R, gemm_rows(N_edges, eb, chunk), C * kNumPaths, kHidden,
-                           false, stream);
-            if (rc != BM_OK) return rc;
-        }
-        mace_tp_backward_kernel<<<order ? (unsigned)(ceil_div(N, 8) * 8) : mace_row_blocks(chunk),
-                                  nthr, 0, stream>>>(w.vec, node_features, src, row_ptr, R,
-                                                     grad_out, w.rows + 2 * (e0 / chunk), order,
-                                                     N, e0, e1, w.gR, w.gY, C);
-        rc = blas_gemm(w.gR, w2, w.gh, gemm_rows(N_edges, eb, chunk), kHidden, C * kNumPaths, true, stream);
-        if (rc != BM_OK) return rc;
-        mace_radial_backward_kernel<<<(unsigned)ceil_div(eb, 256), 256, 0, stream>>>(
-            w.vec, w1, b1, w.gh, w.gY, e0, e1, cutoff, w.gv);
-    }
+    MaceShape sh;
+    int rc = mace_shape(mace_fused_backward_kernel, C, &sh);
+    if (rc != BM_OK) return rc;
+    rc = mace_prepare(positions, mace_box(box), w1, b1, src, dst, row_ptr, order, N, N_edges,
+                      cutoff, sh, w, true, stream);
+    if (rc != BM_OK) return rc;
+    mace_fused_backward_kernel<<<sh.grid, 256, 0, stream>>>(
+        w.u4, w.srcp, w.dstp, w.h, w.sg, w2, node_features, grad_out, w.wstart, w.gv_part,
+        N_edges, C, sh.n_quads, sh.ranges_per_xcd);
+    mace_gv_reduce_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
+        w.gv_part, w.perm, N_edges, sh.n_quads, w.gv);
     mace_forces_kernel<<<(unsigned)ceil_div(N, 256), 256, 0, stream>>>(w.gv, row_ptr, rev, grad_pos,
                                                                         N);
     return (int)hipGetLastError();

@@ -295,10 +295,11 @@ def cpu_baseline_weighted(torch, w, wt, gpu_out):
 def mace_config4(torch, bm, dev, reps=3):
     """MACE-style layer with per-edge radial weights at N = 50,000, C = 128
     (uniform periodic box at ~30 neighbours within 5 A, seed 4): GPU neighbor list +
-    graph, forward, backward w.r.t. positions.  Flop model per edge: radial MLP
-    2 (8 64 + 64 34 C) and channel-wise CG product (1222 + 312) C forward; backward
-    reads the per-edge weights the forward kept and runs the MLP's transpose GEMM and
-    twice the CG work."""
+    graph, forward, backward w.r.t. positions (one fused kernel per pass; the per-edge
+    weights R = h W2 are formed on MFMA per tile and never stored).  Flop model per edge:
+    radial MLP 2 (8 64 + 64 34 C) and channel-wise CG product (1222 + 312) C forward; the
+    backward recomputes R and runs the MLP's transpose GEMM (twice the MLP) and twice the
+    CG work."""
     n, c = 50000, 128
     g = torch.Generator().manual_seed(4)
     L = (n / RHO) ** (1.0 / 3.0)
@@ -306,18 +307,19 @@ def mace_config4(torch, bm, dev, reps=3):
     cell = torch.diag(torch.tensor([L, L, L]))
     x = torch.randn(n, c, 16, generator=g).to(dev)
     go = torch.randn(n, c, 16, generator=g).to(dev)
-    layer = bm.MACEInteraction(c, CUTOFF, device=dev, generator=g, save_edge_weights=True)
+    layer = bm.MACEInteraction(c, CUTOFF, device=dev, generator=g)
     graph = bm.Graph(pos, cell, CUTOFF, c)
     graph.reverse_edges()
+    graph.fine_order()
     build = time_call(torch, lambda: (bm.Graph(pos, cell, CUTOFF, c).reverse_edges()), reps)
     p = pos.clone().requires_grad_(True)
 
-    def run(lay, n_rep):
+    def run(n_rep):
         fwd, bwd = [], []
         for _ in range(n_rep + 1):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            out = lay(graph, p, x)
+            out = layer(graph, p, x)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
             out.backward(go)
@@ -330,29 +332,23 @@ def mace_config4(torch, bm, dev, reps=3):
         return min(fwd[1:]), min(bwd[1:])
 
     torch.cuda.reset_peak_memory_stats(dev)
-    t_f, t_b = run(layer, reps)
+    t_f, t_b = run(reps)
     peak = torch.cuda.max_memory_allocated(dev)
-    # the same layer without the saved weights: the backward recomputes them
-    layer.save_edge_weights = False
-    torch.cuda.reset_peak_memory_stats(dev)
-    _, t_b_re = run(layer, 1)
-    peak_re = torch.cuda.max_memory_allocated(dev)
-    layer.save_edge_weights = True
     e = graph.num_edges
-    # the forward keeps the per-edge weights for the backward (positions require grad),
-    # so the backward runs the MLP's transpose GEMM only
-    f_fwd = e * (2 * (8 * 64 + 64 * 34 * c) + (1222 + 312) * c)
-    f_bwd = e * (2 * (8 * 64 + 64 * 34 * c) + 2 * (1222 + 312) * c)
+    mlp = 2 * (8 * 64 + 64 * 34 * c)
+    f_fwd = e * (mlp + (1222 + 312) * c)
+    f_bwd = e * (2 * mlp + 2 * (1222 + 312) * c)
+    mfma_fwd = e * 2 * 64 * 34 * c          # R = h W2 on MFMA
+    mfma_bwd = 2 * mfma_fwd                 # R again, and g_h = gR W2^T
     return {
         "cfg4_mace_N": n, "cfg4_mace_C": c, "cfg4_mace_E": e,
         "cfg4_mace_graph_build_ms": round(build, 3),
         "cfg4_mace_fwd_ms": round(t_f * 1e3, 3), "cfg4_mace_bwd_ms": round(t_b * 1e3, 3),
         "cfg4_mace_fwd_TFLOPs": round(f_fwd / t_f / 1e12, 2),
         "cfg4_mace_bwd_TFLOPs": round(f_bwd / t_b / 1e12, 2),
-        "cfg4_mace_saved_edge_weights_GB": round(layer.edge_weight_bytes(graph) / 1e9, 2),
+        "cfg4_mace_fwd_mfma_part_frac": round(mfma_fwd / t_f / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4),
+        "cfg4_mace_bwd_mfma_part_frac": round(mfma_bwd / t_b / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4),
         "cfg4_mace_peak_device_GB": round(peak / 1e9, 2),
-        "cfg4_mace_bwd_recompute_ms": round(t_b_re * 1e3, 3),
-        "cfg4_mace_peak_device_GB_recompute": round(peak_re / 1e9, 2),
     }
 
 

@@ -8,17 +8,13 @@
  *   - Work is enqueued on `stream` and is asynchronous unless stated.
  *   - Return value: 0 on success, a hipError_t value (> 0) on a launch/runtime
  *     error, BATMOBILE_HIP_ERR_ARG (-1) for invalid arguments, BATMOBILE_HIP_ERR_WORKSPACE (-2) for a
- *     missing or too small workspace, BATMOBILE_HIP_ERR_BLAS (-3) for a rocBLAS failure,
- *     BATMOBILE_HIP_ERR_SCRATCH (-4) for a call too large for the static scratch of
- *     the no-allocation entry point.
+ *     missing or too small workspace, BATMOBILE_HIP_ERR_SCRATCH (-4) for a call
+ *     too large for the static scratch of the no-allocation entry point.
  *   - No function allocates device memory except the reference-compatible
  *     neighbor_list_cuda(); where scratch is needed the caller passes a
  *     workspace whose size is given by the matching *_workspace_bytes(), except
  *     batteries_tensor_product_backward_l3_noalloc(), whose scratch is a static
- *     device array.  The
- *     MACE layer's plain GEMMs run on rocBLAS: its first call on a device
- *     creates that device's rocBLAS handle (rocBLAS allocates its own
- *     workspace then).
+ *     device array.  No vendor library is called.
  *
  * Each entry point names the reference function it replaces
  * (paths relative to the reference repository).
@@ -40,7 +36,6 @@ extern "C" {
 #define BATMOBILE_HIP_OK 0
 #define BATMOBILE_HIP_ERR_ARG -1
 #define BATMOBILE_HIP_ERR_WORKSPACE -2
-#define BATMOBILE_HIP_ERR_BLAS -3
 #define BATMOBILE_HIP_ERR_SCRATCH -4 /* the call needs more than the static scratch holds */
 
 /* Size of the static device scratch of batteries_tensor_product_backward_l3_noalloc
@@ -364,35 +359,31 @@ size_t neighbor_list_estimate_memory(int64_t N, float density, float cutoff);
 /* C[M,N] = A[M,K] B on MFMA (fp32); B is [K,N] row-major, or [N,K] row-major when trans_b. */
 int batteries_gemm_f32(const float* A, const float* B, float* C, int64_t M, int N, int K,
                        int trans_b, hipStream_t stream);
-/* Workspace of one forward (backward = 0) or backward (backward = 1) pass; with
- * external_weights the per-edge weights live in the caller's edge_weights buffer
- * (batteries_mace_edge_weight_rows(N_edges, C) rows of 34 C floats) instead of a
- * per-chunk workspace buffer. */
-size_t batteries_mace_workspace_bytes(int64_t N_edges, int C, int backward, int external_weights);
-int64_t batteries_mace_edge_weight_rows(int64_t N_edges, int C);
+/* Workspace of one forward (backward = 0) or backward (backward = 1) pass: per-edge
+ * arrays (unit vector, indices, the MLP's 64 hidden values; the backward adds its
+ * derivative factors and per-channel-quad gradient shares), about 0.35 KB per edge
+ * forward and 1.2 KB backward at C = 128.  The per-edge weights R are never stored. */
+size_t batteries_mace_workspace_bytes(int64_t N, int64_t N_edges, int C, int backward);
 /* rev[e] = index of the edge with source and destination swapped (-1 if absent);
  * *d_missing (device int) counts the absent ones. */
 int batteries_mace_reverse_edges(const int64_t* row_ptr, const int64_t* src, int64_t* rev,
                                  int* d_missing, int64_t N, int64_t N_edges, hipStream_t stream);
-/* edge_weights (nullable): when given, R of every edge is written there (row e,
- * path-major [34][C]) and kept for batteries_mace_backward.  order (nullable, [N]): the
- * order in which destination rows are processed, a permutation of 0..N-1 (a spatial
- * order keeps the source rows that neighbouring destinations share in cache); the
- * results do not depend on it.  A row that order names twice is summed twice and a row
- * it does not name is left out, so order must be a permutation. */
+/* out [N, C, 16] (node_features and out 16-byte aligned).  order (nullable, [N]): the
+ * order in which destinations are processed, a permutation of 0..N-1 (a spatial order
+ * keeps the source rows that neighbouring destinations share in cache); the results
+ * do not depend on it, bit for bit.  An order that is not a permutation gives wrong
+ * results (never an access out of bounds). */
 int batteries_mace_forward(const float* positions, const float* box, const float* node_features,
                            const float* w1, const float* b1, const float* w2, const int64_t* src,
                            const int64_t* dst, const int64_t* row_ptr, const int64_t* order,
-                           float* out, float* edge_weights, int64_t N, int64_t N_edges, int C,
-                           float cutoff, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream);
-/* grad_pos[N,3] = d <out, grad_out> / d positions (rev from batteries_mace_reverse_edges).
- * edge_weights (nullable): the forward's saved R; when NULL, R is recomputed per chunk. */
+                           float* out, int64_t N, int64_t N_edges, int C, float cutoff,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* grad_pos[N,3] = d <out, grad_out> / d positions (rev from batteries_mace_reverse_edges;
+ * node_features and grad_out 16-byte aligned). */
 int batteries_mace_backward(const float* positions, const float* box, const float* node_features,
                             const float* w1, const float* b1, const float* w2, const int64_t* src,
                             const int64_t* dst, const int64_t* row_ptr, const int64_t* order,
-                            const int64_t* rev, const float* grad_out, const float* edge_weights,
-                            float* grad_pos,
+                            const int64_t* rev, const float* grad_out, float* grad_pos,
                             int64_t N, int64_t N_edges, int C, float cutoff, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 

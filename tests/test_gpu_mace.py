@@ -52,8 +52,9 @@ def test_mace_layer_forward_and_forces(bm, dev, n, c):
     assert p.grad.sum(0).abs().max().item() <= 1e-5 * p.grad.abs().sum().item()
 
 
-def test_mace_layer_two_edge_chunks(bm, dev):
-    """~285k edges: two chunks (at most 262144 edges each; rows split across chunks add up)."""
+def test_mace_layer_many_tiles(bm, dev):
+    """~285k edges over every position range of the launch, C = 2 (one channel quad,
+    half of it past C)."""
     pos, cell, graph, layer, x, go = _layer_inputs(dev, 9500, 2, 21)
     assert graph.num_edges > 262144
     p = pos.to(dev).requires_grad_(True)
@@ -62,6 +63,36 @@ def test_mace_layer_two_edge_chunks(bm, dev):
     ref_out, ref_grad = _oracle(pos, cell, graph, layer, x, go)
     assert normwise_err(out.detach().cpu(), ref_out) <= 1e-5
     assert normwise_err(p.grad.cpu(), ref_grad) <= 1e-4
+
+
+def test_mace_layer_dense_cluster_long_rows(bm, dev):
+    """125 of 300 atoms on a jittered 0.7 A lattice (a 2.8 A cube): their rows hold 124
+    or more edges, so a destination's sum runs over eight or more 16-edge tiles (the
+    running sum carried from tile to tile), next to ordinary rows and rows with no edge."""
+    import batmobile
+    n, c = 300, 12
+    L = 30.0
+    g = gen(71)
+    pos = torch.rand(n, 3, generator=g) * L
+    grid = torch.stack(torch.meshgrid(*[torch.arange(5.0)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    pos[:125] = torch.tensor([10.0, 12.0, 14.0]) + 0.7 * grid + \
+        (torch.rand(125, 3, generator=g) - 0.5) * 0.1
+    pos[-1] = torch.tensor([25.0, 25.0, 25.0])
+    cell = torch.diag(torch.tensor([L, L, L]))
+    graph = batmobile.Graph(pos.to(dev), cell, 5.0, c)
+    deg = graph.row_ptr[1:] - graph.row_ptr[:-1]
+    assert int(deg.max()) >= 124
+    layer = batmobile.MACEInteraction(c, 5.0, device=dev, generator=gen(72))
+    x = torch.randn(n, c, 16, generator=gen(73))
+    go = torch.randn(n, c, 16, generator=gen(74))
+    p = pos.to(dev).requires_grad_(True)
+    out = layer(graph, p, x.to(dev))
+    out.backward(go.to(dev))
+    ref_out, ref_grad = _oracle(pos, cell, graph, layer, x, go)
+    assert normwise_err(out.detach().cpu(), ref_out) <= 1e-5
+    assert normwise_err(p.grad.cpu(), ref_grad) <= 1e-4
+    empty = (deg == 0).cpu()
+    assert torch.equal(out.detach().cpu()[empty], torch.zeros(int(empty.sum()), c, 16))
 
 
 def test_reverse_edges(bm, dev):
@@ -89,67 +120,46 @@ def test_mace_layer_is_deterministic(bm, dev):
     assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
 
 
-@pytest.mark.parametrize("n,c", [(500, 8), (9500, 2)])
-def test_mace_saved_edge_weights_equal_recomputed(bm, dev, n, c):
-    """The backward reading the forward's saved per-edge weights equals the backward
-    that recomputes them chunk by chunk (same GEMMs on the same inputs)."""
-    pos, cell, graph, layer, x, go = _layer_inputs(dev, n, c, 51)
-    p, xd, god = pos.to(dev), x.to(dev), go.to(dev)
-    args = (p, cell, xd, layer.W1, layer.b1, layer.W2, graph.src, graph.dst, graph.row_ptr)
-    e = graph.num_edges
-    rows = bm.mace_edge_weight_rows(e, c)
-    assert rows >= e
-    ew = torch.empty(rows, 34 * c, device=dev)
-    out_saved = bm.mace_forward(*args, 5.0, ew)
-    out_plain = bm.mace_forward(*args, 5.0)
-    assert torch.equal(out_saved, out_plain)
-    rev = graph.reverse_edges()
-    g_saved = bm.mace_backward(*args, rev, god, 5.0, ew)
-    g_plain = bm.mace_backward(*args, rev, god, 5.0)
-    assert torch.equal(g_saved, g_plain)
-    with pytest.raises(RuntimeError, match="edge_weights"):
-        bm.mace_forward(*args, 5.0, torch.empty(rows - 1, 34 * c, device=dev))
-
-
 def test_mace_row_order_does_not_change_results(bm, dev):
-    """Rows in the graph's spatial order (as MACEInteraction runs them) and in index
-    order give bit-identical outputs and forces: each row is summed by one workgroup in
-    ascending edge order either way.  A malformed order is refused."""
-    pos, cell, graph, layer, x, go = _layer_inputs(dev, 9500, 2, 61)  # two edge chunks
+    """Destinations in the graph's spatial order (as MACEInteraction runs them) and in
+    index order give bit-identical outputs and forces: every destination is summed in
+    ascending edge order, whatever tile its edges fall in.  A malformed order is
+    refused."""
+    pos, cell, graph, layer, x, go = _layer_inputs(dev, 9500, 6, 61)
     p, xd, god = pos.to(dev), x.to(dev), go.to(dev)
     args = (p, cell, xd, layer.W1, layer.b1, layer.W2, graph.src, graph.dst, graph.row_ptr)
     out_idx = bm.mace_forward(*args, 5.0)
     rev = graph.reverse_edges()
     g_idx = bm.mace_backward(*args, rev, god, 5.0)
     for order in (graph.fine_order(), graph.order):   # as MACEInteraction runs them, and the cell order
-        out_sp = bm.mace_forward(*args, 5.0, None, order)
+        out_sp = bm.mace_forward(*args, 5.0, order)
         assert torch.equal(out_idx, out_sp)
-        g_sp = bm.mace_backward(*args, rev, god, 5.0, None, order)
+        g_sp = bm.mace_backward(*args, rev, god, 5.0, order)
         assert torch.equal(g_idx, g_sp)
     # a reversed order as well (any permutation)
-    assert torch.equal(bm.mace_forward(*args, 5.0, None, graph.order.flip(0).contiguous()), out_idx)
+    assert torch.equal(bm.mace_forward(*args, 5.0, graph.order.flip(0).contiguous()), out_idx)
     with pytest.raises(RuntimeError, match="order"):
-        bm.mace_forward(*args, 5.0, None, graph.order[:-1].contiguous())
+        bm.mace_forward(*args, 5.0, graph.order[:-1].contiguous())
     with pytest.raises(RuntimeError, match="order"):
-        bm.mace_forward(*args, 5.0, None, graph.order.to(torch.int32))
+        bm.mace_forward(*args, 5.0, graph.order.to(torch.int32))
 
 
 def test_config4_full_size(bm, dev):
-    """configs[4] as bench.py runs it: N = 50,000, C = 128, ~1.5M edges in six chunks, the
-    per-edge weights saved by the forward.  Outputs of 100 sampled destinations against the
-    float64 oracle restricted to their incoming edges; forces on 100 sampled atoms against the
-    oracle over the edges incident to them (no other edge depends on their positions); the
-    forces sum to zero; two runs are bitwise identical; the backward from the saved weights
-    equals the one that recomputes them."""
+    """configs[4] as bench.py runs it: N = 50,000, C = 128, ~1.5M edges.  Outputs of 100
+    sampled destinations against the float64 oracle restricted to their incoming edges;
+    forces on 100 sampled atoms against the oracle over the edges incident to them (no
+    other edge depends on their positions); the forces sum to zero; two runs are bitwise
+    identical; forward and backward stay under 12 GB of device memory (the per-edge
+    weights, 26 GB, are never stored)."""
     import batmobile
     n, c = 50000, 128
     pos, cell = periodic_box(n, 4)
     graph = batmobile.Graph(pos.to(dev), cell, 5.0, c)
-    layer = batmobile.MACEInteraction(c, 5.0, device=dev, generator=gen(5), save_edge_weights=True)
+    layer = batmobile.MACEInteraction(c, 5.0, device=dev, generator=gen(5))
     x = torch.randn(n, c, 16, generator=gen(6))
     go = torch.randn(n, c, 16, generator=gen(7))
     e = graph.num_edges
-    assert e > 5 * 262144, e   # six edge chunks
+    assert e > 1_400_000, e
     torch.cuda.reset_peak_memory_stats(dev)
     outs, grads = [], []
     for _ in range(2):
@@ -160,8 +170,8 @@ def test_config4_full_size(bm, dev):
         grads.append(p.grad.cpu())
         del o, p
     peak = torch.cuda.max_memory_allocated(dev)
-    print(f"configs[4] E={e} saved R {layer.edge_weight_bytes(graph) / 1e9:.2f} GB, "
-          f"peak device memory {peak / 1e9:.2f} GB", flush=True)
+    print(f"configs[4] E={e} peak device memory {peak / 1e9:.2f} GB", flush=True)
+    assert peak <= 12e9
     assert torch.equal(outs[0], outs[1]) and torch.equal(grads[0], grads[1])
     out, grad = outs[0], grads[0]
     # the forces sum to zero (translation invariance)
@@ -182,10 +192,3 @@ def test_config4_full_size(bm, dev):
     _, ref_grad = om.layer_and_position_grad(pos.numpy(), box, x.numpy(), src[sel].numpy(),
                                              dst[sel].numpy(), w1, b1, w2, 5.0, go.numpy())
     assert normwise_err(grad[sample], ref_grad[sample.numpy()]) <= 1e-4
-
-    # the backward that recomputes the per-edge weights gives the same forces
-    layer.save_edge_weights = False
-    p = pos.to(dev).requires_grad_(True)
-    o = layer(graph, p, x.to(dev))
-    o.backward(go.to(dev))
-    assert torch.equal(o.detach().cpu(), out) and torch.equal(p.grad.cpu(), grad)
