@@ -51,30 +51,6 @@ struct MaceBox {
     float inv[3];
 };
 
-// Bessel basis with envelope, and its derivative with respect to r.
-__device__ __forceinline__ void radial_basis(float r, float rc, float* B, float* dB) {
-    const float d = r / rc;
-    float f = 0.f, df = 0.f;
-    if (d < 1.0f) {
-        const float d5 = d * d * d * d * d, d6 = d5 * d;
-        f = 1.0f - 28.0f * d6 + 48.0f * d6 * d - 21.0f * d6 * d * d;
-        const float om = 1.0f - d;
-        df = -168.0f * d5 * om * om / rc;  // f'(d) / rc
-    }
-    const float norm = sqrtf(2.0f / rc);
-    const float ir = 1.0f / r;
-#pragma unroll
-    for (int k = 0; k < kNBasis; ++k) {
-        const float w = (float)(k + 1) * 3.14159265358979323846f / rc;
-        float sn, cs;
-        sincosf(w * r, &sn, &cs);
-        const float g = norm * sn * ir;                       // bare Bessel
-        const float dg = norm * (w * cs * ir - sn * ir * ir);  // its derivative
-        B[k] = g * f;
-        if (dB) dB[k] = dg * f + g * df;
-    }
-}
-
 __device__ __forceinline__ float sigmoidf(float z) { return 1.0f / (1.0f + expf(-z)); }
 
 // ---------------------------------------------------------------------------
@@ -299,12 +275,17 @@ __device__ __forceinline__ void mace_message(const float* Y, const float* xs, co
     });
 }
 
-// gy[b] = sum over the entries (a, b, o) of every path p of c x[a] R_p g[o],
-// by (l1, l_out) blocks: each product x[a] g[o] is formed once (256 per edge
-// and channel), the block's per-path sums U_p[b] = sum c x[a] g[o] (one path
-// per l2 within the block, so U is indexed by b) are scaled by R_p once.
-__device__ __forceinline__ void mace_grad_y(const float* xs, const float* g, const float* rr,
-                                            float* gy) {
+// The backward's two contractions of c x[a] Y[b] g[o], by (l1, l_out) blocks:
+// each product x[a] g[o] is formed once (256 per edge and channel) and summed
+// into the block's per-path U_p[b] = sum c x[a] g[o] (one path per l2 within the
+// block, so U is indexed by b); then
+//   gy[b] += R_p U_p[b]                      (the gradient of the pair's Y)
+//   path_grad(p, sum_b Y[b] U_p[b])         (gR_p = g . T_p(x, Y), the weight gradient)
+// so both come from the one set of U (1179 operations per edge and channel against
+// 2046 with T_p formed for gR_p separately).
+template <typename F>
+__device__ __forceinline__ void mace_grad_y(const float* xs, const float* g, const float* Y,
+                                            const float* rr, float* gy, F&& path_grad) {
     static_for<4>([&](auto l1c) {
         constexpr int L1 = decltype(l1c)::value;
         static_for<4>([&](auto loc) {
@@ -339,6 +320,10 @@ __device__ __forceinline__ void mace_grad_y(const float* xs, const float* g, con
                     for (int i = 0; i < 2 * l2 + 1; ++i)
                         gy[l2 * l2 + i] = L1 == 0 ? rr[p] * U[l2 * l2 + i]
                                                   : fmaf(rr[p], U[l2 * l2 + i], gy[l2 * l2 + i]);
+                    float gr = Y[l2 * l2] * U[l2 * l2];
+#pragma unroll
+                    for (int i = 1; i < 2 * l2 + 1; ++i) gr = fmaf(Y[l2 * l2 + i], U[l2 * l2 + i], gr);
+                    path_grad(std::integral_constant<int, p>{}, gr);
                 }
             });
         });
@@ -434,7 +419,8 @@ __global__ void mace_reverse_edges_kernel(const int64_t* __restrict__ row_ptr,
 // sequence of additions whatever the tiling, the order of the destinations or
 // the launch shape; each output row is written once, with no atomics.
 // ---------------------------------------------------------------------------
-constexpr int kMaceWaves = 4;                        // waves (position ranges) per workgroup
+constexpr int kMaceFwdWaves = 8;                     // waves (position ranges) per workgroup
+constexpr int kMaceBwdWaves = 4;
 constexpr int kPG = 9;                               // groups of 4 paths (36 slots)
 constexpr int kW2Row = kHidden + 4;                  // LDS row of sW, in floats
 constexpr int kW2Floats = kPG * 16 * kW2Row;         // 39,168 bytes per channel quad
@@ -477,10 +463,10 @@ __device__ __forceinline__ void mace_tile_weights(const float* sA, const float4*
     for (int p = 0; p < kNumPaths; ++p) rr[p] = acc[p >> 2][p & 3];
 }
 
-__device__ __forceinline__ float dpp_prev(float v) {  // lane e - 1 of the 16-lane row
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, false));
-}
-__device__ __forceinline__ int dpp_prev_i(int v) {
+// Lane reads within the 16-lane row.  Call them where every lane runs (a lane that
+// reads a lane skipped by a branch, e.g. the right side of a short-circuit ||,
+// gets no value).
+__device__ __forceinline__ int dpp_prev_i(int v) {  // lane e - 1
     return __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
 }
 __device__ __forceinline__ int dpp_next_i(int v) {  // lane e + 1 of the 16-lane row
@@ -507,53 +493,46 @@ __device__ __forceinline__ void mace_load_tile(const float4* __restrict__ u4,
     t.d = dstp[pos];
 }
 
-// Sum of the rows' messages v over each destination in ascending edge order
-// along the 16-lane row, with the carried running sum of a destination that
-// continues from the previous tile; writes every destination that closes in
-// the tile, and keeps the last one's running sum in sCarry.
-__device__ __forceinline__ void mace_scatter_tile(float* v, int d, bool valid, int e16, int kk,
-                                                  bool cok, int64_t c, int C, float* sCarry,
+// Sum of the tile's messages over each destination, in ascending edge order.
+// The 16 x 16 messages of a row (channel) go through LDS so that lane (row, o)
+// holds component o of all 16 edges; it adds them one after another into acc,
+// restarting at each destination's first edge (the tile's destination pattern
+// is the same on every row, so it is one scalar bit mask), and stores acc when a
+// destination closes.  acc carries a destination that continues into the next
+// tile.  sT: [row (272 floats)][edge (16)][component, in quads rotated by
+// edge / 4] (conflict-free 16-byte writes and 4-byte reads).
+constexpr int kTRow = 272;
+// messages to LDS: lane (row kk, edge e16) writes its 16 components
+__device__ __forceinline__ void mace_stage_tile(const float* v, int e16, int kk, float* sT) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(sT + kk * kTRow + e16 * 16 + 4 * ((i + (e16 >> 2)) & 3)) =
+            make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+__device__ __forceinline__ void mace_scatter_tile(int d, bool valid, int e16, int kk, bool cok,
+                                                  int64_t c, int C, const float* sT, float& acc,
                                                   int& carry_d, float* __restrict__ out) {
-    const int d0 = __builtin_amdgcn_readfirstlane(d);  // lane 0 of the tile is always valid
-    if (carry_d >= 0) {
-        float* cs = sCarry + kk * 16;
-        if (d0 == carry_d) {
-            if (e16 == 0) {
+    const int dp = dpp_prev_i(d), dn = dpp_next_i(d);
+    const uint64_t head = __ballot((e16 == 0) | (dp != d));
+    const uint64_t ends = __ballot(valid & (e16 < 15) & (dn != d));
+    const int d0 = __builtin_amdgcn_readfirstlane(d);  // lane 0 of a tile is always valid
+    // component o = e16 of row kk for all 16 edges
+    float col[16];
 #pragma unroll
-                for (int o = 0; o < 16; ++o) v[o] = cs[o] + v[o];
-            }
-        } else if (e16 == 0 && cok) {
-            float4* op = reinterpret_cast<float4*>(out + ((int64_t)carry_d * C + c) * 16);
+    for (int e = 0; e < 16; ++e)
+        col[e] = sT[kk * kTRow + e * 16 + 4 * (((e16 >> 2) + (e >> 2)) & 3) + (e16 & 3)];
+    float* orow = out + c * 16 + e16;  // + destination * C * 16
+    if (carry_d >= 0 && d0 != carry_d && cok) orow[(int64_t)carry_d * C * 16] = acc;
+    acc = (d0 == carry_d) ? acc + col[0] : col[0];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) op[q] = make_float4(cs[4 * q], cs[4 * q + 1], cs[4 * q + 2], cs[4 * q + 3]);
+    for (int e = 0; e < 16; ++e) {
+        if (e > 0) acc = ((head >> e) & 1) ? col[e] : acc + col[e];
+        if ((ends >> e) & 1) {
+            const int de = __builtin_amdgcn_readlane(d, e);
+            if (cok) orow[(int64_t)de * C * 16] = acc;
         }
     }
-    // the lane reads must run on every lane (a short-circuit || would put them in a
-    // branch that lane 0 skips, and a lane reading a skipped lane gets no value)
-    const int dp = dpp_prev_i(d);
-    const bool head = (e16 == 0) | (dp != d);
-#pragma unroll
-    for (int t = 1; t < 16; ++t) {
-        const bool take = e16 == t && !head;
-#pragma unroll
-        for (int o = 0; o < 16; ++o) {
-            const float pv = dpp_prev(v[o]);
-            v[o] = take ? v[o] + pv : v[o];
-        }
-    }
-    const int dn = dpp_next_i(d);
-    if (valid & (e16 < 15) & (dn != d) & cok) {
-        float4* op = reinterpret_cast<float4*>(out + ((int64_t)d * C + c) * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) op[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-    }
-    const int d15 = __builtin_amdgcn_readlane(d, 15);
-    if (d15 >= 0 && e16 == 15) {
-        float* cs = sCarry + kk * 16;
-#pragma unroll
-        for (int o = 0; o < 16; ++o) cs[o] = v[o];
-    }
-    carry_d = d15;  // -1: the tile's last lane is past the range (nothing to carry)
+    carry_d = __builtin_amdgcn_readlane(d, 15);  // -1: the tile's last lane is past the range
 }
 
 // Workgroup -> (channel quad, position range): consecutive workgroup ids go to
@@ -562,35 +541,38 @@ __device__ __forceinline__ void mace_scatter_tile(float* v, int d, bool valid, i
 struct MaceWg {
     int quad, wave_range;
 };
+template <int WAVES>
 __device__ __forceinline__ MaceWg mace_wg(int n_quads, int ranges_per_xcd) {
     const int bid = blockIdx.x, xcd = bid & 7, k = bid >> 3;
     MaceWg w;
     w.quad = k % n_quads;
-    w.wave_range = ((xcd * ranges_per_xcd + k / n_quads) * kMaceWaves) + (threadIdx.x >> 6);
+    w.wave_range = ((xcd * ranges_per_xcd + k / n_quads) * WAVES) + (threadIdx.x >> 6);
     return w;
 }
 
 // out[d, c, :] = sum_{e -> d} sum_p R[e, c, p] T_p(x[src_e, c], Y(u_e)) for every
 // destination with an edge (out of the others is zeroed by the caller).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void mace_fused_forward_kernel(
-    const float4* __restrict__ u4, const int* __restrict__ srcp, const int* __restrict__ dstp,
-    const float* __restrict__ h, const float* __restrict__ w2, const float* __restrict__ x,
-    const int64_t* __restrict__ wstart, float* __restrict__ out, int C, int n_quads,
-    int ranges_per_xcd) {
+__global__ __launch_bounds__(64 * kMaceFwdWaves) __attribute__((amdgpu_waves_per_eu(4))) void
+mace_fused_forward_kernel(const float4* __restrict__ u4, const int* __restrict__ srcp,
+                          const int* __restrict__ dstp, const float* __restrict__ h,
+                          const float* __restrict__ w2, const float* __restrict__ x,
+                          const int64_t* __restrict__ wstart, float* __restrict__ out, int C,
+                          int n_quads, int ranges_per_xcd) {
     __shared__ __attribute__((aligned(16))) float sW[kW2Floats];
-    __shared__ __attribute__((aligned(16))) float sCarryAll[kMaceWaves * 4 * 16];
-    const MaceWg wg = mace_wg(n_quads, ranges_per_xcd);
+    __shared__ __attribute__((aligned(16))) float sTAll[kMaceFwdWaves * 4 * kTRow];
+    const MaceWg wg = mace_wg<kMaceFwdWaves>(n_quads, ranges_per_xcd);
     const int lane = threadIdx.x & 63, e16 = lane & 15, kk = lane >> 4;
     const int c0 = wg.quad * 4;
     mace_fill_w2(w2, C, c0, sW);
     __syncthreads();
-    float* sCarry = sCarryAll + (threadIdx.x >> 6) * 64;
+    float* sT = sTAll + (threadIdx.x >> 6) * 4 * kTRow;
     const int64_t p0 = wstart[wg.wave_range], p1 = wstart[wg.wave_range + 1];
     const int c = c0 + kk;
     const bool cok = c < C;
     const int cc = cok ? c : C - 1;
     const float* sA = sW + (lane & 15) * kW2Row + 4 * kk;
     int carry_d = -1;
+    float acc = 0.0f;
     MaceTileIn cur;
     if (p0 < p1) mace_load_tile(u4, srcp, dstp, h, min(p0 + e16, p1 - 1), kk, cur);
     for (int64_t t0 = p0; t0 < p1; t0 += 16) {
@@ -604,26 +586,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void m
         }
         float rr[kNumPaths];
         mace_tile_weights(sA, cur.hb, rr);
-        // the next tile's operands, in flight during this tile's products
-        MaceTileIn nxt;
-        const int64_t t1 = t0 + 16;
-        mace_load_tile(u4, srcp, dstp, h, t1 < p1 ? min(t1 + e16, p1 - 1) : p1 - 1, kk, nxt);
         float Y[16];
         sh_forward<3>(cur.u.x, cur.u.y, cur.u.z, Y);
         float m[16];
 #pragma unroll
         for (int o = 0; o < 16; ++o) m[o] = 0.0f;
         mace_message(Y, xs, rr, m);
-        mace_scatter_tile(m, valid ? cur.d : -1, valid, e16, kk, cok, c, C, sCarry, carry_d,
-                          out);
-        cur = nxt;
+        mace_stage_tile(m, e16, kk, sT);
+        const int dcur = valid ? cur.d : -1;
+        // the next tile's operands (the other waves of the SIMD cover their latency)
+        const int64_t t1 = t0 + 16;
+        mace_load_tile(u4, srcp, dstp, h, t1 < p1 ? min(t1 + e16, p1 - 1) : p1 - 1, kk, cur);
+        mace_scatter_tile(dcur, valid, e16, kk, cok, c, C, sT, acc, carry_d, out);
     }
-    if (carry_d >= 0 && e16 == 0 && cok) {
-        const float* cs = sCarry + kk * 16;
-        float4* op = reinterpret_cast<float4*>(out + ((int64_t)carry_d * C + c) * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) op[q] = make_float4(cs[4 * q], cs[4 * q + 1], cs[4 * q + 2], cs[4 * q + 3]);
-    }
+    if (carry_d >= 0 && cok) out[((int64_t)carry_d * C + c) * 16 + e16] = acc;
 }
 
 // Backward: per pair, gR_p = sum_o g[d, c, o] T_p[o] feeds the MLP's transpose GEMM
@@ -634,14 +610,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void m
 //   g_v = g_r u + (g_u - u (u . g_u)) / r,  g_r = sum_k D[k][e] s[e][k],
 //   g_u = SH backward of gY at u,
 // with s[e][k] = silu'(z_k) sum_b W1[b][k] dB_b/dr, goes to gv_part[quad][position].
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mace_fused_backward_kernel(
+__global__ __launch_bounds__(64 * kMaceBwdWaves) __attribute__((amdgpu_waves_per_eu(3))) void mace_fused_backward_kernel(
     const float4* __restrict__ u4, const int* __restrict__ srcp, const int* __restrict__ dstp,
     const float* __restrict__ h, const float* __restrict__ sg, const float* __restrict__ w2,
     const float* __restrict__ x, const float* __restrict__ gout,
     const int64_t* __restrict__ wstart, float* __restrict__ gv_part, int64_t n_pos, int C,
     int n_quads, int ranges_per_xcd) {
     __shared__ __attribute__((aligned(16))) float sW[kW2Floats];
-    const MaceWg wg = mace_wg(n_quads, ranges_per_xcd);
+    const MaceWg wg = mace_wg<kMaceBwdWaves>(n_quads, ranges_per_xcd);
     const int lane = threadIdx.x & 63, e16 = lane & 15, kk = lane >> 4;
     const int c0 = wg.quad * 4;
     mace_fill_w2(w2, C, c0, sW);
@@ -671,6 +647,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
 #pragma unroll
             for (int o = 0; o < 16; ++o) g[o] = 0.0f;
         }
+        float Y[16];
+        sh_forward<3>(cur.u.x, cur.u.y, cur.u.z, Y);
+        // gY of the pair, and gR_p = g . T_p per path straight into the transpose GEMM
+        v4f gh[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gh[j] = v4f{0.f, 0.f, 0.f, 0.f};
+        float gy[16];
+        // (W2 read per tile through an opaque base, as in mace_tile_weights)
+        int wbase = 0;
+        asm volatile("" : "+v"(wbase));
+        const float* sWt = sW + wbase;
+        mace_grad_y(xs, g, Y, rr, gy, [&](auto pp, float gr) {
+            constexpr int p = decltype(pp)::value;
+            const float* a = sWt + ((p >> 2) * 16 + 4 * kk + (p & 3)) * kW2Row + e16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) gh[j] = mfma1(a[16 * j], gr, gh[j]);
+        });
+        // the next tile's operands and this tile's s, in flight during the reductions
         MaceTileIn nxt;
         const int64_t t1 = t0 + 16;
         mace_load_tile(u4, srcp, dstp, h, t1 < p1 ? min(t1 + e16, p1 - 1) : p1 - 1, kk, nxt);
@@ -678,28 +672,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
         float4 sv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) sv[j] = sr[4 * j];
-        float Y[16];
-        sh_forward<3>(cur.u.x, cur.u.y, cur.u.z, Y);
-        // gR_p = g . T_p per path, straight into the transpose GEMM
-        v4f gh[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) gh[j] = v4f{0.f, 0.f, 0.f, 0.f};
-        for_blocks<0>([&](auto b0, auto b1) {
-            block_products<decltype(b0)::value, decltype(b1)::value>(
-                Y, xs, [&](auto pp, const float* tq) {
-                    constexpr int p = decltype(pp)::value;
-                    constexpr int lo = kPathL[p][2];
-                    float gr = g[lo * lo] * tq[0];
-#pragma unroll
-                    for (int q = 1; q < 2 * lo + 1; ++q) gr = fmaf(g[lo * lo + q], tq[q], gr);
-                    const float* a = sW + ((p >> 2) * 16 + 4 * kk + (p & 3)) * kW2Row + e16;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) gh[j] = mfma1(a[16 * j], gr, gh[j]);
-                });
-        });
-        // gY of the pair, summed over the quad's channels (rows of the wave)
-        float gy[16];
-        mace_grad_y(xs, g, rr, gy);
+        // summed over the quad's channels (rows of the wave)
 #pragma unroll
         for (int b = 0; b < 16; ++b) {
             gy[b] += __shfl_xor(gy[b], 16, 64);
@@ -782,6 +755,10 @@ __global__ void mace_worker_starts_kernel(const int64_t* __restrict__ pos0, int6
 
 // Per position p (edge e = perm[p]): unit vector and length, source, destination,
 // h = silu(B(r) W1 + b1); with sg, also s[k] = silu'(z_k) sum_b W1[b][k] dB_b/dr.
+// Sixteen lanes per position: lane q evaluates Bessel function q % 8 (one sincos)
+// and shares it with the position's other lanes, then forms hidden units
+// 4q .. 4q + 3, so every store instruction writes whole 256-byte rows.
+constexpr int kPrepPositions = 16;  // positions per 256-thread workgroup
 __global__ __launch_bounds__(256) void mace_prep_kernel(
     const float* __restrict__ pos, MaceBox bx, const int64_t* __restrict__ src,
     const int64_t* __restrict__ dst, const int64_t* __restrict__ perm,
@@ -792,41 +769,64 @@ __global__ __launch_bounds__(256) void mace_prep_kernel(
     for (int i = threadIdx.x; i < kNBasis * kHidden + kHidden; i += blockDim.x)
         sW[i] = i < kNBasis * kHidden ? w1[i] : b1[i - kNBasis * kHidden];
     __syncthreads();
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= n_edges) return;
+    const int q = threadIdx.x & 15;
+    int64_t p = (int64_t)blockIdx.x * kPrepPositions + (threadIdx.x >> 4);
+    const bool valid = p < n_edges;
+    p = valid ? p : n_edges - 1;  // every lane takes part in the shuffles below
     int64_t e = perm[p];
     e = e < 0 ? 0 : (e >= n_edges ? n_edges - 1 : e);
     const int64_t s = src[e], d = dst[e];
     float v[3];
     edge_vector(pos, s, d, bx.box, bx.inv, v);
     const float r = normalize3(v[0], v[1], v[2]);
-    u4[p] = make_float4(v[0], v[1], v[2], r);
-    srcp[p] = (int)s;
-    dstp[p] = (int)d;
+    if (valid && q == 0) {
+        u4[p] = make_float4(v[0], v[1], v[2], r);
+        srcp[p] = (int)s;
+        dstp[p] = (int)d;
+    }
+    // Bessel function k = q % 8 of this position, with the envelope
+    const float dd = r / rc;
+    float f = 0.f, df = 0.f;
+    if (dd < 1.0f) {
+        const float d5 = dd * dd * dd * dd * dd, d6 = d5 * dd;
+        f = 1.0f - 28.0f * d6 + 48.0f * d6 * dd - 21.0f * d6 * dd * dd;
+        const float om = 1.0f - dd;
+        df = -168.0f * d5 * om * om / rc;
+    }
+    const float norm = sqrtf(2.0f / rc), ir = 1.0f / r;
+    const float w = (float)((q & 7) + 1) * 3.14159265358979323846f / rc;
+    float sn, cs;
+    sincosf(w * r, &sn, &cs);
+    const float gk = norm * sn * ir;
+    const float bk = gk * f;
+    const float dbk = sg ? (norm * (w * cs * ir - sn * ir * ir)) * f + gk * df : 0.0f;
+    const int base = (threadIdx.x & 63) & ~15;
     float B[kNBasis], dB[kNBasis];
-    radial_basis(r, rc, B, sg ? dB : nullptr);
-    float4* ho = reinterpret_cast<float4*>(h + p * kHidden);
-    float4* so = sg ? reinterpret_cast<float4*>(sg + p * kHidden) : nullptr;
 #pragma unroll
-    for (int j4 = 0; j4 < kHidden / 4; ++j4) {
-        float z[4], sd[4];
+    for (int k = 0; k < kNBasis; ++k) B[k] = __shfl(bk, base + k, 64);
+    if (sg) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int j = j4 * 4 + t;
-            float acc = sW[kNBasis * kHidden + j];
+        for (int k = 0; k < kNBasis; ++k) dB[k] = __shfl(dbk, base + k, 64);
+    }
+    float z[4], sd[4];
 #pragma unroll
-            for (int k = 0; k < kNBasis; ++k) acc = fmaf(B[k], sW[k * kHidden + j], acc);
-            const float sgm = sigmoidf(acc);
-            z[t] = acc * sgm;
-            if (sg) {
-                float q = 0.0f;
+    for (int t = 0; t < 4; ++t) {
+        const int j = 4 * q + t;
+        float acc = sW[kNBasis * kHidden + j];
 #pragma unroll
-                for (int k = 0; k < kNBasis; ++k) q = fmaf(sW[k * kHidden + j], dB[k], q);
-                sd[t] = sgm * (1.0f + acc * (1.0f - sgm)) * q;
-            }
+        for (int k = 0; k < kNBasis; ++k) acc = fmaf(B[k], sW[k * kHidden + j], acc);
+        const float sgm = sigmoidf(acc);
+        z[t] = acc * sgm;
+        if (sg) {
+            float qq = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kNBasis; ++k) qq = fmaf(sW[k * kHidden + j], dB[k], qq);
+            sd[t] = sgm * (1.0f + acc * (1.0f - sgm)) * qq;
         }
-        ho[j4] = make_float4(z[0], z[1], z[2], z[3]);
-        if (sg) so[j4] = make_float4(sd[0], sd[1], sd[2], sd[3]);
+    }
+    if (valid) {
+        reinterpret_cast<float4*>(h + p * kHidden)[q] = make_float4(z[0], z[1], z[2], z[3]);
+        if (sg) reinterpret_cast<float4*>(sg + p * kHidden)[q] = make_float4(sd[0], sd[1], sd[2], sd[3]);
     }
 }
 
@@ -943,14 +943,15 @@ struct MaceShape {
 };
 
 template <typename K>
-static int mace_shape(K kernel, int C, MaceShape* sh) {
+static int mace_shape(K kernel, int waves, int C, MaceShape* sh) {
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess || occ < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 64 * waves, 0) != hipSuccess ||
+        occ < 1)
         occ = 1;
     const int per_xcd = std::max(1, mace_cu_count() / 8);
     sh->n_quads = mace_quads(C);
     sh->ranges_per_xcd = std::max(1, per_xcd * occ / sh->n_quads);
-    sh->n_workers = 8 * sh->ranges_per_xcd * kMaceWaves;
+    sh->n_workers = 8 * sh->ranges_per_xcd * waves;
     if (sh->n_workers > kMaceMaxWorkers) return BM_ERR_ARG;
     sh->grid = (unsigned)(8 * sh->ranges_per_xcd * sh->n_quads);
     return BM_OK;
@@ -970,7 +971,7 @@ static int mace_prepare(const float* positions, const MaceBox& bx, const float* 
     mace_positions_kernel<<<nb, 256, 0, stream>>>(row_ptr, order, w.pos0, N, E, w.perm);
     mace_worker_starts_kernel<<<(unsigned)ceil_div(sh.n_workers + 1, 256), 256, 0, stream>>>(
         w.pos0, N, E, sh.n_workers, w.wstart);
-    mace_prep_kernel<<<(unsigned)ceil_div(E, 256), 256, 0, stream>>>(
+    mace_prep_kernel<<<(unsigned)ceil_div(E, kPrepPositions), 256, 0, stream>>>(
         positions, bx, src, dst, w.perm, w1, b1, cutoff, E, w.u4, w.srcp, w.dstp, w.h,
         backward ? w.sg : nullptr);
     return (int)hipGetLastError();
@@ -1037,12 +1038,12 @@ extern "C" int batteries_mace_forward(const float* positions, const float* box,
         row_ptr, N, C, reinterpret_cast<float4*>(out));
     if (N_edges == 0) return (int)hipGetLastError();
     MaceShape sh;
-    int rc = mace_shape(mace_fused_forward_kernel, C, &sh);
+    int rc = mace_shape(mace_fused_forward_kernel, kMaceFwdWaves, C, &sh);
     if (rc != BM_OK) return rc;
     rc = mace_prepare(positions, mace_box(box), w1, b1, src, dst, row_ptr, order, N, N_edges,
                       cutoff, sh, w, false, stream);
     if (rc != BM_OK) return rc;
-    mace_fused_forward_kernel<<<sh.grid, 256, 0, stream>>>(w.u4, w.srcp, w.dstp, w.h, w2,
+    mace_fused_forward_kernel<<<sh.grid, 64 * kMaceFwdWaves, 0, stream>>>(w.u4, w.srcp, w.dstp, w.h, w2,
                                                             node_features, w.wstart, out, C,
                                                             sh.n_quads, sh.ranges_per_xcd);
     return (int)hipGetLastError();
@@ -1067,12 +1068,12 @@ extern "C" int batteries_mace_backward(const float* positions, const float* box,
         return (int)hipGetLastError();
     }
     MaceShape sh;
-    int rc = mace_shape(mace_fused_backward_kernel, C, &sh);
+    int rc = mace_shape(mace_fused_backward_kernel, kMaceBwdWaves, C, &sh);
     if (rc != BM_OK) return rc;
     rc = mace_prepare(positions, mace_box(box), w1, b1, src, dst, row_ptr, order, N, N_edges,
                       cutoff, sh, w, true, stream);
     if (rc != BM_OK) return rc;
-    mace_fused_backward_kernel<<<sh.grid, 256, 0, stream>>>(
+    mace_fused_backward_kernel<<<sh.grid, 64 * kMaceBwdWaves, 0, stream>>>(
         w.u4, w.srcp, w.dstp, w.h, w.sg, w2, node_features, grad_out, w.wstart, w.gv_part,
         N_edges, C, sh.n_quads, sh.ranges_per_xcd);
     mace_gv_reduce_kernel<<<(unsigned)ceil_div(N_edges, 256), 256, 0, stream>>>(
