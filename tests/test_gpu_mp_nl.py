@@ -108,6 +108,23 @@ def test_edge_index_to_csr(bm, dev):
     assert rp0.cpu().tolist() == [0] * 8 and ci0.numel() == 0
 
 
+def test_edge_index_to_csr_row_lengths(bm, dev):
+    """Rows of 1, 63, 64, 65, 300 (several register chunks per lane) and 600 entries (past
+    the register sort) next to random short rows, edges in a shuffled order: bit-exact
+    against the stable sort of the oracle."""
+    n = 200
+    tgt = torch.cat([torch.full((600,), 0), torch.full((300,), 1), torch.full((64,), 2),
+                     torch.full((65,), 3), torch.full((63,), 4), torch.full((1,), 5),
+                     torch.randint(6, n, (5000,), generator=gen(61))])
+    tgt = tgt[torch.randperm(tgt.numel(), generator=gen(62))]
+    src = torch.randint(0, n, (tgt.numel(),), generator=gen(63))
+    ei = torch.stack([src, tgt])
+    rp, ci = bm.edge_index_to_csr(ei.to(dev), n)
+    wrp, wci = omp.edge_index_to_csr(ei.numpy(), n)
+    np.testing.assert_array_equal(rp.cpu().numpy(), wrp)
+    np.testing.assert_array_equal(ci.cpu().numpy(), wci)
+
+
 def test_fused_message_passing_simple(bm, dev):
     n, e, c = 400, 8000, 32
     vec, x, src, dst = _random_graph(n, e, c, 21)
