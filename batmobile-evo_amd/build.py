@@ -29,7 +29,7 @@ LIB = os.path.join(LIBDIR, "libbatmobile_hip.so")
 NL_LIB = os.path.join(LIBDIR, "libbatteries_neighbor.so")
 EXT = os.path.join(PYDIR, "_batmobile" + sysconfig.get_config_var("EXT_SUFFIX"))
 
-HIP_SOURCES = ["sh.hip", "tp.hip", "mp.hip", "nl.hip", "mace.hip"]
+HIP_SOURCES = ["sh.hip", "tp.hip", "mp.hip", "nl.hip", "graph.hip", "mace.hip"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"

@@ -749,6 +749,71 @@ neighbor_graph_capacity(const torch::Tensor& positions, const torch::Tensor& cel
     return {src, dst, vec, offsets, order, overflow};
 }
 
+// Extension for batmobile.Graph: the whole build (neighbor list in the message-passing
+// layout, spatial order, schedule) by batteries_graph_build_count / _write, for the
+// systems within its limits; None otherwise (the caller then uses neighbor_graph and
+// mp_schedule, which give the same results).  max_edges < 0: arrays of exactly E edges
+// (one host synchronisation for E); else arrays of max_edges edges, no host
+// synchronisation, overflow [1] int32 as in neighbor_graph_capacity.
+// Returns (src, dst, edge_vectors, row_offsets, order, row_ptr_s, edge_perm, row_dst,
+// n_blocks, rows_per_block, overflow or None).
+pybind11::object graph_build(const torch::Tensor& positions, const torch::Tensor& cell,
+                             double cutoff, bool self_loops, int64_t C, int64_t max_edges,
+                             int64_t row_capacity) {
+    TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
+    TORCH_CHECK(positions.dtype() == torch::kFloat32, "positions must be float32");
+    TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
+    TORCH_CHECK(C > 0 && C <= INT32_MAX, "C must be positive");
+    TORCH_CHECK(row_capacity >= 0 && row_capacity <= 1 << 20, "row_capacity out of range");
+    check_device(positions, "positions");
+    const int64_t N = positions.size(0);
+    torch::Tensor cell_cpu = cell.detach().to(torch::kCPU, torch::kFloat32).contiguous();
+    const float* h = cell_cpu.data_ptr<float>();
+    const float box[3] = {h[0], h[4], h[8]};
+    const float rc = (float)cutoff;
+    const size_t wsb = batteries_graph_build_workspace_bytes(N, box, rc, (int)C, (int)row_capacity);
+    if (wsb == 0) return pybind11::none();
+    int nb = 0, rpb = 0;
+    check_status(batteries_mp_schedule_shape(N, (int)C, &nb, &rpb), "graph_build");
+    const int64_t ns = (int64_t)nb * rpb;
+    auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(positions.device());
+    auto i32 = torch::TensorOptions().dtype(torch::kInt32).device(positions.device());
+    const c10::DeviceGuard guard(positions.device());
+    hipStream_t s = current_stream(positions);
+    torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
+    // the per-atom and per-slot results in one allocation
+    torch::Tensor meta = torch::empty({(N + 1) + N + (ns + 1) + ns}, i64);
+    torch::Tensor row_ptr = meta.narrow(0, 0, N + 1);
+    torch::Tensor order = meta.narrow(0, N + 1, N);
+    torch::Tensor rps = meta.narrow(0, 2 * N + 1, ns + 1);
+    torch::Tensor rdst = meta.narrow(0, 2 * N + 2 + ns, ns);
+    torch::Tensor overflow = torch::empty({1}, i32);
+    check_status(batteries_graph_build_count(
+                     cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0, (int)C,
+                     nb, rpb, max_edges, (int)row_capacity, ws.data_ptr(), wsb,
+                     row_ptr.data_ptr<int64_t>(), order.data_ptr<int64_t>(),
+                     rps.data_ptr<int64_t>(), rdst.data_ptr<int64_t>(), overflow.data_ptr<int>(),
+                     s),
+                 "graph_build");
+    const int64_t E = max_edges < 0 ? row_ptr[N].item<int64_t>() : max_edges;  // exact: one sync
+    torch::Tensor eidx = torch::empty({3 * E}, i64);  // src | dst | edge_perm
+    torch::Tensor src = eidx.narrow(0, 0, E);
+    torch::Tensor dst = eidx.narrow(0, E, E);
+    torch::Tensor ep = eidx.narrow(0, 2 * E, E);
+    torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
+    if (E > 0)
+        check_status(batteries_graph_build_write(
+                         cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
+                         (int)row_capacity, ws.data_ptr(), wsb, row_ptr.data_ptr<int64_t>(),
+                         overflow.data_ptr<int>(), src.data_ptr<int64_t>(),
+                         dst.data_ptr<int64_t>(), vec.data_ptr<float>(),
+                         ep.data_ptr<int64_t>(), s),
+                     "graph_build");
+    pybind11::object ov = max_edges < 0 ? pybind11::none() : pybind11::cast(overflow);
+    return pybind11::make_tuple(src, dst, vec, row_ptr, order, rps, ep, rdst, (int64_t)nb,
+                                (int64_t)rpb, ov);
+}
+
 torch::Tensor selftest_mfma_16x16x4(const torch::Tensor& A, const torch::Tensor& B) {
     TORCH_CHECK(A.numel() == 64 && B.numel() == 64 && A.dtype() == torch::kFloat32 &&
                     B.dtype() == torch::kFloat32,
@@ -978,6 +1043,12 @@ PYBIND11_MODULE(_batmobile, m) {
           "(src, dst, edge_vectors, row_offsets, order, overflow); the edge count is "
           "row_offsets[-1] on the device, overflow [1] is 1 (and every row empty) when it "
           "exceeded the capacity");
+    m.def("graph_build", &graph_build, py::arg("positions"), py::arg("cell"), py::arg("cutoff"),
+          py::arg("self_loops"), py::arg("C"), py::arg("max_edges") = -1,
+          py::arg("row_capacity") = 0,
+          "batmobile.Graph's build in four kernels (None outside its limits): (src, dst, "
+          "edge_vectors, row_offsets, order, row_ptr_s, edge_perm, row_dst, n_blocks, "
+          "rows_per_block, overflow or None)");
     m.def("mp_schedule", &mp_schedule, py::arg("row_ptr"), py::arg("order"), py::arg("C"),
           py::arg("col_perm") = py::none(), py::arg("num_edges") = -1,
           "Spatial processing schedule for sh_tp_scatter_scheduled: "

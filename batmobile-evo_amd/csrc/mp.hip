@@ -21,6 +21,7 @@
 //   without atomics, in a fixed order: results are deterministic.
 #include "common.h"
 #include "batmobile_hip.h"
+#include "mp_schedule.h"
 
 namespace bmhip {
 
@@ -360,7 +361,6 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kSBatch = 64;       // edges per batch (operators in LDS, one edge per lane in phase 1)
 constexpr int kRing = 32;         // gathers in flight per lane (edges ahead)
-constexpr int kScatterRows = 11;  // row slots per workgroup
 constexpr int kStageSlots = 3;    // rows staged per wave between two flushes
 constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
@@ -810,6 +810,12 @@ static int blocks_per_xcd(int C) {
     return std::max(1, 2 * device_cu_count() / groups / 8);
 }
 
+// Workgroups of one schedule group (mp_schedule.h): the workgroups resident on an XCD
+// at once, at most one wave's lanes.
+int bmhip::schedule_group_size(int n_blocks, int C) {
+    return std::min(std::min(n_blocks / 8, blocks_per_xcd(C)), kSchedMaxQ);
+}
+
 // Launch with an explicit split: n_logical workgroups (a multiple of 8), each
 // owning `per` consecutive destinations (SCATTER) or edges (MESSAGES).
 static int launch_mp(bool scatter, bool norm, const float* vec, const float* X, int64_t n_src,
@@ -975,35 +981,11 @@ extern "C" int batteries_edge_index_to_csr(const int64_t* edge_index, int64_t* r
 }
 
 // ---------------------------------------------------------------------------
-// Destination schedule: the fused scatter kernel runs n_blocks workgroups of
-// rows_per_block (R) row slots; slot t of workgroup b is scheduled row
-// q = b * R + t.  Workgroup b = x * P + k runs on XCD x (P = n_blocks / 8), and
-// the workgroups of an XCD run in generations of Q resident ones.
-//
-//   - Each (XCD, generation) group owns a contiguous range of the spatial
-//     order, cut so that every group holds edges in proportion to its number
-//     of workgroups (at most Qg * R rows).
-//   - Inside a group the rows are dealt in slices of Qg consecutive spatial
-//     positions: slice t goes to slot t of the group's workgroups, so the rows
-//     in flight on an XCD at one time stay spatially compact and their source
-//     rows stay in L2.  Within a slice the heaviest row goes to the lightest
-//     workgroup so far; a few rounds of pairwise swaps inside slices (the i-th
-//     heaviest workgroup with the i-th lightest) then even out the totals.
-//
-// The kernel time is that of the busiest compute unit, so equal edge counts
-// per workgroup matter: at configs[3] this brings the largest workgroup from
-// 361 edges (fixed rows per workgroup) to within a few percent of the mean.
-// Every destination is still summed by one wave in ascending edge order, so
-// the result does not depend on the schedule.
+// Destination schedule (the layout and the balancing are described in mp_schedule.h):
+// degrees in processing order, their running sums and the group bounds, then one
+// wave per group balances the group's workgroups, then edge_perm.
 // ---------------------------------------------------------------------------
 namespace bmhip {
-
-constexpr int kSchedMaxQ = 256;       // workgroups of one group (threads of the balancing block)
-// Swap rounds after the dealing.  At configs[3] the largest workgroup stops shrinking
-// after four (314 edges against a mean of 294 in a host simulation of the rounds; swaps
-// still happen after that but only between workgroups below the largest), and each round
-// costs about 1.25 us of the balancing kernel (21.6 us with eight rounds, 16.6 with four).
-constexpr int kSchedSwapRounds = 4;
 
 // degm[m] = in-degree of destination order[m]
 __global__ void sched_degm_kernel(const int64_t* __restrict__ row_ptr,
@@ -1015,48 +997,21 @@ __global__ void sched_degm_kernel(const int64_t* __restrict__ row_ptr,
     degm[m] = (d >= 0 && d < n_dst) ? row_ptr[d + 1] - row_ptr[d] : 0;
 }
 
-// Group boundaries gb[0 .. 8G] in spatial positions.  First every group's
-// end is placed where the cumulative edge count reaches its share (one
-// thread per group), then one thread clamps the ends in order so that every
-// group fits its Qg * R slots and leaves room for the later groups.
+// Group boundaries gb[0 .. 8G] in spatial positions: every group's target end (one
+// thread per group), then one thread clamps the ends in order.
 __global__ void sched_group_targets_kernel(const int64_t* __restrict__ cum, int64_t n_dst, int P,
                                            int Q, int64_t* __restrict__ gb) {
     const int G = (P + Q - 1) / Q;
     const int gi = blockIdx.x * blockDim.x + threadIdx.x;
     if (gi >= 8 * G) return;
-    const int x = gi / G, gen = gi - x * G;
-    const int Qg = min(Q, P - gen * Q);
-    const int64_t E = cum[n_dst];
-    const int64_t w_end = (int64_t)x * P + (int64_t)gen * Q + Qg;
-    const double target = (double)E * (double)w_end / (8.0 * (double)P);
-    // first position whose cumulative edge count reaches the target, or the
-    // one before it when that is closer
-    int64_t lo = 0, hi = n_dst;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if ((double)cum[mid] < target) lo = mid + 1;
-        else hi = mid;
-    }
-    if (lo > 0 && target - (double)cum[lo - 1] < (double)cum[lo] - target) --lo;
-    gb[gi + 1] = lo;
+    gb[gi + 1] = sched_group_target(gi, P, Q, n_dst, (double)cum[n_dst],
+                                    [&](int64_t m) { return cum[m]; });
 }
 
 __global__ void sched_groups_kernel(int64_t n_dst, int P, int Q, int R, int64_t* __restrict__ gb) {
     if (blockIdx.x != 0 || threadIdx.x != 0) return;
-    const int G = (P + Q - 1) / Q;
-    const int64_t total_wg = 8LL * P;
-    int64_t start = 0;
-    gb[0] = 0;
-    for (int gi = 0; gi < 8 * G; ++gi) {
-        const int gen = gi % G;
-        const int Qg = min(Q, P - gen * Q);
-        const int64_t w_end = (int64_t)(gi / G) * P + (int64_t)gen * Q + Qg;
-        const int64_t low = max(start, n_dst - (total_wg - w_end) * (int64_t)R);
-        const int64_t high = min(n_dst, start + (int64_t)Qg * R);
-        const int64_t pos = max(low, min(high, gb[gi + 1]));
-        gb[gi + 1] = pos;
-        start = pos;
-    }
+    sched_clamp_groups(P, Q, R, n_dst, [&](int gi) { return gb[gi + 1]; },
+                       [&](int i, int64_t v) { gb[i] = v; });
 }
 
 // The scan, sched_group_targets_kernel and sched_groups_kernel in one workgroup, for up
@@ -1064,9 +1019,8 @@ __global__ void sched_groups_kernel(int64_t n_dst, int P, int Q, int R, int64_t*
 // degm (from sched_degm_kernel, which spreads its scattered row_ptr reads over many
 // compute units) is read with coalesced loads into LDS, summed there in int32 (and
 // written out as cum, as the scan would), and the group targets and the clamp read the
-// sums from LDS.  The sums are exact in int32, and
-// the targets compare the same values in double as sched_group_targets_kernel, so gb is
-// the same as the three kernels'.
+// sums from LDS.  The sums are exact in int32, and the targets compare the same values
+// in double as sched_group_targets_kernel, so gb is the same as the three kernels'.
 constexpr int kPrepThreads = 1024;
 constexpr int kPrepPer = 16;
 constexpr int kPrepMaxDst = kPrepThreads * kPrepPer;
@@ -1128,393 +1082,36 @@ __global__ __launch_bounds__(kPrepThreads) void sched_prep_kernel(
     __syncthreads();
     // the sums to global memory for the balancing kernel (coalesced)
     for (int i = t; i <= n; i += kPrepThreads) cum[i] = sCum[i];
-    // group ends where the cumulative edge count reaches each group's share
     const int G = (P + Q - 1) / Q;
-    const double E = (double)total;
-    for (int gi = t; gi < 8 * G; gi += kPrepThreads) {
-        const int xg = gi / G, gen = gi - xg * G;
-        const int Qg = min(Q, P - gen * Q);
-        const int64_t w_end = (int64_t)xg * P + (int64_t)gen * Q + Qg;
-        const double target = E * (double)w_end / (8.0 * (double)P);
-        int lo = 0, hi = n;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if ((double)sCum[mid] < target) lo = mid + 1;
-            else hi = mid;
-        }
-        if (lo > 0 && target - (double)sCum[lo - 1] < (double)sCum[lo] - target) --lo;
-        sPos[gi] = lo;
-    }
+    for (int gi = t; gi < 8 * G; gi += kPrepThreads)
+        sPos[gi] = (int)sched_group_target(gi, P, Q, n_dst, (double)total,
+                                           [&](int64_t m) { return (int64_t)sCum[m]; });
     __syncthreads();
-    // the clamp, in group order (every group fits its slots and leaves room for the rest)
-    if (t == 0) {
-        const int64_t total_wg = 8LL * P;
-        int64_t start = 0;
-        gb[0] = 0;
-        for (int gi = 0; gi < 8 * G; ++gi) {
-            const int gen = gi % G;
-            const int Qg = min(Q, P - gen * Q);
-            const int64_t w_end = (int64_t)(gi / G) * P + (int64_t)gen * Q + Qg;
-            const int64_t low = max(start, n_dst - (total_wg - w_end) * (int64_t)R);
-            const int64_t high = min(n_dst, start + (int64_t)Qg * R);
-            const int64_t pos = max(low, min(high, (int64_t)sPos[gi]));
-            gb[gi + 1] = pos;
-            start = pos;
-        }
-    }
+    if (t == 0)
+        sched_clamp_groups(P, Q, R, n_dst, [&](int gi) { return (int64_t)sPos[gi]; },
+                           [&](int i, int64_t v) { gb[i] = v; });
 }
 
-// One block per group: deal the group's rows to its workgroups' slots.
-__global__ __launch_bounds__(kSchedMaxQ) void sched_balance_kernel(
+// One wave per group, kBalGroups groups per workgroup.
+constexpr int kBalGroups = 4;
+__global__ __launch_bounds__(64 * kBalGroups) void sched_balance_kernel(
     const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
     const int64_t* __restrict__ gb, const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
     int R, int64_t* __restrict__ row_dst, int64_t* __restrict__ row_ptr_s) {
-    __shared__ int64_t sLoad[kSchedMaxQ];
-    __shared__ int64_t sA[kScatterRows][kSchedMaxQ];   // degree in (slot, workgroup)
-    __shared__ int sPos[kScatterRows][kSchedMaxQ];     // row (offset in the group) or -1
-    __shared__ int sAt[kSchedMaxQ];
-    __shared__ int64_t sDeg[kScatterRows * kSchedMaxQ];  // degrees of the group's rows
     const int G = (P + Q - 1) / Q;
-    const int gi = blockIdx.x;
-    const int x = gi / G, gen = gi - x * G;
-    const int Qg = min(Q, P - gen * Q);
-    const int k = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), k = threadIdx.x & 63;
+    const int gi = blockIdx.x * kBalGroups + w;
+    if (blockIdx.x == 0 && threadIdx.x == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];
+    if (gi >= 8 * G) return;  // uniform per wave
+    const SchedGroup s = sched_group(gi, P, Q);
     const int64_t s0 = gb[gi], s1 = gb[gi + 1];
-    const int n = (int)(s1 - s0);
-    const int T = (n + Qg - 1) / Qg;  // <= R: a group holds at most Qg * R rows
-    if (gi == 0 && k == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];  // all the edges
-    sLoad[k] = 0;
-    for (int t = 0; t < kScatterRows; ++t) {
-        sA[t][k] = 0;
-        sPos[t][k] = -1;
-    }
-    for (int i = k; i < n; i += kSchedMaxQ) sDeg[i] = degm[s0 + i];
-    __syncthreads();
-    for (int t = 0; t < T; ++t) {
-        const int o0 = t * Qg;  // slice start, offset in the group
-        const int nt = min(Qg, n - o0);
-        if (k < nt) {  // rank of row k in the slice, heaviest first
-            const int64_t dk = sDeg[o0 + k];
-            int r = 0;
-            for (int j = 0; j < nt; ++j) {
-                const int64_t dj = sDeg[o0 + j];
-                r += (dj > dk) || (dj == dk && j < k);
-            }
-            sAt[r] = k;
-        }
-        int rw = 0;  // rank of workgroup k, lightest first
-        if (k < Qg) {
-            const int64_t lk = sLoad[k];
-            for (int l = 0; l < Qg; ++l) {
-                const int64_t ll = sLoad[l];
-                rw += (ll < lk) || (ll == lk && l < k);
-            }
-        }
-        __syncthreads();
-        if (k < Qg && rw < nt) {
-            const int i = sAt[rw];
-            const int64_t d = sDeg[o0 + i];
-            sA[t][k] = d;
-            sPos[t][k] = o0 + i;
-            sLoad[k] += d;
-        }
-        __syncthreads();
-    }
-    for (int rd = 0; rd < kSchedSwapRounds; ++rd) {
-        int rw = 0;
-        if (k < Qg) {
-            const int64_t lk = sLoad[k];
-            for (int l = 0; l < Qg; ++l) {
-                const int64_t ll = sLoad[l];
-                rw += (ll < lk) || (ll == lk && l < k);
-            }
-        }
-        __syncthreads();
-        if (k < Qg) sAt[rw] = k;
-        __syncthreads();
-        if (k < Qg / 2) {  // pair: k-th lightest with k-th heaviest
-            const int l = sAt[k], h = sAt[Qg - 1 - k];
-            const int64_t diff = sLoad[h] - sLoad[l];
-            int best = -1;
-            int64_t bv = diff;
-            for (int t = 0; t < T; ++t) {
-                const int64_t d = sA[t][h] - sA[t][l];
-                if (d > 0 && d < diff) {
-                    const int64_t v = diff > 2 * d ? diff - 2 * d : 2 * d - diff;
-                    if (v < bv) {
-                        bv = v;
-                        best = t;
-                    }
-                }
-            }
-            if (best >= 0) {
-                const int64_t d = sA[best][h] - sA[best][l];
-                const int64_t ah = sA[best][h];
-                const int ph = sPos[best][h];
-                sA[best][h] = sA[best][l];
-                sPos[best][h] = sPos[best][l];
-                sA[best][l] = ah;
-                sPos[best][l] = ph;
-                sLoad[h] -= d;
-                sLoad[l] += d;
-            }
-        }
-        __syncthreads();
-    }
-    // slot offsets: the group's slots follow the edges of the earlier groups (cum at
-    // the group's first position) in workgroup order, slot order within a workgroup
-    int64_t wl = 0;
-    if (k < Qg)
-        for (int t = 0; t < T; ++t) {
-            const int p = sPos[t][k];
-            if (p >= 0) {
-                const int64_t o = order[s0 + p];
-                if (o >= 0 && o < n_dst) wl += sA[t][k];
-            }
-        }
-    sLoad[k] = wl;
-    __syncthreads();
-    if (k < Qg) {
-        const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
-        int64_t off = cum[s0];
-        for (int l = 0; l < k; ++l) off += sLoad[l];
-        for (int t = 0; t < R; ++t) {
-            const int p = t < T ? sPos[t][k] : -1;
-            int64_t d = -1, dg = 0;
-            if (p >= 0) {
-                const int64_t o = order[s0 + p];
-                if (o >= 0 && o < n_dst) {
-                    d = o;
-                    dg = sA[t][k];
-                }
-            }
-            row_dst[b * R + t] = d;
-            row_ptr_s[b * R + t] = off;
-            off += dg;
-        }
-    }
-}
-
-// The same dealing and swap rounds as sched_balance_kernel, by a block of four
-// waves per group (Qg <= 64 workgroups; lane k of wave 0 = workgroup k, whose
-// slots it keeps in registers).  Ranks come from comparing every key with each
-// other one: rows heaviest first, key deg * 64 + (63 - k); workgroups lightest
-// first, key load * 64 + k (the tie rules of the block version; keys fit 32
-// bits when the edges number under 2^25).  The four waves rank the slices' rows
-// in parallel, and each workgroup ranking is split between them (16 keys per
-// wave, partial counts added through LDS).  Rows and swap partners are
-// exchanged by rank through LDS.  At configs[3]: 68 us for the block version
-// (serial LDS loops in one active wave).
-constexpr int kBalWaves = 4;
-__global__ __launch_bounds__(64 * kBalWaves) void sched_balance_wave_kernel(
-    const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
-    const int64_t* __restrict__ gb, const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
-    int R, int64_t* __restrict__ row_dst, int64_t* __restrict__ row_ptr_s) {
-    __shared__ __attribute__((aligned(16))) int sRk[kScatterRows][64];  // row keys per slice
-    __shared__ __attribute__((aligned(16))) int sKey[64];               // workgroup load keys
-    __shared__ int sPart[kBalWaves][64];      // partial load ranks
-    __shared__ int sRowAt[kScatterRows][64];  // row offset (in the group) of row rank r
-    __shared__ int sDegAt[kScatterRows][64];
-    __shared__ int sA[64][kScatterRows];  // slot degrees of the workgroup of load rank r
-    __shared__ int sP[64][kScatterRows];  // slot rows of the workgroup of load rank r
-    __shared__ int sL[64];                // load of the workgroup of load rank r
-    const int G = (P + Q - 1) / Q;
-    const int gi = blockIdx.x;
-    const int x = gi / G, gen = gi - x * G;
-    const int Qg = min(Q, P - gen * Q);
-    const int k = threadIdx.x & 63;
-    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t s0 = gb[gi], s1 = gb[gi + 1];
-    const int n = (int)(s1 - s0);
-    const int T = (n + Qg - 1) / Qg;  // <= R: a group holds at most Qg * R rows
-    if (gi == 0 && threadIdx.x == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];  // all the edges
-    if (n <= 0) {  // no rows: every slot empty, at the group's edge offset
-        if (v == 0 && k < Qg) {
-            const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
-            const int64_t base = cum[s0];
-            for (int t = 0; t < R; ++t) {
-                row_dst[b * R + t] = -1;
-                row_ptr_s[b * R + t] = base;
-            }
-        }
-        return;
-    }
-    auto wave_sync = [] {
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS accesses are done
-        __builtin_amdgcn_wave_barrier();
-    };
-    // how many of the keys [4 Q0, 4 Q0 + 4 NQ) rank before key
-    auto count_before = [&](const int* keys, int key, bool desc, auto q0_c, auto nq_c) {
-        constexpr int Q0 = decltype(q0_c)::value, NQ = decltype(nq_c)::value;
-        int r = 0;
-        static_for<NQ>([&](auto qq) {
-            const int4 w = reinterpret_cast<const int4*>(keys)[Q0 + decltype(qq)::value];
-            if (desc) r += (w.x > key) + (w.y > key) + (w.z > key) + (w.w > key);
-            else r += (w.x < key) + (w.y < key) + (w.z < key) + (w.w < key);
-        });
-        return r;
-    };
-    // load rank of lane k's workgroup (wave 0 holds the loads): sKey written by wave
-    // 0, every wave counts over its 16 keys, wave 0 adds the partials
-    auto load_rank = [&](int load) {
-        if (v == 0) sKey[k] = k < Qg ? load * 64 + k : INT32_MAX;
-        __syncthreads();
-        const int key = sKey[k];
-        int part = 0;
-        switch (v) {
-            case 0: part = count_before(sKey, key, false, std::integral_constant<int, 0>{}, std::integral_constant<int, 4>{}); break;
-            case 1: part = count_before(sKey, key, false, std::integral_constant<int, 4>{}, std::integral_constant<int, 4>{}); break;
-            case 2: part = count_before(sKey, key, false, std::integral_constant<int, 8>{}, std::integral_constant<int, 4>{}); break;
-            default: part = count_before(sKey, key, false, std::integral_constant<int, 12>{}, std::integral_constant<int, 4>{}); break;
-        }
-        sPart[v][k] = part;
-        __syncthreads();
-        return v == 0 ? sPart[0][k] + sPart[1][k] + sPart[2][k] + sPart[3][k] : 0;
-    };
-
-    // row ranks of all slices (heaviest first): slice t by wave t % 4, the wave's
-    // degrees loaded up front (clamped, unconditional loads in flight together)
-    constexpr int kSl = (kScatterRows + kBalWaves - 1) / kBalWaves;
-    int dgs[kSl];
-    static_for<kSl>([&](auto ii) {
-        constexpr int i = decltype(ii)::value;
-        dgs[i] = (int)degm[s0 + min((v + i * kBalWaves) * Qg + k, n - 1)];
-    });
-    static_for<kSl>([&](auto ii) {
-        constexpr int i = decltype(ii)::value;
-        const int t = v + i * kBalWaves;
-        if (t >= T) return;
-        const int nt = min(Qg, n - t * Qg);
-        const int dk = k < nt ? dgs[i] : 0;
-        const int key = k < nt ? dk * 64 + (63 - k) : -1;
-        sRk[t][k] = key;
-        wave_sync();
-        if (k < nt) {
-            const int rr = count_before(sRk[t], key, true, std::integral_constant<int, 0>{},
-                                        std::integral_constant<int, 16>{});
-            sRowAt[t][rr] = t * Qg + k;
-            sDegAt[t][rr] = dk;
-        }
-        wave_sync();
-    });
-    __syncthreads();
-
-    int a[kScatterRows], pos[kScatterRows];
-    int load = 0;
-    static_for<kScatterRows>([&](auto tt) {
-        constexpr int t = decltype(tt)::value;
-        a[t] = 0;
-        pos[t] = -1;
-    });
-    // slice by slice: the r-th heaviest row to the r-th lightest workgroup so far
-    static_for<kScatterRows>([&](auto tt) {
-        constexpr int t = decltype(tt)::value;
-        if (t < T) {
-            const int nt = min(Qg, n - t * Qg);
-            const int rw = load_rank(load);
-            if (v == 0 && k < Qg && rw < nt) {
-                pos[t] = sRowAt[t][rw];
-                a[t] = sDegAt[t][rw];
-                load += a[t];
-            }
-        }
-    });
-    for (int rd = 0; rd < kSchedSwapRounds; ++rd) {
-        const int rw = load_rank(load);
-        if (v == 0) {
-            if (k < Qg) {
-                static_for<kScatterRows>([&](auto tt) {
-                    constexpr int t = decltype(tt)::value;
-                    sA[rw][t] = a[t];
-                    sP[rw][t] = pos[t];
-                });
-                sL[rw] = load;
-            }
-            wave_sync();
-            // pairs: the i-th lightest with the i-th heaviest (i < Qg / 2); both lanes of
-            // a pair compute the same choice from the same values
-            const int pr = Qg - 1 - rw;
-            const bool paired = k < Qg && min(rw, pr) < Qg / 2 && rw != pr;
-            if (paired) {
-                const bool heavy = rw > pr;
-                int pa[kScatterRows];
-                static_for<kScatterRows>([&](auto tt) {
-                    constexpr int t = decltype(tt)::value;
-                    pa[t] = sA[pr][t];
-                });
-                const int pl = sL[pr];
-                const int diff = heavy ? load - pl : pl - load;
-                int best = -1, bv = diff;
-                static_for<kScatterRows>([&](auto tt) {
-                    constexpr int t = decltype(tt)::value;
-                    if (t < T) {
-                        const int d = heavy ? a[t] - pa[t] : pa[t] - a[t];
-                        if (d > 0 && d < diff) {
-                            const int dv = diff > 2 * d ? diff - 2 * d : 2 * d - diff;
-                            if (dv < bv) {
-                                bv = dv;
-                                best = t;
-                            }
-                        }
-                    }
-                });
-                if (best >= 0) {
-                    int d = 0;
-                    static_for<kScatterRows>([&](auto tt) {
-                        constexpr int t = decltype(tt)::value;
-                        if (t == best) {
-                            d = heavy ? a[t] - pa[t] : pa[t] - a[t];
-                            a[t] = pa[t];
-                            pos[t] = sP[pr][t];
-                        }
-                    });
-                    load += heavy ? -d : d;
-                }
-            }
-            wave_sync();
-        }
-    }
-    if (v == 0) {
-        const int64_t b = (int64_t)x * P + (int64_t)gen * Q + k;
-        const bool live = k < Qg;
-        int64_t od[kScatterRows];  // destinations of the slots, loaded together
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            od[t] = order[s0 + (live && pos[t] >= 0 ? pos[t] : 0)];
-        });
-        int64_t dd[kScatterRows];
-        int sd[kScatterRows];
-        int wl = 0;  // edges of workgroup k
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            const int p = live && t < T ? pos[t] : -1;
-            dd[t] = -1;
-            sd[t] = 0;
-            if (p >= 0 && od[t] >= 0 && od[t] < n_dst) {
-                dd[t] = od[t];
-                sd[t] = a[t];
-            }
-            wl += sd[t];
-        });
-        // slot offsets: the group's slots follow the edges of the earlier groups (cum at
-        // the group's first position), in workgroup order: an exclusive scan over lanes
-        int xs = wl;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(xs, off, 64);
-            if (k >= off) xs += y;
-        }
-        int64_t off = cum[s0] + (xs - wl);
-        if (live)
-            static_for<kScatterRows>([&](auto tt) {
-                constexpr int t = decltype(tt)::value;
-                if (t < R) {
-                    row_dst[b * R + t] = dd[t];
-                    row_ptr_s[b * R + t] = off;
-                    off += sd[t];
-                }
-            });
-    }
+    sched_balance_wave<int64_t>(
+        k, s.Qg, R, (int)(s1 - s0), cum[s0], s.b0, [&](int p) { return degm[s0 + p]; },
+        [&](int p) -> int64_t {
+            const int64_t o = order[s0 + p];
+            return (o >= 0 && o < n_dst) ? o : -1;
+        },
+        row_dst, row_ptr_s, [](int64_t, int64_t) {});
 }
 
 // edge_perm over the scheduled slots: one wave per slot, a lane per edge of its row.
@@ -1574,7 +1171,7 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
         return BM_ERR_WORKSPACE;
     const int B = 256;
     const int P = n_blocks / 8;
-    const int Q = std::min(std::min(P, blocks_per_xcd(C)), kSchedMaxQ);
+    const int Q = schedule_group_size(n_blocks, C);
     const int G = (P + Q - 1) / Q;
     int64_t* degm = static_cast<int64_t*>(workspace);
     int64_t* cum = degm + N_dst;
@@ -1592,12 +1189,9 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
             cum, N_dst, P, Q, gb);
         sched_groups_kernel<<<1, 64, 0, stream>>>(N_dst, P, Q, rows_per_block, gb);
     }
-    if (Q <= 64 && N_edges < ((int64_t)1 << 25))
-        sched_balance_wave_kernel<<<(unsigned)(8 * G), 64 * kBalWaves, 0, stream>>>(
-            degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst, row_ptr_s);
-    else
-        sched_balance_kernel<<<(unsigned)(8 * G), kSchedMaxQ, 0, stream>>>(
-            degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst, row_ptr_s);
+    sched_balance_kernel<<<(unsigned)ceil_div(8 * (int64_t)G, kBalGroups), 64 * kBalGroups, 0,
+                           stream>>>(degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst,
+                                     row_ptr_s);
     sched_edges_kernel<<<(unsigned)ceil_div(n_sched, 4), 256, 0, stream>>>(row_ptr, col_perm, row_dst,
                                                                           row_ptr_s, edge_perm, n_sched);
     return (int)hipGetLastError();

@@ -15,71 +15,12 @@
 // fp32 inputs alone.
 #include "common.h"
 #include "batmobile_hip.h"
+#include "nl_geom.h"
 
 #include <cstring>
 #include <vector>
 
 namespace bmhip {
-
-struct BinCfg {
-    int nb[3];
-    float bin[3];
-    float box[3];
-    float inv[3];
-    int total;
-};
-
-static BinCfg make_bin_cfg(const float box[3], float cutoff) {
-    BinCfg c;
-    for (int d = 0; d < 3; ++d) {
-        c.box[d] = box[d];
-        c.inv[d] = 1.0f / box[d];
-        const int n = (int)(box[d] / cutoff);
-        c.nb[d] = n > 3 ? n : 3;
-        c.bin[d] = box[d] / (float)c.nb[d];
-    }
-    c.total = c.nb[0] * c.nb[1] * c.nb[2];
-    return c;
-}
-
-#pragma clang fp contract(off)
-
-__device__ __forceinline__ void bin_coords(float px, float py, float pz, const BinCfg& c,
-                                           int* b) {
-    const float p[3] = {px, py, pz};
-#pragma unroll
-    for (int d = 0; d < 3; ++d) {
-        const float t = p[d] * c.inv[d];
-        const float fl = floorf(t) * c.box[d];
-        const float wpos = p[d] - fl;
-        const int v = (int)(wpos / c.bin[d]);
-        // upper clamp as the reference (neighbor_list.cu:48-50); the lower clamp only
-        // guards non-finite input (a finite wrapped position never gives v < 0)
-        const int hi = v < c.nb[d] - 1 ? v : c.nb[d] - 1;
-        b[d] = hi > 0 ? hi : 0;
-    }
-}
-
-__device__ __forceinline__ float min_image(const float* pi, const float* pj, const BinCfg& c,
-                                           float* d) {
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const float t = pj[k] - pi[k];
-        const float s = t * c.inv[k];
-        const float r = rintf(s);
-        const float m = r * c.box[k];
-        d[k] = t - m;
-    }
-    const float xx = d[0] * d[0];
-    const float yy = d[1] * d[1];
-    const float zz = d[2] * d[2];
-    const float s = xx + yy;
-    return s + zz;
-}
-
-#pragma clang fp contract(on)
-
-__device__ __forceinline__ int wrap_bin(int b, int n) { return (b + n) % n; }
 
 __global__ void nl_zero_i32_kernel(int* __restrict__ p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -673,14 +614,6 @@ static NlLayout nl_layout(int64_t n, int total_bins) {
     return L;
 }
 
-static bool valid_box(const float box[3], float cutoff) {
-    if (!(cutoff > 0.0f)) return false;
-    for (int d = 0; d < 3; ++d)
-        if (!(box[d] > 0.0f)) return false;
-    const BinCfg c = make_bin_cfg(box, cutoff);
-    return (int64_t)c.nb[0] * c.nb[1] * c.nb[2] < (int64_t)1 << 30;
-}
-
 }  // namespace bmhip
 
 using namespace bmhip;
@@ -785,15 +718,6 @@ extern "C" int batteries_neighbor_list_write(const float* positions, const float
 // One workgroup: each thread takes a run of consecutive path positions, their
 // atom counts are scanned across the workgroup, then each thread writes its runs.
 constexpr int kSerpBlock = 1024;
-
-__device__ __forceinline__ int serpentine_cell(int p, const BinCfg& c) {
-    const int nx = c.nb[0], ny = c.nb[1];
-    const int row = p / nx, px = p - row * nx;
-    const int bz = row / ny, py = row - bz * ny;
-    const int by = (bz & 1) ? ny - 1 - py : py;
-    const int bx = (row & 1) ? nx - 1 - px : px;
-    return bx + by * nx + bz * nx * ny;
-}
 
 __global__ __launch_bounds__(kSerpBlock) void nl_serpentine_order_kernel(
     const int64_t* __restrict__ bin_start, const int* __restrict__ order, BinCfg c,

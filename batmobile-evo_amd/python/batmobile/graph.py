@@ -25,9 +25,12 @@ returns all-zero sums (no messages, no forces).  A loop that builds with max_edg
 must call check() (one host synchronisation) before it trusts a result, e.g. once
 every few steps with max_edges sized with headroom, and rebuild larger on an error.
 
-row_ptr is a view into the neighbor list's device workspace (no copy on the hot
-path): it keeps that workspace alive, and saving it serialises the workspace too;
-take row_ptr.clone() to keep the offsets alone.
+Up to 8192 atoms (and 4096 cells) the whole build runs in four kernels
+(_batmobile.graph_build); larger systems take the neighbor list's passes and
+mp_schedule, with the same results (fast_build=False forces that path).  row_ptr,
+order and the schedule, and src, dst and edge_perm, may be views into one
+allocation each (or row_ptr into the neighbor list's workspace): saving one
+serialises its whole storage; clone() keeps a tensor alone.
 """
 import torch
 
@@ -35,29 +38,43 @@ import _batmobile
 
 
 class Graph:
-    def __init__(self, positions, cell, cutoff, channels, self_loops=False, max_edges=None):
-        # the neighbor list written directly in this layout (one pass, no torch glue),
-        # with a spatial order of the atoms from its cells
-        if max_edges is None:
-            src, dst, vec, off, order = _batmobile.neighbor_graph(positions, cell, float(cutoff),
-                                                                  bool(self_loops))
-            self.overflow = None
-            self._num_edges = int(src.numel())
-        else:
-            src, dst, vec, off, order, self.overflow = _batmobile.neighbor_graph_capacity(
-                positions, cell, float(cutoff), bool(self_loops), int(max_edges))
-            self._num_edges = None
+    def __init__(self, positions, cell, cutoff, channels, self_loops=False, max_edges=None,
+                 fast_build=True):
         self.cell = cell
         self.cutoff = float(cutoff)
         self.positions = positions
         self._rev = None
         self._fine_order = None
         self.n_atoms = positions.shape[0]
+        self.channels = int(channels)
+        cap = -1 if max_edges is None else int(max_edges)
+        # up to 8192 atoms: the whole build in four kernels (graph.hip); larger systems,
+        # or fast_build=False, the neighbor list passes then mp_schedule (same results)
+        res = None
+        if fast_build:
+            res = _batmobile.graph_build(positions, cell, self.cutoff, bool(self_loops),
+                                         self.channels, cap, 0)
+        if res is not None:
+            (self.src, self.dst, self.vec, self.row_ptr, self.order, self.row_ptr_s,
+             self.edge_perm, self.row_dst, self.n_blocks, self.rows_per_block,
+             self.overflow) = res
+            self._num_edges = int(self.src.numel()) if max_edges is None else None
+            return
+        # the neighbor list written directly in this layout (one pass, no torch glue),
+        # with a spatial order of the atoms from its cells
+        if max_edges is None:
+            src, dst, vec, off, order = _batmobile.neighbor_graph(positions, cell, self.cutoff,
+                                                                  bool(self_loops))
+            self.overflow = None
+            self._num_edges = int(src.numel())
+        else:
+            src, dst, vec, off, order, self.overflow = _batmobile.neighbor_graph_capacity(
+                positions, cell, self.cutoff, bool(self_loops), cap)
+            self._num_edges = None
         self.src = src
         self.dst = dst
         self.vec = vec
         self.row_ptr = off
-        self.channels = int(channels)
         self.order = order
         (self.row_ptr_s, self.edge_perm, self.row_dst, self.n_blocks,
          self.rows_per_block) = _batmobile.mp_schedule(self.row_ptr, self.order, self.channels,

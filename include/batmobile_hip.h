@@ -312,6 +312,41 @@ int batteries_neighbor_graph_write_capacity(const float* positions, const float*
                                             int64_t* spatial_order, int* overflow,
                                             hipStream_t stream);
 
+/* Graph build in four kernels, for systems of up to 8192 atoms and 4096 cells with
+ * atoms x cells <= 2^23 and at most 256 schedule groups for C channels
+ * (workspace_bytes returns 0 otherwise: use the neighbor graph calls above and
+ * batteries_mp_schedule).  Results bit-identical to those calls
+ * (graph layout, spatial order, schedule of batteries_mp_schedule_shape(N, C)).
+ *
+ * Count (three kernels): binning, one workgroup per cell writing each atom's row
+ * sorted by j into a workspace slab of row_capacity entries per atom (0: chosen
+ * from the density; longer rows are found again by the write), then one workgroup
+ * for the row offsets and the schedule: row_offsets [N+1] (row_offsets[N] = E),
+ * order [N] (spatial order), row_ptr_s [n_blocks*rows_per_block + 1] and row_dst
+ * [n_blocks*rows_per_block].  capacity >= 0: the edge arrays hold `capacity` edges;
+ * when E > capacity *overflow (device int, may be NULL with capacity < 0) is set
+ * to 1 and every row is left empty (as batteries_neighbor_graph_write_capacity).
+ * Write (one kernel, same workspace, after count, no host synchronisation needed):
+ * src, dst [E] int64, edge_vectors [E, 3] (the layout of
+ * batteries_neighbor_graph_write) and edge_perm [E] (of batteries_mp_schedule with
+ * col_perm NULL).  No counterpart in the reference, whose e2e pipeline rebuilds
+ * its neighbor list and converts it with torch per step
+ * (benchmarks/benchmark_e2e_mace.py:192-278); the neighbor set is that of
+ * batteries::neighbor_list_cuda (src/neighbor_list/neighbor_list.cu:242-430). */
+size_t batteries_graph_build_workspace_bytes(int64_t N, const float* box, float cutoff, int C,
+                                             int row_capacity);
+int batteries_graph_build_count(const float* positions, const float* box, int64_t N,
+                                float cutoff, int self_loops, int C, int n_blocks,
+                                int rows_per_block, int64_t capacity, int row_capacity,
+                                void* workspace, size_t workspace_bytes, int64_t* row_offsets,
+                                int64_t* order, int64_t* row_ptr_s, int64_t* row_dst,
+                                int* overflow, hipStream_t stream);
+int batteries_graph_build_write(const float* positions, const float* box, int64_t N,
+                                float cutoff, int self_loops, int row_capacity, void* workspace,
+                                size_t workspace_bytes, const int64_t* row_offsets,
+                                const int* overflow, int64_t* src, int64_t* dst,
+                                float* edge_vectors, int64_t* edge_perm, hipStream_t stream);
+
 /* Phase 2 with int64 indices in the neighbor list's own orientation (same
  * workspace, after phase 1; num_edges = E from phase 1): edge_index [2, E] (row 0 =
  * i, row 1 = j, sorted by (i, j)), edge_vectors [E, 3] = minimum-image pos[j] -
