@@ -327,6 +327,19 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t v) {
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// Inclusive sum over the lanes of a wave: row_shr 1, 2, 4, 8 within each row of 16,
+// then the rows' totals by row_bcast 15 and 31 (lanes with no source add 0).  Every
+// lane of the wave must execute it.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
+    return x;
+}
+
 }  // namespace bmhip
 
 // Status codes returned by the C ABI (0 = success).

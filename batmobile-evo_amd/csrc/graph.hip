@@ -24,7 +24,7 @@
 //   gb_sched_kernel  one workgroup per schedule group: each computes the row offsets
 //                    (exclusive sums of the counts), the degrees in spatial order and
 //                    their sums and the group bounds in LDS, then balances its group
-//                    (mp_schedule.h) with one wave on a compute unit of its own and
+//                    (mp_schedule.h) with four waves on a compute unit of its own and
 //                    writes every scheduled destination's slot offset for the next
 //                    kernel; the first one writes the row offsets.
 //   gb_rows_kernel   one wave per row: the slab row copied to the edge arrays and to
@@ -44,13 +44,15 @@ namespace bmhip {
 constexpr int kGbMaxAtoms = 8192;
 constexpr int kGbMaxCells = 4096;              // 12-bit cell ids in the packed bins
 constexpr int64_t kGbMaxSweep = 1LL << 23;     // atoms x cells: the sweeps' total work
-constexpr int kGbBlock = 256;                  // four waves per cell
+constexpr int kGbWaves = 8;                    // waves per cell
+constexpr int kGbBlock = 64 * kGbWaves;
 constexpr int kGbPer = kGbMaxAtoms / kGbBlock;  // packed bins held per thread
 constexpr int kGbCap = 2048;                   // candidates staged per chunk (32 KB)
 constexpr int kGbHomeCap = 256;                // own atoms per chunk
 constexpr int kGsThreads = 1024;               // the schedule workgroup
 constexpr int kGsPer = kGbMaxAtoms / kGsThreads;
 constexpr int kGsMaxGroups = 256;               // schedule groups (8 per generation)
+constexpr int kGsFastGroups = 32;               // up to this many: targets found in parallel
 
 __device__ __forceinline__ uint64_t lanes_below(int lane) { return (1ull << lane) - 1ull; }
 
@@ -64,25 +66,12 @@ __global__ __launch_bounds__(256) void gb_bin_kernel(const float* __restrict__ p
     pk[i] = cell | (serpentine_pos(b[0], b[1], b[2], c) << 12);
 }
 
-// Inclusive sum over the lanes of a wave: row_shr 1, 2, 4, 8 within each row of 16,
-// then the rows' totals by row_bcast 15 and 31 (lanes with no source add 0).  Every
-// lane of the wave must execute it.
-__device__ __forceinline__ int gb_wave_scan(int x) {
-    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
-    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
-    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
-    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
-    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
-    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
-    return x;
-}
-
 __global__ __launch_bounds__(kGbBlock) void gb_cell_kernel(
     const float* __restrict__ pos, BinCfg c, int n, float rc2, int self_loops,
     const int* __restrict__ pk, int row_cap, float4* __restrict__ slab, int* __restrict__ cnt,
     int64_t* __restrict__ order) {
-    constexpr int kWords = kGbMaxAtoms / 32;  // one bitmap word per thread
-    static_assert(kWords == kGbBlock, "one bitmap word per thread");
+    constexpr int kWords = kGbMaxAtoms / 32;  // bitmap words: one per thread of the first ones
+    static_assert(kWords <= kGbBlock, "one bitmap word per thread");
     __shared__ float4 sCand[kGbCap];
     __shared__ int sCidx[kGbCap];
     __shared__ float4 sHome[kGbHomeCap];
@@ -91,26 +80,28 @@ __global__ __launch_bounds__(kGbBlock) void gb_cell_kernel(
     __shared__ uint32_t sBits[kGbMaxCells / 32];  // the 27 stencil cells
     __shared__ uint32_t sMem[kWords];             // atoms in the stencil cells (members)
     __shared__ uint32_t sOwn[kWords];             // atoms in this cell
-    __shared__ int sWave[4];
-    __shared__ int sBef[4];
+    __shared__ int sWave[kGbWaves];
+    __shared__ int sBef[kGbWaves];
     const int t = threadIdx.x, lane = t & 63;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int p = blockIdx.x;
     const int hc = serpentine_cell(p, c);
     const int nx = c.nb[0], ny = c.nb[1], nz = c.nb[2];
     const int hx = hc % nx, hy = (hc / nx) % ny, hz = hc / (nx * ny);
-    // atom (wv + 4 k) * 64 + lane in slot k: every packed bin loaded up front
+    // atom (wv + kGbWaves k) * 64 + lane in slot k: every packed bin loaded up front
     // (clamped, unconditional)
     int v[kGbPer];
 #pragma unroll
     for (int k = 0; k < kGbPer; ++k) {
-        const int a = (wv + 4 * k) * 64 + lane;
+        const int a = (wv + kGbWaves * k) * 64 + lane;
         v[k] = pk[min(a, n - 1)];
         if (a >= n) v[k] = -1;
     }
     for (int q = t; q < kGbMaxCells / 32; q += kGbBlock) sBits[q] = 0;
-    sMem[t] = 0;
-    sOwn[t] = 0;
+    if (t < kWords) {
+        sMem[t] = 0;
+        sOwn[t] = 0;
+    }
     __syncthreads();
     if (t < 27) {
         const int dz = t / 9 - 1, dy = (t / 3) % 3 - 1, dx = t % 3 - 1;
@@ -129,33 +120,34 @@ __global__ __launch_bounds__(kGbBlock) void gb_cell_kernel(
         const int x = v[k];
         const int cell = x & 0xfff;
         const uint32_t word = sBits[cell >> 5];
-        const int a = (wv + 4 * k) * 64 + lane;
+        const int a = (wv + kGbWaves * k) * 64 + lane;
         if (x >= 0) {
             if ((word >> (cell & 31)) & 1u) atomicOr(&sMem[a >> 5], 1u << (a & 31));
             if (cell == hc) atomicOr(&sOwn[a >> 5], 1u << (a & 31));
             bef += (x >> 12) < p ? 1 : 0;
         }
     });
-    bef = gb_wave_scan(bef);
+    bef = wave_incl_scan(bef);
     if (lane == 63) sBef[wv] = bef;
     __syncthreads();
     // ranks: word t's members and own atoms follow those of the words before it (packed
     // counts, members | own << 16, scanned over the workgroup)
-    const uint32_t mw = sMem[t], ow = sOwn[t];
+    const uint32_t mw = t < kWords ? sMem[t] : 0u, ow = t < kWords ? sOwn[t] : 0u;
     const int cw = __popc(mw) | (__popc(ow) << 16);
-    const int incl = gb_wave_scan(cw);
+    const int incl = wave_incl_scan(cw);
     if (lane == 63) sWave[wv] = incl;
     __syncthreads();
     int before = 0, tot = 0;
+    int base_p = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kGbWaves; ++q) {
         before += q < wv ? sWave[q] : 0;
         tot += sWave[q];
+        base_p += sBef[q];
     }
     const int excl = before + incl - cw;
     const int T = tot & 0xffff, H = tot >> 16;
     if (H == 0) return;  // uniform: no atoms in this cell
-    const int base_p = sBef[0] + sBef[1] + sBef[2] + sBef[3];
     // lists the members with rank in [c_lo, c_lo + kGbCap) and the own atoms with rank
     // in [h_lo, h_lo + kGbHomeCap) from this thread's words
     auto extract = [&](int c_lo, int h_lo) {
@@ -199,7 +191,7 @@ __global__ __launch_bounds__(kGbBlock) void gb_cell_kernel(
                 }
             __syncthreads();
             const bool last = c_lo + kGbCap >= T;
-            for (int hh = wv; hh < nh; hh += 4) {
+            for (int hh = wv; hh < nh; hh += kGbWaves) {
                 const float4 ci = sHome[hh];
                 const int i = __builtin_amdgcn_readfirstlane(__float_as_int(ci.w));
                 const float pi[3] = {ci.x, ci.y, ci.z};
@@ -248,7 +240,7 @@ __device__ int gb_lds_scan(int* s, int n, int* sWsum) {
         v[q] = i0 + q < n ? v[q] : 0;
         sum += v[q];
     }
-    const int x = gb_wave_scan(sum);
+    const int x = wave_incl_scan(sum);
     if (lane == 63) sWsum[w] = x;
     __syncthreads();
     int before = 0, total = 0;
@@ -290,6 +282,8 @@ __global__ __launch_bounds__(kGsThreads) void gb_sched_kernel(
     __shared__ int sGb[kGsMaxGroups + 1];
     __shared__ int sQg[kGsMaxGroups];
     __shared__ int sWend[kGsMaxGroups];
+    __shared__ double sTgt[kGsMaxGroups];
+    __shared__ __attribute__((aligned(16))) SchedLds<int> sL;
     const int t = threadIdx.x, lane = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
     int cv[kGsPer];
@@ -330,11 +324,37 @@ __global__ __launch_bounds__(kGsThreads) void gb_sched_kernel(
         for (int i = t; i <= n; i += kGsThreads) offsets[i] = over ? 0 : sOff[i];
         if (t == 0 && overflow) *overflow = over ? 1 : 0;
     }
+    // each group's edge share, for the search below
+    for (int gi = t; gi < 8 * G; gi += kGsThreads)
+        sTgt[gi] = (double)E * (double)sWend[gi] / (8.0 * (double)P);
     __syncthreads();
     gb_lds_scan(sCum, n, sWsum);
-    for (int gi = t; gi < 8 * G; gi += kGsThreads)
-        sPos[gi] = (int)sched_group_target(gi, P, Q, n, (double)E,
-                                           [&](int64_t m) { return (int64_t)sCum[m]; });
+    if (8 * G <= kGsFastGroups) {
+        // the target position of every group (the search of sched_group_target: the first
+        // position whose running sum reaches the share, or the one before it when that is
+        // closer), found by the thread whose run holds it: positions m in [8t, 8t + 8),
+        // and the last thread also n (sCum[n] = E reaches every share).  A running sum
+        // (an integer) reaches the share when it reaches the share rounded up.
+        const int m0 = t * kGsPer;
+        const int m1 = t == kGsThreads - 1 ? n + 1 : min(m0 + kGsPer, n + 1);
+        if (m0 < m1) {
+            const int before = m0 > 0 ? sCum[m0 - 1] : -1;
+            const int last = sCum[m1 - 1];
+            for (int gi = 0; gi < 8 * G; ++gi) {
+                const double target = sTgt[gi];
+                const int64_t need = (int64_t)ceil(target);
+                if (before < need && last >= need) {  // the crossing is in this run
+                    int m = m0, prev = before;
+                    while (sCum[m] < need) prev = sCum[m++];
+                    sPos[gi] = (m > 0 && target - (double)prev < (double)sCum[m] - target) ? m - 1 : m;
+                }
+            }
+        }
+    } else {
+        for (int gi = t; gi < 8 * G; gi += kGsThreads)
+            sPos[gi] = (int)sched_group_target(gi, P, Q, n, (double)E,
+                                               [&](int64_t m) { return (int64_t)sCum[m]; });
+    }
     __syncthreads();
     if (t == 0) {
         sched_clamp_groups(
@@ -344,17 +364,15 @@ __global__ __launch_bounds__(kGsThreads) void gb_sched_kernel(
         if (first) row_ptr_s[(int64_t)8 * P * R] = E;
     }
     __syncthreads();
-    // workgroup gi balances group gi with its first wave (a compute unit of its own)
+    // workgroup gi balances group gi with its first four waves (a compute unit of its own)
     const int gi = blockIdx.x;
-    if (w == 0 && gi < 8 * G) {
-        const int s0 = sGb[gi], s1 = sGb[gi + 1];
-        const int Qg = sQg[gi];
-        sched_balance_wave<int>(
-            lane, Qg, R, s1 - s0, sCum[s0], (int64_t)sWend[gi] - Qg,
-            [&](int q) { return sCum[s0 + q + 1] - sCum[s0 + q]; },
-            [&](int q) -> int64_t { return sOrd[s0 + q]; }, row_dst, row_ptr_s,
-            [&](int64_t d, int64_t o) { soff[d] = o; });
-    }
+    const int s0 = sGb[gi], s1 = sGb[gi + 1];
+    const int Qg = sQg[gi];
+    sched_balance_group<int>(
+        w, lane, Qg, R, s1 - s0, sCum[s0], (int64_t)sWend[gi] - Qg,
+        [&](int q) { return sCum[s0 + q + 1] - sCum[s0 + q]; },
+        [&](int q) -> int64_t { return sOrd[s0 + q]; }, row_dst, row_ptr_s,
+        [&](int64_t d, int64_t o) { soff[d] = o; }, sL);
 }
 
 __device__ __forceinline__ bool gb_near(int b, int h, int nb) {

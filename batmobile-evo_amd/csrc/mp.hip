@@ -1092,28 +1092,26 @@ __global__ __launch_bounds__(kPrepThreads) void sched_prep_kernel(
                            [&](int i, int64_t v) { gb[i] = v; });
 }
 
-// One wave per group, kBalGroups groups per workgroup.  TD: int when the edges number
-// under 2^31 (every slot degree and workgroup load fits), else int64_t.
-constexpr int kBalGroups = 4;
+// One workgroup of kSchedWaves waves per group.  TD: int when the edges number under
+// 2^31 (every slot degree and workgroup load fits), else int64_t.
 template <typename TD>
-__global__ __launch_bounds__(64 * kBalGroups) void sched_balance_kernel(
+__global__ __launch_bounds__(64 * kSchedWaves) void sched_balance_kernel(
     const int64_t* __restrict__ degm, const int64_t* __restrict__ order,
     const int64_t* __restrict__ gb, const int64_t* __restrict__ cum, int64_t n_dst, int P, int Q,
     int R, int64_t* __restrict__ row_dst, int64_t* __restrict__ row_ptr_s) {
-    const int G = (P + Q - 1) / Q;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), k = threadIdx.x & 63;
-    const int gi = blockIdx.x * kBalGroups + w;
-    if (blockIdx.x == 0 && threadIdx.x == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];
-    if (gi >= 8 * G) return;  // uniform per wave
+    __shared__ __attribute__((aligned(16))) SchedLds<TD> sL;
+    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), k = threadIdx.x & 63;
+    const int gi = blockIdx.x;
+    if (gi == 0 && threadIdx.x == 0) row_ptr_s[(int64_t)8 * P * R] = cum[n_dst];
     const SchedGroup s = sched_group(gi, P, Q);
     const int64_t s0 = gb[gi], s1 = gb[gi + 1];
-    sched_balance_wave<TD>(
-        k, s.Qg, R, (int)(s1 - s0), cum[s0], s.b0, [&](int p) { return (TD)degm[s0 + p]; },
+    sched_balance_group<TD>(
+        v, k, s.Qg, R, (int)(s1 - s0), cum[s0], s.b0, [&](int p) { return (TD)degm[s0 + p]; },
         [&](int p) -> int64_t {
             const int64_t o = order[s0 + p];
             return (o >= 0 && o < n_dst) ? o : -1;
         },
-        row_dst, row_ptr_s, [](int64_t, int64_t) {});
+        row_dst, row_ptr_s, [](int64_t, int64_t) {}, sL);
 }
 
 // edge_perm over the scheduled slots: one wave per slot, a lane per edge of its row.
@@ -1191,12 +1189,12 @@ extern "C" int batteries_mp_schedule(const int64_t* row_ptr, const int64_t* col_
             cum, N_dst, P, Q, gb);
         sched_groups_kernel<<<1, 64, 0, stream>>>(N_dst, P, Q, rows_per_block, gb);
     }
-    const unsigned nbal = (unsigned)ceil_div(8 * (int64_t)G, kBalGroups);
+    const unsigned nbal = (unsigned)(8 * G);
     if (N_edges < INT32_MAX)
-        sched_balance_kernel<int><<<nbal, 64 * kBalGroups, 0, stream>>>(
+        sched_balance_kernel<int><<<nbal, 64 * kSchedWaves, 0, stream>>>(
             degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst, row_ptr_s);
     else
-        sched_balance_kernel<int64_t><<<nbal, 64 * kBalGroups, 0, stream>>>(
+        sched_balance_kernel<int64_t><<<nbal, 64 * kSchedWaves, 0, stream>>>(
             degm, order, gb, cum, N_dst, P, Q, rows_per_block, row_dst, row_ptr_s);
     sched_edges_kernel<<<(unsigned)ceil_div(n_sched, 4), 256, 0, stream>>>(row_ptr, col_perm, row_dst,
                                                                           row_ptr_s, edge_perm, n_sched);

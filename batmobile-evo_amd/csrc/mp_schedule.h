@@ -16,7 +16,7 @@
 //     edge counts: workgroup k pairs with k ^ m (m = 32, 16, 8, 4, 2, 1, 32, 16), and
 //     the pair exchanges the rows of the one slot whose exchange brings their counts
 //     closest (if any exchange reduces the difference).  The pairs need no ranking,
-//     only lane permutes.
+//     only lane permutes; four waves share a group's slots.
 //
 // The kernel time is that of the busiest compute unit, so equal edge counts per
 // workgroup matter.  In a host simulation at configs[3] (5000 destinations, 512
@@ -100,131 +100,179 @@ __device__ inline void sched_clamp_groups(int P, int Q, int R, int64_t n_dst, Ta
                        [&](int gi) { return sched_group(gi, P, Q); });
 }
 
-// The exchange rounds: in round r lane k (workgroup k) pairs with lane k ^ m_r, and the
-// pair exchanges the rows of the one slot whose exchange brings their edge counts
-// closest (if any exchange reduces the difference).  The partner's slot degrees and
-// load come by lane permutes; both lanes of a pair compute the same choice from the
-// same values, so each takes the partner's row of that slot.
+// The exchange rounds: in round r workgroup k pairs with workgroup k ^ m_r, and the pair
+// exchanges the rows of the one slot whose exchange brings their edge counts closest
+// (if any exchange reduces the difference; the first such slot on a tie).
 constexpr int kSchedSwapRounds = 8;
 __device__ __forceinline__ int sched_swap_mask(int r) { return 32 >> (r % 6); }
 
+// Four waves balance one group: lane k of every wave is workgroup b0 + k (k < Qg <= 64),
+// and wave v holds its slots t = v, v + 4, v + 8 in registers.  In a round each wave
+// takes the partner's degrees of its slots by lane permutes and proposes its best slot;
+// the four proposals meet in LDS (one barrier per round, buffers alternating by round)
+// and every wave applies the best, the owner of the slot taking the partner's row.
+// Both lanes of a pair see the same values, so they make the same choice.
+constexpr int kSchedWaves = 4;
+constexpr int kSchedSlotsPerWave = (kScatterRows + kSchedWaves - 1) / kSchedWaves;
+
 template <typename TD>
-__device__ inline void sched_swap_rounds(int k, int Qg, int T, int (&pos)[kScatterRows],
-                                         TD (&a)[kScatterRows], TD& load) {
-#pragma unroll
-    for (int rd = 0; rd < kSchedSwapRounds; ++rd) {
-        const int m = sched_swap_mask(rd);
-        TD pa[kScatterRows];
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            pa[t] = __shfl_xor(a[t], m, 64);
+struct SchedLds {
+    int64_t key[2][kSchedWaves][64];  // (round parity, wave, lane): dv * 16 + t of its best slot
+    TD d[2][kSchedWaves][64];         // that slot's degree difference
+    TD a[kScatterRows][64];           // the final slot degrees
+    TD part[kSchedWaves][64];         // the waves' partial loads
+};
+
+// Every thread of the workgroup calls it (it holds barriers); waves v >= kSchedWaves take
+// part in the barriers only.  The group's rows are positions [0, n) of its range of the
+// processing order: deg(r) is the degree of row r, dst(r) its destination (-1: none,
+// degree 0); both are called with r clamped into [0, n), so that their loads are all in
+// flight together.  base is the number of edges before the group.  Writes row_dst and
+// row_ptr_s for the group's slots and calls put_soff(d, offset) for every scheduled
+// destination d.
+template <typename TD, class DegF, class DstF, class SoffF>
+__device__ inline void sched_balance_group(int v, int k, int Qg, int R, int n, int64_t base,
+                                           int64_t b0, DegF deg, DstF dst,
+                                           int64_t* __restrict__ row_dst,
+                                           int64_t* __restrict__ row_ptr_s, SoffF put_soff,
+                                           SchedLds<TD>& L) {
+    constexpr int J = kSchedSlotsPerWave;
+    const int T = n > 0 ? (n + Qg - 1) / Qg : 0;  // <= R: a group holds at most Qg * R rows
+    const bool act = v < kSchedWaves;
+    int pos[J];
+    TD a[J];
+    TD part = 0;
+    {
+        TD dv[J];
+        static_for<J>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            dv[j] = (act && T > 0) ? deg(min((v + 4 * j) * Qg + k, n - 1)) : TD(0);
         });
-        const TD pl = __shfl_xor(load, m, 64);
-        const int kp = k ^ m;
-        const bool heavy = load > pl || (load == pl && k > kp);
-        const TD diff = heavy ? load - pl : pl - load;
-        int best = -1;
-        TD bv = diff;
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            if (t < T) {
-                const TD d = heavy ? a[t] - pa[t] : pa[t] - a[t];
-                if (d > 0 && d < diff) {
+        static_for<J>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            const int t = v + 4 * j, p = t * Qg + k;
+            const bool live = act && k < Qg && t < T && p < n;
+            pos[j] = live ? p : -1;
+            a[j] = live ? dv[j] : TD(0);
+            part += a[j];
+        });
+    }
+    if (act) L.part[v][k] = part;
+    __syncthreads();
+    TD load = 0;
+    if (act)
+#pragma unroll
+        for (int q = 0; q < kSchedWaves; ++q) load += L.part[q][k];
+    for (int rd = 0; rd < kSchedSwapRounds && T > 0; ++rd) {
+        const int m = sched_swap_mask(rd), kp = k ^ m, par = rd & 1;
+        TD pa[J];
+        bool heavy = false;
+        if (act) {
+            static_for<J>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
+                pa[j] = __shfl_xor(a[j], m, 64);
+            });
+            const TD pl = __shfl_xor(load, m, 64);
+            heavy = load > pl || (load == pl && k > kp);
+            const TD diff = heavy ? load - pl : pl - load;
+            int64_t bkey = INT64_MAX;
+            TD bd = 0;
+            static_for<J>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
+                const int t = v + 4 * j;
+                const TD d = heavy ? a[j] - pa[j] : pa[j] - a[j];
+                if (t < T && d > 0 && d < diff) {
                     const TD dv = diff > 2 * d ? diff - 2 * d : 2 * d - diff;
-                    if (dv < bv) {
-                        bv = dv;
-                        best = t;
+                    const int64_t key = (int64_t)dv * 16 + t;
+                    if (key < bkey) {
+                        bkey = key;
+                        bd = d;
                     }
                 }
-            }
-        });
-        int mine = -1;  // this lane's row in the chosen slot, for the partner
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            if (t == best) mine = pos[t];
-        });
-        const int theirs = __shfl_xor(mine, m, 64);
-        if (k < Qg && kp < Qg && best >= 0) {
-            static_for<kScatterRows>([&](auto tt) {
-                constexpr int t = decltype(tt)::value;
-                if (t == best) {
-                    const TD d = heavy ? a[t] - pa[t] : pa[t] - a[t];
-                    a[t] = pa[t];
-                    pos[t] = theirs;
-                    load += heavy ? -d : d;
-                }
             });
+            L.key[par][v][k] = bkey;
+            L.d[par][v][k] = bd;
+        }
+        __syncthreads();
+        if (act) {
+            int64_t best = INT64_MAX;
+            TD bd = 0;
+#pragma unroll
+            for (int q = 0; q < kSchedWaves; ++q) {
+                const int64_t key = L.key[par][q][k];
+                if (key < best) {
+                    best = key;
+                    bd = L.d[par][q][k];
+                }
+            }
+            const bool swap = k < Qg && kp < Qg && best != INT64_MAX;
+            const int tb = swap ? (int)(best & 15) : -1;
+            int mine = -1;  // this lane's row in the chosen slot (in its owner wave), for the partner
+            static_for<J>([&](auto jj) {
+                constexpr int j = decltype(jj)::value;
+                if (v + 4 * j == tb) mine = pos[j];
+            });
+            const int theirs = __shfl_xor(mine, m, 64);
+            if (swap) {
+                load += heavy ? -bd : bd;
+                static_for<J>([&](auto jj) {
+                    constexpr int j = decltype(jj)::value;
+                    if (v + 4 * j == tb) {
+                        a[j] = pa[j];
+                        pos[j] = theirs;
+                    }
+                });
+            }
         }
     }
-}
-
-// One wave balances one group: lane k is workgroup b0 + k (k < Qg <= 64), holding
-// its R slots in registers.  The group's rows are positions [0, n) of its range of
-// the processing order: deg(r) is the degree of row r, dst(r) its destination (-1:
-// none, degree 0); both are called for every slot with r clamped into [0, n), so
-// that their loads are all in flight together.  base is the number of edges before
-// the group.  Writes row_dst and row_ptr_s for the group's slots and calls
-// put_soff(d, offset) for every scheduled destination d.
-template <typename TD, class DegF, class DstF, class SoffF>
-__device__ inline void sched_balance_wave(int k, int Qg, int R, int n, int64_t base, int64_t b0,
-                                          DegF deg, DstF dst, int64_t* __restrict__ row_dst,
-                                          int64_t* __restrict__ row_ptr_s, SoffF put_soff) {
-    const int T = n > 0 ? (n + Qg - 1) / Qg : 0;  // <= R: a group holds at most Qg * R rows
-    int pos[kScatterRows];
-    TD a[kScatterRows];
-    TD load = 0;
-    if (T > 0) {
-        TD dv[kScatterRows];
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            dv[t] = deg(min(t * Qg + k, n - 1));
-        });
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            const int p = t * Qg + k;
-            const bool live = k < Qg && t < T && p < n;
-            pos[t] = live ? p : -1;
-            a[t] = live ? dv[t] : TD(0);
-            load += a[t];
-        });
-        sched_swap_rounds(k, Qg, T, pos, a, load);
-    } else {
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
-            pos[t] = -1;
-            a[t] = 0;
-        });
-    }
-    // destinations of the slots (loads issued together), then the slot offsets: the
-    // group's slots follow the edges of the earlier groups, in workgroup order
-    int64_t dd[kScatterRows];
-    static_for<kScatterRows>([&](auto tt) {
-        constexpr int t = decltype(tt)::value;
-        dd[t] = T > 0 ? dst(max(pos[t], 0)) : -1;
+    // destinations of the slots (loads issued together); the slots' degrees to LDS
+    int64_t dd[J];
+    static_for<J>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        dd[j] = (act && T > 0) ? dst(max(pos[j], 0)) : -1;
     });
-    int64_t wl = 0;
-    static_for<kScatterRows>([&](auto tt) {
-        constexpr int t = decltype(tt)::value;
-        if (pos[t] < 0) dd[t] = -1;
-        if (dd[t] < 0) a[t] = 0;
-        wl += a[t];
+    static_for<J>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        const int t = v + 4 * j;
+        if (pos[j] < 0) dd[j] = -1;
+        if (dd[j] < 0) a[j] = 0;
+        if (act && t < kScatterRows) L.a[t][k] = a[j];
     });
-    int64_t xs = wl;  // inclusive scan of the workgroup loads over the lanes
+    __syncthreads();
+    if (!act) return;
+    // slot offsets: the group's slots follow the edges of the earlier groups, in workgroup
+    // order, then slot order
+    TD run[kScatterRows + 1];
+    run[0] = 0;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int64_t y = __shfl_up(xs, off, 64);
-        if (k >= off) xs += y;
+    for (int t = 0; t < kScatterRows; ++t) run[t + 1] = run[t] + (t < R ? L.a[t][k] : TD(0));
+    const int64_t wl = run[kScatterRows];
+    int64_t xs;  // inclusive scan of the workgroup loads over the lanes
+    if constexpr (sizeof(TD) == 4) {
+        xs = wave_incl_scan((int)wl);
+    } else {
+        xs = wl;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int64_t y = __shfl_up(xs, off, 64);
+            if (k >= off) xs += y;
+        }
     }
-    int64_t off = base + (xs - wl);
+    const int64_t off0 = base + (xs - wl);
     if (k < Qg) {
         const int64_t b = b0 + k;
-        static_for<kScatterRows>([&](auto tt) {
-            constexpr int t = decltype(tt)::value;
+        static_for<J>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            const int t = v + 4 * j;
             if (t < R) {
-                row_dst[b * R + t] = dd[t];
-                row_ptr_s[b * R + t] = off;
-                if (dd[t] >= 0) put_soff(dd[t], off);
-                off += a[t];
+                int64_t o = off0;
+                static_for<kScatterRows>([&](auto uu) {
+                    constexpr int u = decltype(uu)::value;
+                    if (u == t) o += run[u];
+                });
+                row_dst[b * R + t] = dd[j];
+                row_ptr_s[b * R + t] = o;
+                if (dd[j] >= 0) put_soff(dd[j], o);
             }
         });
     }
