@@ -613,7 +613,8 @@ torch::Tensor sh_tp_scatter_scheduled(const torch::Tensor& edge_vectors,
 // returns (edge_index int64 [2, E] with row 0 = i, row 1 = j sorted by (i, j),
 // edge_vectors [E, 3] = minimum-image pos[j] - pos[i], row_offsets int64 [N+1]).
 std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
-    const torch::Tensor& positions, const torch::Tensor& cell, double cutoff, bool self_loops) {
+    const torch::Tensor& positions, const torch::Tensor& cell, double cutoff, bool self_loops,
+    int64_t row_capacity) {
     TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
     TORCH_CHECK(positions.dtype() == torch::kFloat32, "positions must be float32");
     TORCH_CHECK(cell.numel() == 9, "cell must be [3, 3]");
@@ -623,12 +624,36 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> neighbor_list(
     const float* h = cell_cpu.data_ptr<float>();
     const float box[3] = {h[0], h[4], h[8]};
     const float rc = (float)cutoff;
-    const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, rc);
-    TORCH_CHECK(wsb > 0, "invalid cell or cutoff");
+    TORCH_CHECK(row_capacity <= 1 << 20, "row_capacity out of range");
     auto i64 = torch::TensorOptions().dtype(torch::kInt64).device(positions.device());
     auto i32 = torch::TensorOptions().dtype(torch::kInt32).device(positions.device());
     const c10::DeviceGuard guard(positions.device());
     hipStream_t s = current_stream(positions);
+    // up to 8192 atoms: three kernels and a scan (row_capacity < 0 takes the passes below)
+    const size_t cwsb = row_capacity >= 0
+                            ? batteries_neighbor_list_cells_workspace_bytes(N, box, rc, (int)row_capacity)
+                            : 0;
+    if (cwsb > 0) {
+        torch::Tensor ws = torch::empty({(int64_t)((cwsb + 7) / 8)}, i64);
+        torch::Tensor offsets = torch::empty({N + 2}, i64);  // [N+1] and E once more
+        check_status(batteries_neighbor_list_cells_count(
+                         cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
+                         (int)row_capacity, ws.data_ptr(), cwsb, offsets.data_ptr<int64_t>(),
+                         nullptr, s),
+                     "neighbor_list");
+        const int64_t E = offsets[N].item<int64_t>();  // one host sync, as in the reference
+        torch::Tensor edge_index = torch::empty({2, E}, i64);
+        torch::Tensor vec = torch::empty({E, 3}, f32_like(positions));
+        check_status(batteries_neighbor_list_cells_write_i64(
+                         cptr<float>(positions, "positions"), box, N, rc, self_loops ? 1 : 0,
+                         (int)row_capacity, ws.data_ptr(), cwsb, offsets.data_ptr<int64_t>(), E,
+                         E ? edge_index.data_ptr<int64_t>() : nullptr,
+                         E ? vec.data_ptr<float>() : nullptr, s),
+                     "neighbor_list");
+        return {edge_index, vec, offsets.narrow(0, 0, N + 1)};
+    }
+    const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, rc);
+    TORCH_CHECK(wsb > 0, "invalid cell or cutoff");
     torch::Tensor ws = torch::empty({(int64_t)((wsb + 7) / 8)}, i64);
     torch::Tensor total = torch::empty({1}, i64);
     check_status(batteries_neighbor_list_count(cptr<float>(positions, "positions"), box, N, rc,
@@ -1032,8 +1057,10 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("cutoff"), py::arg("self_loops") = false,
           "neighbor list in the message-passing layout: (src = j, dst = i, pos[i] - pos[j], row_offsets, spatial_order)");
     m.def("neighbor_list", &neighbor_list, py::arg("positions"), py::arg("cell"),
-          py::arg("cutoff"), py::arg("self_loops") = false,
-          "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], row_offsets)");
+          py::arg("cutoff"), py::arg("self_loops") = false, py::arg("row_capacity") = 0,
+          "Cell-list PBC neighbor list -> (edge_index [2,E] int64, edge_vectors [E,3], "
+          "row_offsets); up to 8192 atoms in three kernels and a scan (row_capacity: entries "
+          "per atom of its slab, 0 = from the density; < 0 takes the general passes)");
     m.def("spatial_order", &spatial_order, py::arg("positions"), py::arg("cell"),
           "Atoms sorted by the Morton code of their cell (2^b cells per axis, the largest "
           "b <= 5 with 8^b <= N)");

@@ -16,6 +16,7 @@
 #include "common.h"
 #include "batmobile_hip.h"
 #include "nl_geom.h"
+#include "nl_cells.h"
 
 #include <cstring>
 #include <vector>
@@ -589,8 +590,9 @@ static int scan_i64(const int64_t* in, int64_t* out, int64_t n, hipStream_t s,
     scan_exclusive_kernel<int64_t><<<1, kScanBlock, 0, s>>>(in, out, n, total_out);
     return (int)hipGetLastError();
 }
-static int scan_i32(const int* in, int64_t* out, int64_t n, hipStream_t s) {
-    scan_exclusive_kernel<int><<<1, kScanBlock, 0, s>>>(in, out, n, nullptr);
+static int scan_i32(const int* in, int64_t* out, int64_t n, hipStream_t s,
+                    int64_t* total_out = nullptr) {
+    scan_exclusive_kernel<int><<<1, kScanBlock, 0, s>>>(in, out, n, total_out);
     return (int)hipGetLastError();
 }
 
@@ -926,6 +928,76 @@ extern "C" int batteries_spatial_order(const float* positions, const float* box,
 // include/neighbor_list.cuh:25-33): library-owned device buffers, freed by
 // neighbor_list_free; cell [3,3] in device memory; one host sync for E.
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// The neighbor list in three kernels and a scan for systems within the limits of
+// nl_cells.h: binning, one workgroup per cell writing each atom's row already sorted
+// by j into a slab, the exclusive scan of the counts, then the rows copied out.
+// ---------------------------------------------------------------------------
+extern "C" size_t batteries_neighbor_list_cells_workspace_bytes(int64_t N, const float* box,
+                                                                float cutoff, int row_capacity) {
+    if (N < 0 || !box || !valid_box(box, cutoff) || row_capacity < 0) return 0;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    if (!cells_supported(N, c)) return 0;
+    return gb_layout(N, gb_row_cap(N, box, cutoff, row_capacity)).total;
+}
+
+extern "C" int batteries_neighbor_list_cells_count(const float* positions, const float* box,
+                                                   int64_t N, float cutoff, int self_loops,
+                                                   int row_capacity, void* workspace,
+                                                   size_t workspace_bytes, int64_t* row_offsets,
+                                                   int64_t* d_num_edges, hipStream_t stream) {
+    if (N < 0 || !box || !valid_box(box, cutoff) || row_capacity < 0 || !row_offsets)
+        return BM_ERR_ARG;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    if (!cells_supported(N, c)) return BM_ERR_ARG;
+    const int rc = gb_row_cap(N, box, cutoff, row_capacity);
+    const GbLayout L = gb_layout(N, rc);
+    if (!workspace || workspace_bytes < L.total) return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    int* pk = reinterpret_cast<int*>(ws + L.pk);
+    int* cnt = reinterpret_cast<int*>(ws + L.cnt);
+    float4* slab = reinterpret_cast<float4*>(ws + L.slab);
+    const int n = (int)N;
+    gb_bin_kernel<<<(unsigned)ceil_div(N, 256), 256, 0, stream>>>(positions, c, n, pk);
+    gb_cell_kernel<<<(unsigned)c.total, kGbBlock, 0, stream>>>(positions, c, n, cutoff * cutoff,
+                                                               self_loops, pk, rc, slab, cnt,
+                                                               nullptr);
+    const int r = scan_i32(cnt, row_offsets, N, stream, d_num_edges);
+    if (r != BM_OK) return r;
+    return (int)hipGetLastError();
+}
+
+template <typename TI>
+static int cells_write(const float* positions, const float* box, int64_t N, float cutoff,
+                       int self_loops, int row_capacity, void* workspace, size_t workspace_bytes,
+                       const int64_t* row_offsets, TI* src, TI* dst, float* edge_vectors,
+                       hipStream_t stream) {
+    if (N < 0 || !box || !valid_box(box, cutoff) || row_capacity < 0 || !row_offsets)
+        return BM_ERR_ARG;
+    const BinCfg c = make_bin_cfg(box, cutoff);
+    if (!cells_supported(N, c)) return BM_ERR_ARG;
+    const int rc = gb_row_cap(N, box, cutoff, row_capacity);
+    const GbLayout L = gb_layout(N, rc);
+    if (!workspace || workspace_bytes < L.total) return BM_ERR_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    gb_rows_kernel<true, TI><<<(unsigned)ceil_div(N, 4), 256, 0, stream>>>(
+        positions, c, (int)N, cutoff * cutoff, self_loops, reinterpret_cast<const int*>(ws + L.pk),
+        rc, reinterpret_cast<const float4*>(ws + L.slab), reinterpret_cast<const int*>(ws + L.cnt),
+        row_offsets, nullptr, nullptr, src, dst, edge_vectors, nullptr);
+    return (int)hipGetLastError();
+}
+
+extern "C" int batteries_neighbor_list_cells_write_i64(
+    const float* positions, const float* box, int64_t N, float cutoff, int self_loops,
+    int row_capacity, void* workspace, size_t workspace_bytes, const int64_t* row_offsets,
+    int64_t num_edges, int64_t* edge_index, float* edge_vectors, hipStream_t stream) {
+    if (num_edges < 0 || (num_edges > 0 && (!edge_index || !edge_vectors))) return BM_ERR_ARG;
+    if (num_edges == 0) return BM_OK;
+    return cells_write<int64_t>(positions, box, N, cutoff, self_loops, row_capacity, workspace,
+                                workspace_bytes, row_offsets, edge_index, edge_index + num_edges,
+                                edge_vectors, stream);
+}
+
 extern "C" int neighbor_list_cuda(const float* positions, const float* cell, int64_t N,
                                   float cutoff, bool self_loops, NeighborListResult* result,
                                   hipStream_t stream) {
@@ -942,6 +1014,56 @@ extern "C" int neighbor_list_cuda(const float* positions, const float* cell, int
     if (e != hipSuccess) return (int)e;
     const float box[3] = {h_cell[0], h_cell[4], h_cell[8]};
     if (!valid_box(box, cutoff)) return BM_ERR_ARG;
+    // systems within the limits of nl_cells.h: three kernels, the scan, one host
+    // synchronisation for E, the rows copied out
+    const size_t cwsb = batteries_neighbor_list_cells_workspace_bytes(N, box, cutoff, 0);
+    if (cwsb > 0) {
+        void* cws = nullptr;
+        int64_t* d_off = nullptr;
+        e = hipMalloc(&cws, cwsb);
+        if (e != hipSuccess) return (int)e;
+        e = hipMalloc(&d_off, sizeof(int64_t) * (size_t)(N + 2));
+        if (e != hipSuccess) {
+            (void)hipFree(cws);
+            return (int)e;
+        }
+        int rc = batteries_neighbor_list_cells_count(positions, box, N, cutoff, self_loops ? 1 : 0,
+                                                     0, cws, cwsb, d_off, d_off + N + 1, stream);
+        int64_t total = 0;
+        if (rc == BM_OK) {
+            e = hipMemcpyAsync(&total, d_off + N + 1, sizeof(int64_t), hipMemcpyDeviceToHost,
+                               stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(stream);
+            rc = (int)e;
+        }
+        if (rc == BM_OK && total > 0) {
+            int* d_ei = nullptr;
+            float* d_vec = nullptr;
+            e = hipMalloc(&d_ei, sizeof(int) * 2 * (size_t)total);
+            if (e == hipSuccess) e = hipMalloc(&d_vec, sizeof(float) * 3 * (size_t)total);
+            if (e != hipSuccess) {
+                if (d_ei) (void)hipFree(d_ei);
+                rc = (int)e;
+            } else {
+                rc = cells_write<int>(positions, box, N, cutoff, self_loops ? 1 : 0, 0, cws, cwsb,
+                                      d_off, d_ei, d_ei + total, d_vec, stream);
+                if (rc == BM_OK) rc = (int)hipStreamSynchronize(stream);
+                if (rc == BM_OK) {
+                    result->d_edge_index = d_ei;
+                    result->d_edge_vectors = d_vec;
+                    result->edge_index = d_ei;
+                    result->edge_vectors = d_vec;
+                    result->num_edges = total;
+                } else {
+                    (void)hipFree(d_ei);
+                    (void)hipFree(d_vec);
+                }
+            }
+        }
+        (void)hipFree(cws);
+        (void)hipFree(d_off);
+        return rc;
+    }
     const size_t wsb = batteries_neighbor_list_workspace_bytes(N, box, cutoff);
     void* ws = nullptr;
     int64_t* d_total = nullptr;

@@ -359,6 +359,32 @@ int batteries_neighbor_list_write_i64(const float* positions, const float* box, 
                                       float* tmp_vec, int64_t* edge_index, float* edge_vectors,
                                       int64_t* row_offsets, hipStream_t stream);
 
+/* The neighbor list in three kernels and a scan, for systems of up to 8192 atoms and
+ * 4096 cells with atoms x cells <= 2^23 (workspace_bytes returns 0 otherwise: use the
+ * count / write calls above): binning, one workgroup per cell writing each atom's
+ * neighbors already sorted by j into a workspace slab of row_capacity entries per atom
+ * (0: chosen from the density; longer rows are found again by the write), and the
+ * exclusive scan of the counts into row_offsets [N+1] (row_offsets[N] = E, also to
+ * *d_num_edges, a device int64, when not NULL).  Write (same workspace, after count):
+ * edge_index [2, num_edges] int64 (row 0 = i, row 1 = j, sorted by (i, j)) and
+ * edge_vectors [num_edges, 3] = minimum-image pos[j] - pos[i], the arrays of
+ * batteries_neighbor_list_write_i64 bit for bit.  neighbor_list_cuda takes this path
+ * for such systems.  Replaces the reference's passes, src/neighbor_list/neighbor_list.cu:
+ * 242-430, for them. */
+size_t batteries_neighbor_list_cells_workspace_bytes(int64_t N, const float* box, float cutoff,
+                                                     int row_capacity);
+int batteries_neighbor_list_cells_count(const float* positions, const float* box, int64_t N,
+                                        float cutoff, int self_loops, int row_capacity,
+                                        void* workspace, size_t workspace_bytes,
+                                        int64_t* row_offsets, int64_t* d_num_edges,
+                                        hipStream_t stream);
+int batteries_neighbor_list_cells_write_i64(const float* positions, const float* box, int64_t N,
+                                            float cutoff, int self_loops, int row_capacity,
+                                            void* workspace, size_t workspace_bytes,
+                                            const int64_t* row_offsets, int64_t num_edges,
+                                            int64_t* edge_index, float* edge_vectors,
+                                            hipStream_t stream);
+
 /* Result of neighbor_list_cuda; same layout as include/neighbor_list.cuh:25-33. */
 typedef struct NeighborListResult {
     int* edge_index;      /* [2, num_edges] int32: row 0 = src i, row 1 = dst j */

@@ -1,5 +1,7 @@
 """GPU parity of the four-kernel graph build (batteries_graph_build_count / _write,
-_batmobile.graph_build, batmobile.Graph for up to 8192 atoms).
+_batmobile.graph_build, batmobile.Graph for up to 8192 atoms), and of the neighbor list
+from the same cell kernels (batteries_neighbor_list_cells_*, _batmobile.neighbor_list
+for up to 8192 atoms) against the general passes (row_capacity < 0).
 
 Every array it returns (edges in the message-passing layout, vectors, row offsets,
 spatial order, schedule and edge_perm) must equal, bit for bit, the general path's
@@ -178,3 +180,32 @@ def test_graph_build_repeated_builds_agree(bm, dev):
     pos2 = pos + 0.3 * torch.randn(pos.shape, generator=gen(93)).to(dev)
     fast, general = _graphs(pos2, cell, 5.0)
     _assert_same(fast, general)
+
+
+@pytest.mark.parametrize("case", ["cfg3", "dense", "self_loops", "cap1", "cap8", "skewed", "tiny"])
+def test_neighbor_list_cells_equal_general_passes(bm, dev, case):
+    """_batmobile.neighbor_list through the cell kernels equals the general passes bit for
+    bit ([2, E] int64 sorted by (i, j), vectors, row offsets), and the C oracle."""
+    cutoff, sl, cap = 5.0, False, 0
+    if case == "dense":
+        pos = torch.rand(3000, 3, generator=gen(81)) * 12.0
+        cell, cutoff = torch.diag(torch.tensor([12.0, 12.0, 12.0])), 4.0
+    elif case == "skewed":
+        L = torch.tensor([31.0, 22.5, 40.0])
+        pos = (torch.rand(2500, 3, generator=gen(82)) * 3.0 - 1.0) * L
+        cell = torch.diag(L)
+    elif case == "tiny":
+        pos = torch.rand(2, 3, generator=gen(83)) * 2.0
+        cell = torch.diag(torch.tensor([20.0, 20.0, 20.0]))
+    else:
+        pos, cell = periodic_box(5000 if case == "cfg3" else 2000, 3 if case == "cfg3" else 84)
+        sl = case == "self_loops"
+        cap = {"cap1": 1, "cap8": 8}.get(case, 0)
+    pos = pos.to(dev)
+    a = bm.neighbor_list(pos, cell, cutoff, sl, cap)
+    b = bm.neighbor_list(pos, cell, cutoff, sl, -1)
+    for x, y, name in zip(a, b, ("edge_index", "vectors", "row_offsets")):
+        assert torch.equal(x, y), name
+    s, d, v = onl.cell_list(pos.cpu().numpy(), cell.numpy(), cutoff, sl)
+    np.testing.assert_array_equal(a[0].cpu().numpy(), np.stack([s, d]))
+    np.testing.assert_array_equal(a[1].cpu().numpy(), v)

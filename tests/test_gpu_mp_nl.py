@@ -331,16 +331,20 @@ def test_neighbor_list_reference_c_abi(bm, dev, libpath):
     np.testing.assert_array_equal(vv, v)
 
 
-def test_neighbor_list_c_abi_long_rows_in_place(bm, dev):
-    """The reference C ABI's int32 layout sorts rows in place: rows of 65..512 neighbours
-    ranked in registers, longer ones ranked from memory and permuted by cycles (ranks held
-    in the source column, which is restored).  The dense cluster of
-    test_neighbor_list_bin_over_1024_atoms_and_rows_over_512 through neighbor_list_cuda."""
+@pytest.mark.parametrize("box", [30.0, 90.0])
+def test_neighbor_list_c_abi_long_rows_in_place(bm, dev, box):
+    """The dense cluster of test_neighbor_list_bin_over_1024_atoms_and_rows_over_512 through
+    neighbor_list_cuda.  In a 30 A box (216 cells) it takes the cell kernels, whose slab rows
+    (sized from the mean density) are far shorter than the cluster's rows: those are found
+    again by the row kernel.  In a 90 A box (5832 cells, past the cell kernels' 4096) it
+    takes the general passes, whose int32 layout sorts rows in place: rows of 65..512
+    neighbours ranked in registers, longer ones ranked from memory and permuted by cycles
+    (ranks held in the source column, which is restored)."""
     g = gen(11)
     dense = torch.rand(1100, 3, generator=g) * 4.6 + 0.2
-    spread = torch.rand(1500, 3, generator=g) * 30.0
+    spread = torch.rand(1500, 3, generator=g) * box
     pos = torch.cat([spread[:700], dense, spread[700:]])
-    cell = torch.diag(torch.tensor([30.0, 30.0, 30.0]))
+    cell = torch.diag(torch.tensor([box, box, box]))
     ei, vv = _nl_c_abi(LIB, dev, pos, cell)
     s, d, v = onl.cell_list(pos.numpy(), cell.numpy(), 5.0)
     assert np.bincount(s).max() > 512
