@@ -82,6 +82,21 @@ __device__ v4i_t struct_buffer_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex
     __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
 constexpr int kMaxBufferStride = 16383;
 
+// Store of a lane's 16 bytes of an MFMA accumulator at base + lane_off (base
+// uniform, in scalar registers), issued from the accumulator registers as
+// inline assembly.  The compiler does not count the store in the vector-memory
+// counter: on gfx9 that counter is shared by loads and stores, and a store it
+// knew of would make it wait for every load in flight at the next use of one.
+// Loads complete in order, so a store it does not know of can only lengthen a
+// wait for a load, never end one early.  The nops cover the SGPR-write ->
+// VMEM-read and the store-data -> VALU-write hazards, which the compiler does
+// not check inside inline assembly.  Nothing in the same kernel may read what
+// this writes.
+__device__ __forceinline__ void store_row_acc(char* base, int lane_off, v4f acc) {
+    asm volatile("s_nop 4\n\tglobal_store_dwordx4 %0, %1, %2\n\ts_nop 1" ::"v"(lane_off), "a"(acc),
+                 "s"(base));
+}
+
 __device__ __forceinline__ v4f mfma4(const float4 a, const float4 b, v4f acc) {
     acc = mfma1(a.x, b.x, acc);
     acc = mfma1(a.y, b.y, acc);

@@ -345,23 +345,18 @@ __global__ __launch_bounds__(kMpBlock) void mp_simple_mfma_kernel(
 //     gathers row 0 of the same tensor, a valid address whose value is never
 //     used: edges past the end only touch the accumulator after the block's
 //     last row has been written or staged);
-//   - a row that closes inside a batch is staged in LDS (kStageSlots per wave)
-//     and written to HBM during the next batch's phase 1, after the edge
-//     records it needs are in registers: the drain that the stores force then
-//     happens at the first gather of phase 2, by which time phase 1 has covered
-//     the latency of the gathers and of the stores;
-//   - a batch in which more than kStageSlots rows close (rows much shorter
-//     than the batch) takes a copy of the loop that writes each row as it
-//     closes and drains the counter at the end of the batch;
-//   - the last batch issues no gathers for a next batch, stages its rows the
-//     same way, and the remaining rows are written after it.
+//   - a row that closes is written where it closes, straight from the MFMA
+//     accumulator, by a store the compiler does not see (store_row_acc): the
+//     gathers' waits stay exact, because loads complete in order and a store
+//     only ever adds to the count (a wait for a gather with a store in flight
+//     can only last longer, never end before the gather is in);
+//   - the last batch issues no gathers for a next batch.
 // The per-edge control is one scalar bit test: `ends` (a 64-bit mask per batch,
 // built with scalar arithmetic from the row ends) marks the edges that close a
-// row; there the accumulator is staged (or written) and reset to zero.
+// row; there the accumulator is written and reset to zero.
 // ---------------------------------------------------------------------------
 constexpr int kSBatch = 64;       // edges per batch (operators in LDS, one edge per lane in phase 1)
 constexpr int kRing = 32;         // gathers in flight per lane (edges ahead)
-constexpr int kStageSlots = 3;    // rows staged per wave between two flushes
 constexpr int kLdsAhead = 3;      // operator rows read from LDS this many edges ahead
 
 template <bool NORM, bool BUF, bool PERM, bool IDX>
@@ -373,9 +368,8 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     static_assert(kSBatch == 64, "one edge per lane in phase 1, 64-bit row-end mask");
     static_assert(kSBatch % kRing == 0, "ring slots must line up across batches");
     static_assert(!IDX || BUF, "index-mode gathers use the buffer descriptor");
-    // 66.5 KB + 12 KB + row ranges: two workgroups per compute unit
+    // 66.5 KB + row ranges: two workgroups per compute unit
     __shared__ __attribute__((aligned(16))) float sM[kSBatch * kMStride];
-    __shared__ float4 sStage[4][kStageSlots][64];
     __shared__ int64_t sRow[kScatterRows + 1];
     __shared__ int64_t sDst[kScatterRows];
     __shared__ int64_t sNE[kScatterRows];  // output rows of the non-empty rows, in row order
@@ -455,12 +449,12 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
     v4f acc = zero4;
 
-    // Non-empty rows close in row order: k_ne of them have closed, k_out of
-    // those are written, and rows k_out .. k_ne-1 sit in sStage[w][0 ..).
-    int k_ne = 0, k_out = 0;
-    auto flush = [&]() {
-        for (int s = 0; k_out < k_ne; ++s, ++k_out) put_out(sNE[k_out], sStage[w][s][lane]);
-    };
+    // Non-empty rows close in row order: k_ne of them have closed.  onext is
+    // the output row of the next one, read from LDS at the previous close (or
+    // here) so that a close never waits for it.
+    int k_ne = 0;
+    int64_t onext = sNE[0];
+    const int lane_off = c * 64 + g * 16;  // byte offset of the lane's float4 in an output row
     EdgeRec cur = record(edge_id(e0));
     EdgeRec nxt = record(edge_id(e0 + kSBatch));
     int64_t id2 = edge_id(e0 + 2 * kSBatch);
@@ -486,11 +480,8 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     int gsrc = 0, lsel = 0;
     uint32_t ends_h = 0;
     int64_t kh = e0;
-    int direct = 0;  // wave-uniform: rows of this batch are written as they close
     // edge j of a half: four MFMAs into the row accumulator, the gather of the
-    // edge kRing positions ahead (GATHER), and where j closes a row its staging
-    // or, in a batch with more closing rows than staging slots, its store,
-    // waited for at once so that no store is pending where the paths meet
+    // edge kRing positions ahead (GATHER), and where j closes a row its store
     auto edge = [&](auto jj, auto gather_c) {
         constexpr int j = decltype(jj)::value;
         // IDX: one wait per pair of edges, at the even one, for both edges'
@@ -529,15 +520,11 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         // rare: laid out off the edge path, so that an edge that closes no row
         // falls through (no taken branch, 54.2 -> 53.0 us at configs[3])
         if (__builtin_expect((ends_h >> j) & 1u, 0)) {
-            const float4 v = make_float4(acc[0], acc[1], acc[2], acc[3]);
-            if (direct == 0) {
-                sStage[w][k_ne - k_out][lane] = v;
-            } else {
-                put_out(sNE[k_ne], v);
-                ++k_out;
-                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-            }
+            const int64_t orow = uniform_i64(onext);
+            if (c < C && orow >= 0)
+                store_row_acc(reinterpret_cast<char*>(out) + orow * (int64_t)row_bytes, lane_off, acc);
             ++k_ne;
+            onext = sNE[min(k_ne, kScatterRows - 1)];
             acc = zero4;
         }
     };
@@ -552,16 +539,8 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         // records of batch b+2 and the edge ids of b+3 (no load past e1)
         const EdgeRec nn = record(id2);
         id2 = edge_id(kb + 3 * kSBatch);
-        // the wait for this batch's records comes before the flush's stores
-        // (after them it would be a full drain): the empty asm takes the
-        // record as an operand, so its wait is placed here
-        asm volatile("" : "+v"(cur.x), "+v"(cur.y), "+v"(cur.z));
         float Y[16];
         edge_sh<NORM>(cur, Y);
-        // rows closed in the previous batch go to HBM here (see above)
-        __builtin_amdgcn_sched_barrier(0);
-        flush();
-        __builtin_amdgcn_sched_barrier(0);
         if (lane < nb) edge_rows(Y, sM + lane * kMStride, w);
         if constexpr (IDX)
             if (w == 0) sTgt[(lane + kRing) & (kSBatch - 1)] = lane >= kRing ? cur.src : nxt.src;
@@ -573,11 +552,10 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             const int p = row_last[r] - rel;
             if (row_last[r] >= 0 && p >= 0 && p < kSBatch) ends |= 1ull << p;
         });
-        direct = __builtin_amdgcn_readfirstlane(__builtin_popcountll(ends) > kStageSlots ? 1 : 0);
-        // The flush's stores (and this batch's record loads) are waited for
-        // here, at the end of phase 1, where they have had its whole length to
-        // complete: pending at the half loop's header, they would make the
-        // compiler drain the gathers at the first edge of every half.
+        // This batch's record loads are waited for here, at the end of phase
+        // 1, where they have had its whole length to complete: pending at the
+        // half loop's header, they would make the compiler drain the gathers
+        // at the first edge of every half.
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
         static_for<kLdsAhead>([&](auto qq) {
@@ -630,7 +608,6 @@ partial:
             });
     });
 done:
-    flush();
     for (int r = 0; r < nrows; ++r)
         if (sRow[r + 1] == sRow[r]) put_out(sDst[r], make_float4(0.f, 0.f, 0.f, 0.f));
 }
