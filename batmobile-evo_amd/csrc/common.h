@@ -355,6 +355,18 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
     return x;
 }
 
+// OR of x over lanes 0..15, returned uniform: row_shr 1, 2, 4, 8 inside the first row
+// of 16 lanes (lanes with no source take 0), then lane 15.  Every lane of the wave
+// must execute it.
+__device__ __forceinline__ uint32_t row0_or(uint32_t x) {
+    int v = (int)x;
+    v |= __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+    v |= __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+    v |= __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+    v |= __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_readlane(v, 15);
+}
+
 }  // namespace bmhip
 
 // Status codes returned by the C ABI (0 = success).

@@ -406,23 +406,20 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     auto put_out = [&](int64_t orow, float4 v) {
         if (c < C && orow >= 0) *reinterpret_cast<float4*>(out + (orow * C + c) * 16 + 4 * g) = v;
     };
-    // list the non-empty rows (the empty ones are written as zeros at the end)
-    if (threadIdx.x < nrows && sRow[threadIdx.x + 1] > sRow[threadIdx.x]) {
-        int k = 0;
-        for (int i = 0; i < (int)threadIdx.x; ++i) k += sRow[i + 1] > sRow[i] ? 1 : 0;
-        sNE[k] = sDst[threadIdx.x];
+    // list the non-empty rows (the empty ones are written as zeros at the end): wave
+    // 0, the rank of a row among them from a ballot
+    if (threadIdx.x < 64) {
+        const bool ne = (int)threadIdx.x < nrows && sRow[threadIdx.x + 1] > sRow[threadIdx.x];
+        const uint64_t m = __ballot(ne);
+        if (ne) sNE[__builtin_popcountll(m & ((1ull << threadIdx.x) - 1))] = sDst[threadIdx.x];
     }
     __syncthreads();
 
-    // Last edge of each non-empty row, relative to e0 (-1: empty or absent row).
-    // Wave-uniform, kept in scalar registers.
-    int row_last[kScatterRows];
-    static_for<kScatterRows>([&](auto rr) {
-        constexpr int r = decltype(rr)::value;
-        int v = -1;
-        if (r < nrows && sRow[r + 1] > sRow[r]) v = (int)(sRow[r + 1] - 1 - e0);
-        row_last[r] = __builtin_amdgcn_readfirstlane(v);
-    });
+    // Lane r < nrows: the last edge of row r relative to e0 (-1: empty or absent
+    // row).  The row ends in a batch are then a few lane-parallel instructions and a
+    // 16-lane OR, not a scalar test per row.
+    int rlast = -1;
+    if (lane < nrows && sRow[lane + 1] > sRow[lane]) rlast = (int)(sRow[lane + 1] - 1 - e0);
 
     // Edge records move through a three-stage pipeline so that no wait is on a
     // load younger than the gathers in flight: the edge id of batch b+3 (one
@@ -455,6 +452,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     int k_ne = 0;
     int64_t onext = sNE[0];
     const int lane_off = c * 64 + g * 16;  // byte offset of the lane's float4 in an output row
+    const bool tile_full = blockIdx.y * kChanGroup + w * 16 + 16 <= C;  // wave-uniform
     EdgeRec cur = record(edge_id(e0));
     EdgeRec nxt = record(edge_id(e0 + kSBatch));
     int64_t id2 = edge_id(e0 + 2 * kSBatch);
@@ -521,7 +519,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         // falls through (no taken branch, 54.2 -> 53.0 us at configs[3])
         if (__builtin_expect((ends_h >> j) & 1u, 0)) {
             const int64_t orow = uniform_i64(onext);
-            if (c < C && orow >= 0)
+            if (orow >= 0 && (tile_full || c < C))
                 store_row_acc(reinterpret_cast<char*>(out) + orow * (int64_t)row_bytes, lane_off, acc);
             ++k_ne;
             onext = sNE[min(k_ne, kScatterRows - 1)];
@@ -544,14 +542,16 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         if (lane < nb) edge_rows(Y, sM + lane * kMStride, w);
         if constexpr (IDX)
             if (w == 0) sTgt[(lane + kRing) & (kSBatch - 1)] = lane >= kRing ? cur.src : nxt.src;
-        // edges of this batch that close a row
+        // edges of this batch that close a row (distinct rows end at distinct edges)
         const int rel = (int)(kb - e0);
-        uint64_t ends = 0;
-        static_for<kScatterRows>([&](auto rr) {
-            constexpr int r = decltype(rr)::value;
-            const int p = row_last[r] - rel;
-            if (row_last[r] >= 0 && p >= 0 && p < kSBatch) ends |= 1ull << p;
-        });
+        uint64_t ends;
+        {
+            const int p = rlast - rel;
+            const bool in = rlast >= 0 && p >= 0 && p < kSBatch;
+            const uint32_t lo = (in && p < 32) ? 1u << (p & 31) : 0u;
+            const uint32_t hi = (in && p >= 32) ? 1u << (p & 31) : 0u;
+            ends = ((uint64_t)row0_or(hi) << 32) | row0_or(lo);
+        }
         // This batch's record loads are waited for here, at the end of phase
         // 1, where they have had its whole length to complete: pending at the
         // half loop's header, they would make the compiler drain the gathers
