@@ -446,11 +446,17 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
     v4f acc = zero4;
 
-    // Non-empty rows close in row order: k_ne of them have closed.  onext is
-    // the output row of the next one, read from LDS at the previous close (or
-    // here) so that a close never waits for it.
+    // Non-empty rows close in row order: k_ne of them have closed.  Lane k holds
+    // the byte offset of the k-th one's output row (-1: none), which a close takes
+    // with two lane reads.
     int k_ne = 0;
-    int64_t onext = sNE[0];
+    int64_t obyte = -1;
+    if (lane < kScatterRows) {
+        const int64_t orow = sNE[lane];
+        if (lane < __builtin_popcountll(__ballot(lane < nrows && sRow[lane + 1] > sRow[lane])) && orow >= 0)
+            obyte = orow * (int64_t)row_bytes;
+    }
+    const int ob_lo = (int)(uint32_t)obyte, ob_hi = (int)((uint64_t)obyte >> 32);
     const int lane_off = c * 64 + g * 16;  // byte offset of the lane's float4 in an output row
     const bool tile_full = blockIdx.y * kChanGroup + w * 16 + 16 <= C;  // wave-uniform
     EdgeRec cur = record(edge_id(e0));
@@ -518,11 +524,12 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         // rare: laid out off the edge path, so that an edge that closes no row
         // falls through (no taken branch, 54.2 -> 53.0 us at configs[3])
         if (__builtin_expect((ends_h >> j) & 1u, 0)) {
-            const int64_t orow = uniform_i64(onext);
-            if (orow >= 0 && (tile_full || c < C))
-                store_row_acc(reinterpret_cast<char*>(out) + orow * (int64_t)row_bytes, lane_off, acc);
+            const int hi = __builtin_amdgcn_readlane(ob_hi, k_ne);
+            const int64_t ob = (int64_t)(((uint64_t)(uint32_t)hi << 32) |
+                                         (uint32_t)__builtin_amdgcn_readlane(ob_lo, k_ne));
+            if (hi >= 0 && (tile_full || c < C))
+                store_row_acc(reinterpret_cast<char*>(out) + ob, lane_off, acc);
             ++k_ne;
-            onext = sNE[min(k_ne, kScatterRows - 1)];
             acc = zero4;
         }
     };
