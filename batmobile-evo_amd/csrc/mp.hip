@@ -58,6 +58,30 @@ __device__ __forceinline__ void build_rows(const float* Y, float* sMj) {
     });
 }
 
+// The scatter kernel's phase 1: wave 0 also computes the next batch's Y (into LDS, for
+// all four waves), so it builds fewer rows.  Rows per wave (-1: none) chosen so that the
+// waves' VALU work comes out nearly equal: Y (about 45 instructions) + 126 CG terms,
+// 164, 162 and 159 terms, against 45 + 152-154 terms in every wave when each computes Y.
+constexpr int kRowsOfWaveSh[4][5] = {
+    {7, 9, 13, -1, -1}, {5, 8, 10, 14, -1}, {1, 2, 3, 4, -1}, {0, 6, 11, 12, 15}};
+
+template <int W>
+__device__ __forceinline__ void build_rows_sh(const float* Y, float* sMj) {
+    static_for<5>([&](auto rr) {
+        constexpr int o = kRowsOfWaveSh[W][decltype(rr)::value];
+        if constexpr (o >= 0) {
+            constexpr int sw = quad_swizzle(o);
+            float m[16];
+            edge_operator_row<o>(Y, m);
+            float4* dst = reinterpret_cast<float4*>(sMj + o * 16);
+            dst[0 ^ sw] = make_float4(m[0], m[1], m[2], m[3]);
+            dst[1 ^ sw] = make_float4(m[4], m[5], m[6], m[7]);
+            dst[2 ^ sw] = make_float4(m[8], m[9], m[10], m[11]);
+            dst[3 ^ sw] = make_float4(m[12], m[13], m[14], m[15]);
+        }
+    });
+}
+
 // One edge of a batch as seen by the lane that owns it in phase 1.
 struct EdgeRec {
     float x, y, z;
@@ -375,6 +399,9 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     __shared__ int64_t sNE[kScatterRows];  // output rows of the non-empty rows, in row order
     // IDX: source rows of the gather targets, entry t for edge kb + kRing + t
     __shared__ int sTgt[kSBatch];
+    // Y of a batch's edges (lane j: edge j), written by wave 0 one batch ahead; two
+    // buffers by batch parity.  Lane j's four quads at j * 16, quad q at q ^ (j >> 1 & 3).
+    __shared__ __attribute__((aligned(16))) float sYb[2][kSBatch * 16];
 
     const int per_xcd = (n_logical + 7) / 8;
     const int logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
@@ -533,7 +560,35 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
             acc = zero4;
         }
     };
+    // Y in LDS: lane j's 16 values as four swizzled quads
+    auto put_y = [&](float* buf, const float* Yv) {
+        float4* q = reinterpret_cast<float4*>(buf + lane * 16);
+        const int sw = (lane >> 1) & 3;
+        static_for<4>([&](auto qq) {
+            constexpr int k = decltype(qq)::value;
+            q[k ^ sw] = make_float4(Yv[4 * k], Yv[4 * k + 1], Yv[4 * k + 2], Yv[4 * k + 3]);
+        });
+    };
+    auto get_y = [&](const float* buf, float* Yv) {
+        const float4* q = reinterpret_cast<const float4*>(buf + lane * 16);
+        const int sw = (lane >> 1) & 3;
+        static_for<4>([&](auto qq) {
+            constexpr int k = decltype(qq)::value;
+            const float4 v = q[k ^ sw];
+            Yv[4 * k] = v.x;
+            Yv[4 * k + 1] = v.y;
+            Yv[4 * k + 2] = v.z;
+            Yv[4 * k + 3] = v.w;
+        });
+    };
+    int ypar = 0;
     if (e0 == e1) goto done;
+    // the first batch's Y, for the first phase 1 (after the barrier at the top of the loop)
+    if (w == 0) {
+        float Y0[16];
+        edge_sh<NORM>(cur, Y0);
+        put_y(sYb[0], Y0);
+    }
     static_for<kRing>([&](auto uu) {
         constexpr int u = decltype(uu)::value;
         ring[u] = gather<BUF>(X, xr, voff, __builtin_amdgcn_readlane(cur.src, u), row_bytes);
@@ -544,9 +599,26 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         // records of batch b+2 and the edge ids of b+3 (no load past e1)
         const EdgeRec nn = record(id2);
         id2 = edge_id(kb + 3 * kSBatch);
-        float Y[16];
-        edge_sh<NORM>(cur, Y);
-        if (lane < nb) edge_rows(Y, sM + lane * kMStride, w);
+        // wave 0: Y of the next batch's edges; every wave: its rows of this batch's
+        // operators from this batch's Y (written one batch ago)
+        if (w == 0) {
+            float Yn[16];
+            edge_sh<NORM>(nxt, Yn);
+            put_y(sYb[ypar ^ 1], Yn);
+        }
+        {
+            float Y[16];
+            get_y(sYb[ypar], Y);
+            if (lane < nb) {
+                switch (w) {
+                    case 0: build_rows_sh<0>(Y, sM + lane * kMStride); break;
+                    case 1: build_rows_sh<1>(Y, sM + lane * kMStride); break;
+                    case 2: build_rows_sh<2>(Y, sM + lane * kMStride); break;
+                    default: build_rows_sh<3>(Y, sM + lane * kMStride); break;
+                }
+            }
+        }
+        ypar ^= 1;
         if constexpr (IDX)
             if (w == 0) sTgt[(lane + kRing) & (kSBatch - 1)] = lane >= kRing ? cur.src : nxt.src;
         // edges of this batch that close a row (distinct rows end at distinct edges)
