@@ -392,6 +392,7 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     static_assert(kSBatch == 64, "one edge per lane in phase 1, 64-bit row-end mask");
     static_assert(kSBatch % kRing == 0, "ring slots must line up across batches");
     static_assert(!IDX || BUF, "index-mode gathers use the buffer descriptor");
+    static_assert(kScatterRows <= 16, "row ends gathered by a 16-lane OR (row0_or)");
     // 66.5 KB + row ranges: two workgroups per compute unit
     __shared__ __attribute__((aligned(16))) float sM[kSBatch * kMStride];
     __shared__ int64_t sRow[kScatterRows + 1];
