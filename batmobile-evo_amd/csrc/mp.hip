@@ -487,9 +487,12 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
     const int ob_lo = (int)(uint32_t)obyte, ob_hi = (int)((uint64_t)obyte >> 32);
     const int lane_off = c * 64 + g * 16;  // byte offset of the lane's float4 in an output row
     const bool tile_full = blockIdx.y * kChanGroup + w * 16 + 16 <= C;  // wave-uniform
+    // IDX: after the first batch's (the ring fill's source rows) only wave 0 uses the
+    // records (Y into LDS, gather indices into sTgt), so the other waves skip them
+    const bool recs = !IDX || w == 0;  // wave-uniform
     EdgeRec cur = record(edge_id(e0));
-    EdgeRec nxt = record(edge_id(e0 + kSBatch));
-    int64_t id2 = edge_id(e0 + 2 * kSBatch);
+    EdgeRec nxt = recs ? record(edge_id(e0 + kSBatch)) : EdgeRec{0.f, 0.f, 0.f, 0};
+    int64_t id2 = recs ? edge_id(e0 + 2 * kSBatch) : (int64_t)-1;
     // Every wave runs the edge loop, also one whose 16 channels are all past C
     // (its lanes read channel C-1 and never store): a branch around the loop
     // would make the loop-carried records look like the youngest loads on one
@@ -598,8 +601,8 @@ __global__ __launch_bounds__(kMpBlock) void mp_scatter_kernel(
         const int nb = (int)min<int64_t>(kSBatch, e1 - kb);
         __syncthreads();
         // records of batch b+2 and the edge ids of b+3 (no load past e1)
-        const EdgeRec nn = record(id2);
-        id2 = edge_id(kb + 3 * kSBatch);
+        const EdgeRec nn = recs ? record(id2) : EdgeRec{0.f, 0.f, 0.f, 0};
+        if (recs) id2 = edge_id(kb + 3 * kSBatch);
         // wave 0: Y of the next batch's edges; every wave: its rows of this batch's
         // operators from this batch's Y (written one batch ago)
         if (w == 0) {
