@@ -506,6 +506,29 @@ torch::Tensor sh_tp_scatter_weighted(const torch::Tensor& edge_vectors,
     return out;
 }
 
+// Extension: the weighted scatter's processing order with each XCD's tiles sorted by
+// decreasing edge count (batteries_weighted_tile_order).
+torch::Tensor weighted_tile_order(const c10::optional<torch::Tensor>& order,
+                                  const torch::Tensor& row_ptr) {
+    TORCH_CHECK(row_ptr.dim() == 1 && row_ptr.dtype() == torch::kInt64 && row_ptr.numel() >= 1,
+                "row_ptr must be int64 [N_dst + 1]");
+    check_device(row_ptr, "row_ptr");
+    const int64_t N_dst = row_ptr.numel() - 1;
+    const int64_t* op = nullptr;
+    if (order.has_value() && order->defined()) {
+        TORCH_CHECK(order->dtype() == torch::kInt64 && order->numel() == N_dst,
+                    "order must be int64 [N_dst]");
+        op = cptr<int64_t>(*order, "order");
+    }
+    const c10::DeviceGuard guard(row_ptr.device());
+    torch::Tensor out = torch::empty({N_dst}, row_ptr.options());
+    check_status(batteries_weighted_tile_order(op, cptr<int64_t>(row_ptr, "row_ptr"), N_dst,
+                                               mptr<int64_t>(out, "order_out"),
+                                               current_stream(row_ptr)),
+                 "weighted_tile_order");
+    return out;
+}
+
 // Extension: atoms in Morton order of a 32^3 grid over the (orthorhombic) box.
 torch::Tensor spatial_order(const torch::Tensor& positions, const torch::Tensor& cell) {
     TORCH_CHECK(positions.dim() == 2 && positions.size(1) == 3, "positions must be [N, 3]");
@@ -1049,6 +1072,8 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("source_idx"), py::arg("row_ptr"), py::arg("perm") = py::none(),
           py::arg("normalize") = false,
           "Fused SH + simple TP + scatter-add over CSR rows (no messages tensor, no atomics)");
+    m.def("weighted_tile_order", &weighted_tile_order, py::arg("order"), py::arg("row_ptr"),
+          "Processing order for sh_tp_scatter_weighted: each XCD's tiles by decreasing edge count");
     m.def("sh_tp_scatter_weighted", &sh_tp_scatter_weighted, py::arg("edge_vectors"),
           py::arg("node_features"), py::arg("weights"), py::arg("source_idx"), py::arg("row_ptr"),
           py::arg("perm") = py::none(), py::arg("order") = py::none(), py::arg("normalize") = true,

@@ -1720,7 +1720,93 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// ---------------------------------------------------------------------------
+// Processing order for the weighted scatter with the heaviest tiles first.  The kernel
+// deals tile k of XCD x (4 destinations at positions 4 (x P + k) .. + 3 of the order,
+// P = ceil(tiles / 8)) to its workgroup x + 8 k, and the hardware starts workgroups in
+// index order as slots free up: at configs[3] 1250 tiles fill 512 slots 2.44 times, and
+// the last partial round runs at half occupancy.  Sorting each XCD's tiles by decreasing
+// edge count (ties by position) starts the long ones first and leaves short ones for the
+// end (largest-first list scheduling); the spatial ranges of the XCDs, and so their L2
+// footprints, stay as they were.  One workgroup per XCD range: keys (inverted edge
+// count, tile) in LDS, bitonic sort.  A partial last tile keeps its place.
+// ---------------------------------------------------------------------------
+constexpr int kTileSortMax = 4096;  // tiles per XCD range sorted in LDS (more: order copied)
+
+__global__ __launch_bounds__(1024) void wf_tile_order_kernel(const int64_t* __restrict__ order,
+                                                             const int64_t* __restrict__ row_ptr,
+                                                             int64_t n_dst, int64_t per_xcd,
+                                                             int64_t* __restrict__ out) {
+    __shared__ uint64_t key[kTileSortMax];
+    const int64_t ntile = (n_dst + 3) / 4;
+    const int64_t t0 = (int64_t)blockIdx.x * per_xcd;
+    const int64_t t1 = min(ntile, t0 + per_xcd);
+    if (t0 >= t1) return;
+    // the last tile of all stays in place when it is partial
+    const int64_t tsort = (t1 == ntile && (n_dst & 3)) ? t1 - 1 : t1;
+    const int T = (int)(tsort - t0);
+    auto dst_at = [&](int64_t pos) -> int64_t { return order ? order[pos] : pos; };
+    int Tp = 1;
+    while (Tp < T) Tp <<= 1;
+    for (int k = threadIdx.x; k < Tp; k += blockDim.x) {
+        uint64_t v = ~0ull;
+        if (k < T) {
+            int64_t w = 0;
+            for (int i = 0; i < 4; ++i) {
+                const int64_t d = dst_at(4 * (t0 + k) + i);
+                if (d >= 0 && d < n_dst) w += row_ptr[d + 1] - row_ptr[d];
+            }
+            const uint32_t wc = (uint32_t)min<int64_t>(w, 0xfffffffell);
+            v = ((uint64_t)(0xffffffffu - wc) << 32) | (uint32_t)k;
+        }
+        key[k] = v;
+    }
+    __syncthreads();
+    for (int size = 2; size <= Tp; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < Tp; i += blockDim.x) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = (i & size) == 0;
+                    const uint64_t a = key[i], b = key[j];
+                    if ((a > b) == up) {
+                        key[i] = b;
+                        key[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int64_t q = threadIdx.x; q < 4 * (t1 - t0); q += blockDim.x) {
+        const int64_t j = q >> 2;  // position in the range
+        const int64_t k = j < T ? (int64_t)(uint32_t)key[j] : j;
+        const int64_t pos = 4 * (t0 + k) + (q & 3), opos = 4 * (t0 + j) + (q & 3);
+        if (opos < n_dst) out[opos] = pos < n_dst ? dst_at(pos) : -1;
+    }
+}
+
+__global__ void wf_copy_order_kernel(const int64_t* __restrict__ order, int64_t n,
+                                     int64_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = order ? order[i] : i;
+}
+
 }  // namespace bmhip
+
+extern "C" int batteries_weighted_tile_order(const int64_t* order, const int64_t* row_ptr,
+                                            int64_t N_dst, int64_t* order_out, hipStream_t stream) {
+    if (N_dst < 0 || !row_ptr || !order_out) return BM_ERR_ARG;
+    if (N_dst == 0) return BM_OK;
+    const int64_t ntile = ceil_div(N_dst, 4);
+    const int64_t per_xcd = ceil_div(ntile, 8);
+    if (per_xcd <= kTileSortMax)
+        wf_tile_order_kernel<<<8, 1024, 0, stream>>>(order, row_ptr, N_dst, per_xcd, order_out);
+    else
+        wf_copy_order_kernel<<<(unsigned)ceil_div(N_dst, 256), 256, 0, stream>>>(order, N_dst,
+                                                                                 order_out);
+    return (int)hipGetLastError();
+}
 
 extern "C" size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges,
                                                                    int C_in, int C_out) {

@@ -195,8 +195,8 @@ int batteries_sh_tp_scatter_scheduled(const float* edge_vectors, const float* no
  * 152-168), without the [E, C_out, 16] messages.  order (optional, [N_dst]) is the
  * order in which destinations are processed: a permutation of 0..N_dst-1 (a spatial
  * order keeps source rows in L2); entries outside [0, N_dst) are skipped, leaving rows
- * that no entry names unwritten.  Workspace: per-edge Y and source rows, the per-path sums
- * [N_dst][156][16 ceil(C_in / 16)] and W transposed to [34][C_out][16 ceil(C_in / 16)]. */
+ * that no entry names unwritten.  One fused kernel, no workspace (the workspace size is 0;
+ * the arguments are kept for callers written against a version that had one). */
 size_t batteries_sh_tp_scatter_weighted_workspace_bytes(int64_t N_dst, int64_t N_edges, int C_in,
                                                         int C_out);
 int batteries_sh_tp_scatter_weighted(const float* edge_vectors, const float* node_features,
@@ -206,6 +206,16 @@ int batteries_sh_tp_scatter_weighted(const float* edge_vectors, const float* nod
                                      int64_t N_dst, int64_t N_edges, int C_in, int C_out,
                                      int normalize, void* workspace, size_t workspace_bytes,
                                      hipStream_t stream);
+
+/* Extension with no counterpart in the reference (like the spatial order): a processing
+ * order for batteries_sh_tp_scatter_weighted that keeps each XCD's range of 4-destination
+ * tiles (as the kernel deals them) and sorts its tiles by decreasing edge count, ties by
+ * position, so that the longest tiles start first; a partial last tile keeps its place.
+ * order (nullable: 0..N_dst-1) is the order to rearrange, row_ptr the CSR rows [N_dst + 1];
+ * order_out [N_dst].  Ranges of more than 4096 tiles are copied unchanged.  The results of
+ * the weighted scatter do not depend on the order. */
+int batteries_weighted_tile_order(const int64_t* order, const int64_t* row_ptr, int64_t N_dst,
+                                  int64_t* order_out, hipStream_t stream);
 
 /* node_output[N_atoms, C, 16]; CSR slot k is edge col_idx[k], whose source is
  * edge_index[0, col_idx[k]] and vector edge_vectors[col_idx[k]].

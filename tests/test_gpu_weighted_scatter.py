@@ -160,3 +160,52 @@ def test_config3_weighted_full_size(bm, dev):
                                         x.cpu().double().numpy(), w.cpu().double().numpy(),
                                         graph.src.cpu()[ks].numpy(), dloc.numpy(), pick.numel())
     assert normwise_err(out.cpu()[pick], want) <= 1e-5
+
+
+def _tile_order_expected(order, deg, n):
+    """Each XCD range of 4-destination tiles (P = ceil(tiles / 8) per range, as the weighted
+    kernel deals them) sorted by decreasing edge count, ties by position; a partial last
+    tile stays last."""
+    ntile = (n + 3) // 4
+    per = (ntile + 7) // 8
+    out = order.copy()
+    for x in range(8):
+        t0, t1 = x * per, min(ntile, (x + 1) * per)
+        if t0 >= t1:
+            continue
+        ts = t1 - 1 if (t1 == ntile and n % 4) else t1
+        w = [int(deg[order[4 * t:4 * t + 4]].sum()) for t in range(t0, ts)]
+        idx = sorted(range(ts - t0), key=lambda k: (-w[k], k))
+        for j, k in enumerate(idx):
+            out[4 * (t0 + j):4 * (t0 + j) + 4] = order[4 * (t0 + k):4 * (t0 + k) + 4]
+    return out
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 31, 33, 130, 1001, 5000, 16390])
+def test_weighted_tile_order(bm, dev, n):
+    """batteries_weighted_tile_order against a direct statement of the rule, for sizes with
+    empty XCD ranges, a partial last tile and ranges of one tile; and the weighted scatter
+    is bit-identical in the sorted and the spatial order."""
+    g = gen(80 + n)
+    deg = torch.randint(0, 60, (n,), generator=g)
+    deg[torch.rand(n, generator=g) < 0.1] = 0
+    rp = torch.zeros(n + 1, dtype=torch.int64)
+    rp[1:] = torch.cumsum(deg, 0)
+    order = torch.randperm(n, generator=g)
+    got = bm.weighted_tile_order(order.to(dev), rp.to(dev)).cpu().numpy()
+    want = _tile_order_expected(order.numpy(), deg.numpy(), n)
+    np.testing.assert_array_equal(got, want)
+    got_id = bm.weighted_tile_order(None, rp.to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got_id, _tile_order_expected(np.arange(n), deg.numpy(), n))
+    if n <= 1001:
+        e = int(rp[-1])
+        dst = torch.repeat_interleave(torch.arange(n), deg)
+        src = torch.randint(0, n, (e,), generator=g)
+        vec = unit_vectors(e, 81) * 1.5 if e else torch.zeros(0, 3)
+        x = torch.randn(n, 16, 16, generator=g)
+        w = _weights(16, 16, 82)
+        a = bm.sh_tp_scatter_weighted(vec.to(dev), x.to(dev), w.to(dev), src.to(dev), rp.to(dev),
+                                      None, order.to(dev), True)
+        b = bm.sh_tp_scatter_weighted(vec.to(dev), x.to(dev), w.to(dev), src.to(dev), rp.to(dev),
+                                      None, torch.from_numpy(got).to(dev), True)
+        assert torch.equal(a, b)
