@@ -1536,7 +1536,8 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
         deg = __builtin_amdgcn_readfirstlane((int)(b - a));
     }
     // k-steps of 4 edges, padded to a multiple of 2 (the unroll of the pipeline below);
-    // padding steps and lanes past the last edge have Y = 0 and source 0 (a valid row)
+    // padding steps and lanes past the last edge have Y = 0 and source 0 (a valid row), and
+    // the padding step runs no MFMAs
     const int nst = (deg + 3) >> 2;
     const int nst2 = (nst + 1) & ~1;
     const int nseg = (nst2 + kWfSegSteps - 1) / kWfSegSteps;  // 0: no edges
@@ -1629,18 +1630,21 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
             for (int sg = 0; sg < nseg; ++sg) {
                 const int s0 = sg * kWfSegSteps;
                 const int len = min(kWfSegSteps, nst2 - s0);  // even
+                const int lenr = min(kWfSegSteps, nst - s0);  // steps with edges
                 if (nseg > 1) stage(s0, len);
                 float4 xa[4], xb[4];
                 int4 sv = ld_s(0);
                 float4 yv = ld_y(0);
                 gather4(c0, sv.x, xa);
                 gather4(c0, len > 1 ? sv.y : 0, xb);
-                // one step from stage x, whose refill is step s + 2 (source value snext)
-                auto step = [&](float4 (&x)[4], float y, int snext, bool refill) {
+                // one step from stage x, whose refill is step s + 2 (source value snext); the
+                // padding step of an odd step count (live false) issues its gathers but no MFMAs
+                auto step = [&](float4 (&x)[4], float y, int snext, bool refill, bool live) {
                     float4 xs[4];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) xs[t] = x[t];
                     gather4(c0, refill ? snext : 0, x);
+                    if (live)
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         acc[t][0] = mfma1(xs[t].x, y, acc[t][0]);
@@ -1653,11 +1657,11 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
                     // steps s .. s + 3 (the last block may hold only s, s + 1)
                     const int4 svn = s + 4 < len ? ld_s(s + 4) : make_int4(0, 0, 0, 0);
                     const float4 yn = s + 4 < len ? ld_y(s + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                    step(xa, yv.x, sv.z, s + 2 < len);
-                    step(xb, yv.y, sv.w, s + 3 < len);
+                    step(xa, yv.x, sv.z, s + 2 < len, true);
+                    step(xb, yv.y, sv.w, s + 3 < len, s + 1 < lenr);
                     if (s + 2 < len) {
-                        step(xa, yv.z, svn.x, s + 4 < len);
-                        step(xb, yv.w, svn.y, s + 5 < len);
+                        step(xa, yv.z, svn.x, s + 4 < len, true);
+                        step(xb, yv.w, svn.y, s + 5 < len, s + 3 < lenr);
                     }
                     sv = svn;
                     yv = yn;
@@ -1721,23 +1725,30 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // ---------------------------------------------------------------------------
-// Processing order for the weighted scatter with the heaviest tiles first.  The kernel
-// deals tile k of XCD x (4 destinations at positions 4 (x P + k) .. + 3 of the order,
-// P = ceil(tiles / 8)) to its workgroup x + 8 k, and the hardware starts workgroups in
-// index order as slots free up: at configs[3] 1250 tiles fill 512 slots 2.44 times, and
-// the last partial round runs at half occupancy.  Sorting each XCD's tiles by decreasing
-// edge count (ties by position) starts the long ones first and leaves short ones for the
-// end (largest-first list scheduling); the spatial ranges of the XCDs, and so their L2
-// footprints, stay as they were.  One workgroup per XCD range: keys (inverted edge
-// count, tile) in LDS, bitonic sort.  A partial last tile keeps its place.
+// Processing order for the weighted scatter.  The kernel deals tile k of XCD x (4
+// destinations at positions 4 (x P + k) .. + 3 of the order, P = ceil(tiles / 8)) to its
+// workgroup x + 8 k, and the hardware starts workgroups in index order as slots free up.
+// Two reorderings inside each XCD's range of the spatial order (the ranges, and so the
+// XCDs' L2 footprints, stay as they were):
+//  - within each window of 16 consecutive positions (4 tiles) the destinations are sorted
+//    by decreasing edge count (ties by position), so a tile's four destinations, one per
+//    wave in the edge-sum phase, have similar counts and its waves meet at the barrier
+//    after that phase with less waiting;
+//  - the tiles are then sorted by decreasing edge count (ties by position): at configs[3]
+//    1250 tiles fill 512 slots 2.44 times, and starting the long tiles first leaves short
+//    ones for the last partial round (largest-first list scheduling).
+// One workgroup per XCD range, everything in LDS; a partial last tile keeps its place.
 // ---------------------------------------------------------------------------
-constexpr int kTileSortMax = 4096;  // tiles per XCD range sorted in LDS (more: order copied)
+constexpr int kTileSortMax = 2048;  // tiles per XCD range sorted in LDS (more: order copied)
+constexpr int kOrderWindow = 16;    // positions per degree-sorted window
 
 __global__ __launch_bounds__(1024) void wf_tile_order_kernel(const int64_t* __restrict__ order,
                                                              const int64_t* __restrict__ row_ptr,
                                                              int64_t n_dst, int64_t per_xcd,
                                                              int64_t* __restrict__ out) {
     __shared__ uint64_t key[kTileSortMax];
+    __shared__ int sdeg[4 * kTileSortMax];  // edge count of each position of the range
+    __shared__ int spos[4 * kTileSortMax];  // window-sorted positions (relative to the range)
     const int64_t ntile = (n_dst + 3) / 4;
     const int64_t t0 = (int64_t)blockIdx.x * per_xcd;
     const int64_t t1 = min(ntile, t0 + per_xcd);
@@ -1745,17 +1756,33 @@ __global__ __launch_bounds__(1024) void wf_tile_order_kernel(const int64_t* __re
     // the last tile of all stays in place when it is partial
     const int64_t tsort = (t1 == ntile && (n_dst & 3)) ? t1 - 1 : t1;
     const int T = (int)(tsort - t0);
+    const int NP = 4 * T;
     auto dst_at = [&](int64_t pos) -> int64_t { return order ? order[pos] : pos; };
+    for (int q = threadIdx.x; q < NP; q += blockDim.x) {
+        const int64_t d = dst_at(4 * t0 + q);
+        // an order entry out of range sums no edges
+        sdeg[q] = (d >= 0 && d < n_dst) ? (int)min<int64_t>(row_ptr[d + 1] - row_ptr[d], INT32_MAX)
+                                        : 0;
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < NP; q += blockDim.x) {
+        const int wb = q - q % kOrderWindow, we = min(wb + kOrderWindow, NP);
+        const int dq = sdeg[q];
+        int rank = 0;
+        for (int r = wb; r < we; ++r) {
+            const int dr = sdeg[r];
+            rank += (dr > dq) || (dr == dq && r < q);
+        }
+        spos[wb + rank] = q;
+    }
+    __syncthreads();
     int Tp = 1;
     while (Tp < T) Tp <<= 1;
     for (int k = threadIdx.x; k < Tp; k += blockDim.x) {
         uint64_t v = ~0ull;
         if (k < T) {
             int64_t w = 0;
-            for (int i = 0; i < 4; ++i) {
-                const int64_t d = dst_at(4 * (t0 + k) + i);
-                if (d >= 0 && d < n_dst) w += row_ptr[d + 1] - row_ptr[d];
-            }
+            for (int i = 0; i < 4; ++i) w += sdeg[spos[4 * k + i]];
             const uint32_t wc = (uint32_t)min<int64_t>(w, 0xfffffffell);
             v = ((uint64_t)(0xffffffffu - wc) << 32) | (uint32_t)k;
         }
@@ -1779,9 +1806,10 @@ __global__ __launch_bounds__(1024) void wf_tile_order_kernel(const int64_t* __re
         }
     }
     for (int64_t q = threadIdx.x; q < 4 * (t1 - t0); q += blockDim.x) {
-        const int64_t j = q >> 2;  // position in the range
-        const int64_t k = j < T ? (int64_t)(uint32_t)key[j] : j;
-        const int64_t pos = 4 * (t0 + k) + (q & 3), opos = 4 * (t0 + j) + (q & 3);
+        const int64_t j = q >> 2;  // tile position in the range
+        const int64_t pos = j < T ? 4 * t0 + spos[4 * (int)(uint32_t)key[j] + (int)(q & 3)]
+                                  : 4 * t0 + q;
+        const int64_t opos = 4 * t0 + q;
         if (opos < n_dst) out[opos] = pos < n_dst ? dst_at(pos) : -1;
     }
 }

@@ -209,10 +209,12 @@ int batteries_sh_tp_scatter_weighted(const float* edge_vectors, const float* nod
 
 /* Extension with no counterpart in the reference (like the spatial order): a processing
  * order for batteries_sh_tp_scatter_weighted that keeps each XCD's range of 4-destination
- * tiles (as the kernel deals them) and sorts its tiles by decreasing edge count, ties by
- * position, so that the longest tiles start first; a partial last tile keeps its place.
- * order (nullable: 0..N_dst-1) is the order to rearrange, row_ptr the CSR rows [N_dst + 1];
- * order_out [N_dst].  Ranges of more than 4096 tiles are copied unchanged.  The results of
+ * tiles (as the kernel deals them).  Inside a range, the destinations of each window of 16
+ * consecutive positions are sorted by decreasing edge count, then the tiles by decreasing
+ * edge count (ties by position in both), so that a tile's destinations have similar counts
+ * and the longest tiles start first; a partial last tile keeps its place.  order
+ * (nullable: 0..N_dst-1) is the order to rearrange, row_ptr the CSR rows [N_dst + 1];
+ * order_out [N_dst].  Ranges of more than 2048 tiles are copied unchanged.  The results of
  * the weighted scatter do not depend on the order. */
 int batteries_weighted_tile_order(const int64_t* order, const int64_t* row_ptr, int64_t N_dst,
                                   int64_t* order_out, hipStream_t stream);

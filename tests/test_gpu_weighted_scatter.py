@@ -164,24 +164,32 @@ def test_config3_weighted_full_size(bm, dev):
 
 def _tile_order_expected(order, deg, n):
     """Each XCD range of 4-destination tiles (P = ceil(tiles / 8) per range, as the weighted
-    kernel deals them) sorted by decreasing edge count, ties by position; a partial last
-    tile stays last."""
+    kernel deals them): destinations sorted by decreasing edge count inside windows of 16
+    positions from the range start, then tiles sorted by decreasing edge count, ties by
+    position in both; a partial last tile stays last; ranges of more than 2048 tiles are
+    left as they are."""
     ntile = (n + 3) // 4
     per = (ntile + 7) // 8
     out = order.copy()
+    if per > 2048:
+        return out
     for x in range(8):
         t0, t1 = x * per, min(ntile, (x + 1) * per)
         if t0 >= t1:
             continue
         ts = t1 - 1 if (t1 == ntile and n % 4) else t1
-        w = [int(deg[order[4 * t:4 * t + 4]].sum()) for t in range(t0, ts)]
+        seg = order[4 * t0:4 * ts].copy()
+        for wb in range(0, len(seg), 16):
+            win = seg[wb:wb + 16]
+            seg[wb:wb + 16] = win[sorted(range(len(win)), key=lambda i: (-deg[win[i]], i))]
+        w = [int(deg[seg[4 * t:4 * t + 4]].sum()) for t in range(ts - t0)]
         idx = sorted(range(ts - t0), key=lambda k: (-w[k], k))
         for j, k in enumerate(idx):
-            out[4 * (t0 + j):4 * (t0 + j) + 4] = order[4 * (t0 + k):4 * (t0 + k) + 4]
+            out[4 * (t0 + j):4 * (t0 + j) + 4] = seg[4 * k:4 * k + 4]
     return out
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 31, 33, 130, 1001, 5000, 16390])
+@pytest.mark.parametrize("n", [1, 3, 4, 31, 33, 130, 1001, 5000, 16390, 65529, 65541])
 def test_weighted_tile_order(bm, dev, n):
     """batteries_weighted_tile_order against a direct statement of the rule, for sizes with
     empty XCD ranges, a partial last tile and ranges of one tile; and the weighted scatter
