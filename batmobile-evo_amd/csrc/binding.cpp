@@ -506,8 +506,9 @@ torch::Tensor sh_tp_scatter_weighted(const torch::Tensor& edge_vectors,
     return out;
 }
 
-// Extension: the weighted scatter's processing order with each XCD's tiles sorted by
-// decreasing edge count (batteries_weighted_tile_order).
+// Extension: the weighted scatter's processing order, destinations grouped by edge count
+// within 16-position windows and each XCD's tiles sorted by decreasing edge count
+// (batteries_weighted_tile_order).
 torch::Tensor weighted_tile_order(const c10::optional<torch::Tensor>& order,
                                   const torch::Tensor& row_ptr) {
     TORCH_CHECK(row_ptr.dim() == 1 && row_ptr.dtype() == torch::kInt64 && row_ptr.numel() >= 1,
@@ -1073,7 +1074,8 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("normalize") = false,
           "Fused SH + simple TP + scatter-add over CSR rows (no messages tensor, no atomics)");
     m.def("weighted_tile_order", &weighted_tile_order, py::arg("order"), py::arg("row_ptr"),
-          "Processing order for sh_tp_scatter_weighted: each XCD's tiles by decreasing edge count");
+          "Processing order for sh_tp_scatter_weighted: destinations grouped by edge count, "
+          "each XCD's tiles by decreasing edge count");
     m.def("sh_tp_scatter_weighted", &sh_tp_scatter_weighted, py::arg("edge_vectors"),
           py::arg("node_features"), py::arg("weights"), py::arg("source_idx"), py::arg("row_ptr"),
           py::arg("perm") = py::none(), py::arg("order") = py::none(), py::arg("normalize") = true,

@@ -117,10 +117,12 @@ class Graph:
         return self._fine_order
 
     def weighted_order(self):
-        """The weighted scatter's processing order (built on first use): the spatial order
-        with each XCD's 4-destination tiles sorted by decreasing edge count, so that the
-        longest tiles start first and the short ones fill the last partial round of
-        workgroups (configs[3]: 138 -> 134 us).  Results do not depend on it."""
+        """The weighted scatter's processing order (built on first use): each XCD's range
+        of the spatial order, with the destinations of every 16-position window sorted by
+        decreasing edge count and then the 4-destination tiles sorted by decreasing edge
+        count, so that a tile's destinations have similar counts, the longest tiles start
+        first and the short ones fill the last partial round of workgroups (configs[3]:
+        137 -> 132 us).  Results do not depend on it."""
         if self._order_w is None:
             self._order_w = _batmobile.weighted_tile_order(self.order, self.row_ptr)
         return self._order_w
@@ -137,7 +139,7 @@ class Graph:
 
         With weights [34, C_in, C_out]: out[d] = sum_{e -> d} tensor_product(X[src_e],
         Y_lm(v_e), weights), the per-path sums over each destination's edges mixed once
-        per destination (destinations processed in the spatial order).
+        per destination (destinations processed in weighted_order()).
 
         A graph built with max_edges whose edges outgrew it gives all-zero sums here
         without an error: call check() before trusting the result."""
