@@ -602,7 +602,7 @@ torch::Tensor sh_tp_scatter_scheduled(const torch::Tensor& edge_vectors,
                                       const torch::Tensor& row_ptr_s,
                                       const torch::Tensor& edge_perm, const torch::Tensor& row_dst,
                                       int64_t n_blocks, int64_t rows_per_block, int64_t N_dst,
-                                      bool normalize) {
+                                      bool normalize, bool channel_split) {
     check_vectors(edge_vectors);
     check_features(node_features, "node_features");
     const int64_t E = edge_vectors.size(0);
@@ -622,8 +622,9 @@ torch::Tensor sh_tp_scatter_scheduled(const torch::Tensor& edge_vectors,
     if (N_dst == 0) return out;
     const c10::DeviceGuard guard(node_features.device());
     torch::Tensor x = aligned16(node_features);
-    check_status(batteries_sh_tp_scatter_scheduled(
-                     cptr<float>(edge_vectors, "edge_vectors"), cptr<float>(x, "node_features"),
+    auto run = channel_split ? batteries_sh_tp_scatter_scheduled_chsplit
+                             : batteries_sh_tp_scatter_scheduled;
+    check_status(run(cptr<float>(edge_vectors, "edge_vectors"), cptr<float>(x, "node_features"),
                      cptr<int64_t>(source_idx, "source_idx"), cptr<int64_t>(row_ptr_s, "row_ptr_s"),
                      cptr<int64_t>(edge_perm, "edge_perm"), cptr<int64_t>(row_dst, "row_dst"),
                      (int)n_blocks, (int)rows_per_block, mptr<float>(out, "output"),
@@ -1112,7 +1113,9 @@ PYBIND11_MODULE(_batmobile, m) {
           py::arg("node_features"), py::arg("source_idx"), py::arg("row_ptr_s"),
           py::arg("edge_perm"), py::arg("row_dst"), py::arg("n_blocks"),
           py::arg("rows_per_block"), py::arg("N_dst"), py::arg("normalize") = false,
-          "sh_tp_scatter processed in the order of an mp_schedule (same result)");
+          py::arg("channel_split") = false,
+          "sh_tp_scatter processed in the order of an mp_schedule (same result); channel_split: "
+          "XCD halves take channel halves (graphs whose sources have no spatial order)");
     m.def("gemm_f32", &gemm_f32, py::arg("A"), py::arg("B"), py::arg("trans_b") = false,
           "C = A @ B (or A @ B.T) on MFMA, fp32 (extension)");
     m.def("mace_reverse_edges", &mace_reverse_edges, py::arg("row_ptr"), py::arg("src"),

@@ -696,6 +696,364 @@ done:
 }
 
 // ---------------------------------------------------------------------------
+// Channel-half scatter kernel: the sums of mp_scatter_kernel for graphs whose source rows
+// have no spatial order (sources spread over all atoms).  There one XCD's workgroups gather
+// from nearly every row of X, and at C = 64 (20 MB at configs[3]'s size) its 4 MB L2 holds
+// a fifth of them.  Here the XCDs form 4 / NCH groups, each taking 16 NCH channels of every
+// 64-channel group for every destination (NCH = 2: XCDs 0-3 channels 0-31, XCDs 4-7
+// channels 32-63), so an XCD's L2 sees a part of each row.
+//
+// A workgroup owns its destination block for 16 NCH channels.  Its edge range [e0, e1) is
+// cut into P equal parts; the 4 / P waves of a part share its NCH 16-channel tiles (P = 2,
+// NCH = 2: one tile per wave, 4 MFMAs per edge; P = 4: NCH tiles per wave, on one operator
+// fragment).  Phase 1 builds the operators of 64 edges per batch (64 / P of each part) as
+// mp_scatter_kernel does, so each edge's operator is built once per channel group.  Gathers
+// run 32 / P edges ahead (a float4 per tile; tiles 1 KB apart in the row, one index pair
+// and the instruction's offset field).  The launch uses P = 2, NCH = 2 (kHalfParts,
+// kHalfTiles); P = 4 ran at the same speed, NCH = 1 slower (four operator builds per edge).
+//
+// A row cut by a part boundary is summed in pieces: the part that holds the row's first
+// edge keeps its piece in the accumulator (the tail), a part that the row covers entirely
+// keeps its piece too, and the part where the row ends writes its piece (the head) to the
+// output row as if the row were its own.  After the last batch the covered parts' pieces
+// meet in LDS, and the wave of the first piece adds them and the head (read back from the
+// output row) in part order and writes the row.  The cuts depend only on e0 and e1, so the
+// result is deterministic; rows that no cut crosses are summed in the same order as by
+// mp_scatter_kernel.
+// ---------------------------------------------------------------------------
+template <bool NORM, bool PERM, int P, int NCH>
+__global__ __launch_bounds__(kMpBlock) void mp_scatter_half_kernel(
+    const float* __restrict__ vec, const float* __restrict__ X, const int64_t* __restrict__ src_idx,
+    const int64_t* __restrict__ perm, const int64_t* __restrict__ row_ptr,
+    const int64_t* __restrict__ row_dst, float* __restrict__ out, int64_t n_rows, int C,
+    int rows_per_block, int n_logical, uint32_t x_bytes) {
+    static_assert(P == 2 || P == 4, "two or four parts");
+    static_assert(NCH == 1 || NCH == 2, "16 or 32 channels per workgroup");
+    constexpr int kEsPer = kSBatch / P;    // edges of a part per batch
+    constexpr int kEsRing = kEsPer / 2;    // edges ahead whose source rows are in flight
+    constexpr int kWpp = 4 / P;            // waves per part
+    constexpr int kEsTiles = NCH / kWpp;   // 16-channel tiles per wave
+    static_assert(kEsTiles >= 1, "every wave owns a tile");
+    constexpr int kGroups = 4 / NCH;       // channel groups of a 64-channel group
+    constexpr int kXcdPerGroup = 8 / kGroups;
+    static_assert(kEsPer <= 32, "row ends of a part's batch in a 32-bit mask");
+    static_assert(kScatterRows <= 16, "row ends gathered by a 16-lane OR (row0_or)");
+    // gather source rows: entry kEsPer p + t is part p's edge kEsRing + t of the batch
+    // (t >= kEsRing: the next batch's edge t - kEsRing).  Aligned above the other arrays so
+    // that it is laid out first, at an LDS address that the reads' 16-bit offset field
+    // reaches.
+    __shared__ __attribute__((aligned(64))) int sTgt[kSBatch];
+    __shared__ int sPiece[P];  // per part: see the end of the kernel
+    __shared__ int64_t sRow[kScatterRows + 1];
+    __shared__ int64_t sDst[kScatterRows];
+    __shared__ int64_t sNE[kScatterRows];  // output rows of the non-empty rows, in row order
+    // operators of a batch (+ 3 slots that the read-ahead past a part's last edge may
+    // touch); after the last batch, the row pieces
+    __shared__ __attribute__((aligned(16))) float sM[(kSBatch + 3) * kMStride];
+
+    // XCD x = blockIdx % 8: channel group x / kXcdPerGroup (16 NCH channels); the group's
+    // blocks dealt over its XCDs
+    const int xcd = blockIdx.x & 7, cgrp = xcd / kXcdPerGroup;
+    const int perx = (n_logical + kXcdPerGroup - 1) / kXcdPerGroup;
+    const int logical = (xcd % kXcdPerGroup) * perx + (int)(blockIdx.x >> 3);
+    if (logical >= n_logical) return;
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int part = w / kWpp, tb = (w % kWpp) * kEsTiles;  // the wave's part and first tile
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
+    const uint32_t row_bytes = (uint32_t)C * 64u;
+    // the lane's float4 of its first tile in a row of X or of the output; tile t at + 1024 t
+    const int lane_off = (blockIdx.y * kChanGroup + cgrp * 16 * NCH + tb * 16 + i16) * 64 + g * 16;
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), (short)row_bytes, (int)(x_bytes / row_bytes), kBufferDword3);
+
+    const int64_t d0 = (int64_t)logical * rows_per_block;
+    const int nrows = (int)(min<int64_t>(n_rows, d0 + rows_per_block) - d0);
+    for (int i = threadIdx.x; i <= nrows; i += kMpBlock) {
+        sRow[i] = row_ptr[d0 + i];
+        if (i < nrows) sDst[i] = row_dst ? row_dst[d0 + i] : d0 + i;
+    }
+    __syncthreads();
+    const int64_t e0 = uniform_i64(sRow[0]), e1 = uniform_i64(sRow[nrows]);
+    if (threadIdx.x < 64) {
+        const bool ne = (int)threadIdx.x < nrows && sRow[threadIdx.x + 1] > sRow[threadIdx.x];
+        const uint64_t m = __ballot(ne);
+        if (ne) sNE[__builtin_popcountll(m & ((1ull << threadIdx.x) - 1))] = sDst[threadIdx.x];
+    }
+    // the parts: the waves of part p sum edges [e0 + pb, e0 + pe)
+    const int len = (int)(e1 - e0);
+    const int pb = (int)((int64_t)len * part / P), pe = (int)((int64_t)len * (part + 1) / P);
+    const int plen = pe - pb;
+    const int nbatch = ((len + P - 1) / P + kEsPer - 1) / kEsPer;
+    // lane r < nrows: the last and first edge of row r relative to e0 (-1: empty or
+    // absent); the non-empty rows that end before the part (the part's first close is
+    // row kw0), and whether the part starts inside a row
+    int rlast = -1, rfirst = 0;
+    if (lane < nrows && sRow[lane + 1] > sRow[lane]) {
+        rlast = (int)(sRow[lane + 1] - 1 - e0);
+        rfirst = (int)(sRow[lane] - e0);
+    }
+    const int kw0 = __builtin_popcountll(__ballot(rlast >= 0 && rlast < pb));
+    const bool head = __ballot(rlast >= pb && rfirst < pb) != 0;
+    __syncthreads();
+
+    // lane j's edge in phase 1: part j / kEsPer, edge kEsPer b + j % kEsPer of it
+    const int jw = lane / kEsPer, jpos = lane % kEsPer;
+    const int jpb = (int)((int64_t)len * jw / P), jpe = (int)((int64_t)len * (jw + 1) / P);
+    auto edge_id = [&](int b) -> int64_t {
+        const int k = jpb + b * kEsPer + jpos;
+        if (k >= jpe) return -1;
+        if constexpr (PERM) return perm[e0 + k];
+        else return e0 + k;
+    };
+    auto record = [&](int64_t e) {
+        EdgeRec r{0.f, 0.f, 0.f, 0};
+        if (e >= 0) {
+            r.x = vec[e * 3 + 0];
+            r.y = vec[e * 3 + 1];
+            r.z = vec[e * 3 + 2];
+            r.src = (int)src_idx[e];
+        }
+        return r;
+    };
+
+    const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+    v4f acc[kEsTiles];
+    static_for<kEsTiles>([&](auto tt) { acc[decltype(tt)::value] = zero4; });
+    int k_ne = kw0;
+    bool head_open = head;  // the head row has not closed yet
+    int64_t onext = sNE[min(kw0, kScatterRows - 1)];
+
+    EdgeRec cur = record(edge_id(0));
+    EdgeRec nxt = record(edge_id(1));
+    int64_t id2 = edge_id(2);
+    float4 ring[kEsRing][kEsTiles];
+    const float* mrow = sM + i16 * 16 + 4 * (g ^ quad_swizzle(i16));  // the lane's fragment of slot 0
+    float4 mr[kLdsAhead + 1];
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    v2i_t tgp[4] = {v2i_t{0, lane_off}, v2i_t{0, lane_off}, v2i_t{0, lane_off}, v2i_t{0, lane_off}};
+    const float* mh = mrow;
+    const int* th = sTgt;
+    const int* th2 = sTgt;  // the next half's first gather indices
+    // a zero the compiler cannot see through, so that the index table's address stays in
+    // a VGPR and every read takes its offset from the instruction
+    int vzero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+    uint32_t ends_h = 0;
+
+    // the tile offset in the scalar offset operand: one (index, lane offset) pair serves
+    // the tiles' loads
+    auto gather_t = [&](float4* dst, int idx) {
+        static_for<kEsTiles>([&](auto tt) {
+            constexpr int t = decltype(tt)::value;
+            const v4i_t r = struct_buffer_load_b128(xs, idx, lane_off, 1024 * t, 0);
+            dst[t] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                                 __int_as_float(r.w));
+        });
+    };
+    // a closing row (the head row too: its piece) goes to its output row
+    auto close_row = [&]() {
+        head_open = false;
+        const int64_t orow = uniform_i64(onext);
+        if (orow >= 0) {
+            char* base = reinterpret_cast<char*>(out) + orow * (int64_t)row_bytes;
+            static_for<kEsTiles>([&](auto tt) {
+                constexpr int t = decltype(tt)::value;
+                store_row_acc(base, lane_off + 1024 * t, acc[t]);
+            });
+        }
+        ++k_ne;
+        onext = sNE[min(k_ne, kScatterRows - 1)];
+        static_for<kEsTiles>([&](auto tt) { acc[decltype(tt)::value] = zero4; });
+    };
+    // edge j of a half: 4 MFMAs per tile; GATHER: the gather of the edge kEsRing ahead
+    // into the slot and its index read-ahead; TEST: the row-end test
+    auto edge = [&](auto jj, auto gather_c, auto test_c) {
+        constexpr int j = decltype(jj)::value;
+        if constexpr (decltype(gather_c)::value) {
+            // the slot's gathers (8 edges back), the gather index of this edge and the
+            // operator fragment (3 edges back): one wait before the MFMAs
+            constexpr int m0 = j % (kLdsAhead + 1);
+            if constexpr (kEsTiles == 2)
+                asm volatile("" ::"v"(tgp[j & 3].x), "v"(ring[j][0].x), "v"(ring[j][0].w),
+                             "v"(ring[j][1].x), "v"(ring[j][1].w), "v"(mr[m0].x), "v"(mr[m0].w));
+            else
+                asm volatile("" ::"v"(tgp[j & 3].x), "v"(ring[j][0].x), "v"(ring[j][0].w),
+                             "v"(mr[m0].x), "v"(mr[m0].w));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        mr[(j + kLdsAhead) % (kLdsAhead + 1)] =
+            *reinterpret_cast<const float4*>(mh + (j + kLdsAhead) * kMStride);
+        // tile by tile: each tile's gather for the edge kEsRing ahead follows the four
+        // MFMAs that read its slot, so that the loads spread over the edge
+        static_for<kEsTiles>([&](auto tt) {
+            constexpr int t = decltype(tt)::value;
+            acc[t] = mfma4(mr[j % (kLdsAhead + 1)], ring[j][t], acc[t]);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (decltype(gather_c)::value) {
+                const v4i_t r = struct_buffer_load_b128(xs, tgp[j & 3].x, lane_off, 1024 * t, 0);
+                ring[j][t] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                                         __int_as_float(r.w));
+            }
+        });
+        if constexpr (decltype(gather_c)::value) {
+            // the index of edge j + 4 of the half: past the half, the next half's first
+            // ones (in the second half a valid entry whose value is not used: the next
+            // batch reloads the pairs after its phase 1)
+            if constexpr (j + 4 < kEsRing) tgp[j & 3].x = th[j + 4];
+            else tgp[j & 3].x = th2[j + 4 - kEsRing];
+        }
+        if (decltype(test_c)::value && __builtin_expect((ends_h >> j) & 1u, 0)) close_row();
+    };
+
+    if (e0 == e1) goto done;
+    // the ring: the part's first kEsRing edges
+    static_for<kEsRing>([&](auto uu) {
+        constexpr int u = decltype(uu)::value;
+        const int s = __builtin_amdgcn_readlane(cur.src, kEsPer * part + u);
+        gather_t(ring[u], s);
+    });
+    for (int b = 0; b < nbatch; ++b) {
+        __syncthreads();
+        // records of batch b+2 and the edge ids of b+3
+        const EdgeRec nn = record(id2);
+        id2 = edge_id(b + 3);
+        float Y[16];
+        edge_sh<NORM>(cur, Y);
+        edge_rows(Y, sM + lane * kMStride, w);
+        if (w == 0) sTgt[lane ^ kEsRing] = (lane & kEsRing) ? cur.src : nxt.src;
+        // rows that end in this batch's edges of the part (distinct rows end at distinct
+        // edges: a 16-lane OR)
+        const int rel = pb + b * kEsPer;
+        uint32_t ends;
+        {
+            const int p = rlast - rel;
+            const bool in = rlast >= 0 && rlast < pe && p >= 0 && p < kEsPer;
+            ends = row0_or(in ? 1u << (p & 31) : 0u);
+        }
+        const int nv = min(kEsPer, max(0, plen - b * kEsPer));  // the part's edges in this batch
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this batch's records
+        __syncthreads();
+        mh = mrow + kEsPer * part * kMStride;
+        static_for<kLdsAhead>([&](auto qq) {
+            constexpr int q = decltype(qq)::value;
+            mr[q] = *reinterpret_cast<const float4*>(mh + q * kMStride);
+        });
+        static_for<4>([&](auto qq) {
+            constexpr int q = decltype(qq)::value;
+            tgp[q].x = sTgt[kEsPer * part + q + vzero];
+        });
+        // phase 2 in two halves of kEsRing edges, a loop that is not unrolled (each ring
+        // slot is then defined once per iteration).  A half that the part does not fill
+        // leaves at its top for the walk after the loop.
+        int kh = kEsPer;
+#pragma clang loop unroll(disable)
+        for (int h = 0; h < 2; ++h) {
+            const int jb = h * kEsRing;
+            mh = mrow + (kEsPer * part + jb) * kMStride;
+            th = sTgt + kEsPer * part + jb + vzero;
+            th2 = sTgt + kEsPer * part + (h == 0 ? kEsRing : 0) + vzero;
+            ends_h = ends >> jb;
+            if (nv < jb + kEsRing) {
+                kh = jb;
+                break;
+            }
+            static_for<kEsRing>([&](auto jj) { edge(jj, std::true_type{}, std::true_type{}); });
+        }
+        if (kh < kEsPer) {
+            // the part's last edges: no gathers (no edge of the part follows), and no edge
+            // past the part touches the accumulators.  Later batches (other parts may have
+            // one more) have none.
+            const int rem = nv - kh;
+            static_for<kEsRing>([&](auto jj) {
+                if (decltype(jj)::value < rem) edge(jj, std::false_type{}, std::true_type{});
+            });
+        }
+        cur = nxt;
+        nxt = nn;
+    }
+done:
+    // the pieces of the rows that part boundaries cut
+    __syncthreads();
+    {
+        float4* sP = reinterpret_cast<float4*>(sM);  // [part][tile][lane]: pieces of parts inside one row
+        // the part's last edge ends a row unless its row continues into the next part
+        const bool last_ends = __ballot(rlast >= 0 && rlast == pe - 1) != 0;
+        const bool tail = plen > 0 && part < P - 1 && !last_ends;
+        // 1: the row that the part starts in ends in it (its piece is in the output row),
+        // 2: the part lies inside one row, 3: the part is empty and inside a row
+        int piece = 0;
+        if (head) piece = (head_open && plen > 0) ? 2 : (head_open ? 3 : 1);
+        if (piece == 2)
+            static_for<kEsTiles>([&](auto tt) {
+                constexpr int t = decltype(tt)::value;
+                sP[(part * NCH + tb + t) * 64 + lane] = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            });
+        if (lane == 0 && tb == 0) sPiece[part] = piece;  // the part's waves agree on it
+        // the heads' stores (issued unseen by the compiler) complete before the barrier
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        // the wave that holds a cut row's first edges adds the later pieces in part order
+        if (tail && !(head && head_open)) {
+            const int64_t orow = uniform_i64(onext);
+            v4f sum[kEsTiles];
+            static_for<kEsTiles>([&](auto tt) { sum[decltype(tt)::value] = acc[decltype(tt)::value]; });
+            auto add = [&](v4f* s, const float4* v) {
+                static_for<kEsTiles>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    s[t][0] += v[t].x;
+                    s[t][1] += v[t].y;
+                    s[t][2] += v[t].z;
+                    s[t][3] += v[t].w;
+                });
+            };
+            for (int q = part + 1; q < P; ++q) {
+                const int pc = sPiece[q];
+                float4 v[kEsTiles];
+                if (pc == 2) {
+                    static_for<kEsTiles>([&](auto tt) {
+                        v[decltype(tt)::value] = sP[(q * NCH + tb + decltype(tt)::value) * 64 + lane];
+                    });
+                    add(sum, v);
+                } else if (pc == 1) {
+                    // the head: read back from the output row past the compute unit's cache
+                    // (glc), where the part's wave stored it before the barrier
+                    if (orow >= 0) {
+                        const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+                            out + orow * (int64_t)C * 16, (short)0, (int)row_bytes, kBufferDword3);
+                        static_for<kEsTiles>([&](auto tt) {
+                            constexpr int t = decltype(tt)::value;
+                            const auto r = __builtin_amdgcn_raw_buffer_load_b128(orr, lane_off + 1024 * t, 0, 1);
+                            v[t] = make_float4(__int_as_float(r[0]), __int_as_float(r[1]), __int_as_float(r[2]),
+                                               __int_as_float(r[3]));
+                        });
+                        add(sum, v);
+                    }
+                    break;  // the row ends in part q
+                }
+            }
+            if (orow >= 0)
+                static_for<kEsTiles>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    *reinterpret_cast<float4*>(out + orow * (int64_t)C * 16 + (lane_off + 1024 * t) / 4) =
+                        make_float4(sum[t][0], sum[t][1], sum[t][2], sum[t][3]);
+                });
+        }
+    }
+    // empty rows: zeros, written by the waves of part 0 (their tiles)
+    if (part == 0)
+        for (int r = 0; r < nrows; ++r)
+            if (sRow[r + 1] == sRow[r] && sDst[r] >= 0)
+                static_for<kEsTiles>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    *reinterpret_cast<float4*>(out + sDst[r] * (int64_t)C * 16 + (lane_off + 1024 * t) / 4) =
+                        make_float4(0.f, 0.f, 0.f, 0.f);
+                });
+}
+
+// ---------------------------------------------------------------------------
 // dense channel mix: out[t, co, o] = sum_ci W[ci, co] S[t, ci, o]
 // (reference fused_message_passing.cu:359, weights[c_in * C_out + c_out])
 // ---------------------------------------------------------------------------
@@ -925,6 +1283,33 @@ static int launch_mp(bool scatter, bool norm, const float* vec, const float* X, 
 #undef BM_LAUNCH_SC3
 #undef BM_LAUNCH_SC
 #undef BM_LAUNCH
+    return (int)hipGetLastError();
+}
+
+// The channel-half scatter (mp_scatter_half_kernel) over a schedule's blocks, whose edges
+// come through edge_perm: C a multiple of 64 whose rows fit an index-mode descriptor, X
+// under 2 GiB.  Returns BM_ERR_ARG for other inputs (the caller then runs mp_scatter_kernel).
+constexpr int kHalfParts = 2;  // edge parts of a channel-half workgroup (2 or 4)
+constexpr int kHalfTiles = 2;  // 16-channel tiles of a workgroup (2: XCD halves, 1: quarters)
+
+static int launch_mp_half(bool norm, const float* vec, const float* X, int64_t n_src,
+                          const int64_t* src_idx, const int64_t* perm, const int64_t* row_ptr,
+                          const int64_t* row_dst, float* out, int64_t n_items, int C, int64_t per,
+                          int64_t n_logical, hipStream_t s) {
+    if (C <= 0 || C % kChanGroup || (int64_t)C * 64 > kMaxBufferStride || !perm) return BM_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(out)) & 15) return BM_ERR_ARG;
+    if (n_logical == 0) return BM_OK;
+    if (per <= 0 || per > kScatterRows || n_logical > INT32_MAX / 8) return BM_ERR_ARG;
+    if (n_src <= 0 || n_src > INT32_MAX) return BM_ERR_ARG;
+    const int64_t xb = n_src * (int64_t)C * 64;
+    if (xb > (int64_t)INT32_MAX) return BM_ERR_ARG;
+    dim3 grid((unsigned)(ceil_div(n_logical, 2 * kHalfTiles) * 8), (unsigned)(C / kChanGroup));
+#define BM_LAUNCH_H(NO, PE)                                                                     \
+    mp_scatter_half_kernel<NO, PE, kHalfParts, kHalfTiles><<<grid, kMpBlock, 0, s>>>(            \
+        vec, X, src_idx, perm, row_ptr, row_dst, out, n_items, C, (int)per, (int)n_logical,      \
+        (uint32_t)xb)
+    if (norm) BM_LAUNCH_H(true, true); else BM_LAUNCH_H(false, true);
+#undef BM_LAUNCH_H
     return (int)hipGetLastError();
 }
 
@@ -1277,6 +1662,27 @@ extern "C" int batteries_sh_tp_scatter_scheduled(const float* edge_vectors,
     return launch_mp(true, normalize != 0, edge_vectors, node_features, std::max<int64_t>(N_src, 1),
                      source_idx, edge_perm, row_ptr_s, row_dst, node_output, n_sched, N_edges, C,
                      rows_per_block, n_blocks, stream);
+}
+
+extern "C" int batteries_sh_tp_scatter_scheduled_chsplit(
+    const float* edge_vectors, const float* node_features, const int64_t* source_idx,
+    const int64_t* row_ptr_s, const int64_t* edge_perm, const int64_t* row_dst, int n_blocks,
+    int rows_per_block, float* node_output, int64_t N_src, int64_t N_edges, int C, int normalize,
+    hipStream_t stream) {
+    if (N_src < 0 || N_edges < 0 || C <= 0 || n_blocks <= 0 || n_blocks % 8 || rows_per_block <= 0)
+        return BM_ERR_ARG;
+    if (N_src == 0 && N_edges > 0) return BM_ERR_ARG;
+    const int64_t n_sched = (int64_t)n_blocks * rows_per_block;
+    const int64_t n_src = std::max<int64_t>(N_src, 1);
+    const bool fits = C % kChanGroup == 0 && (int64_t)C * 64 <= kMaxBufferStride && edge_perm &&
+                      n_src * (int64_t)C * 64 <= (int64_t)INT32_MAX;
+    if (!fits)  // shapes the channel-half kernel does not take: the channel-split kernel
+        return launch_mp(true, normalize != 0, edge_vectors, node_features, n_src, source_idx,
+                         edge_perm, row_ptr_s, row_dst, node_output, n_sched, N_edges, C,
+                         rows_per_block, n_blocks, stream);
+    return launch_mp_half(normalize != 0, edge_vectors, node_features, n_src, source_idx, edge_perm,
+                          row_ptr_s, row_dst, node_output, n_sched, C, rows_per_block, n_blocks,
+                          stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -398,8 +398,9 @@ def reference_workloads(torch, bm, dev, reps=200):
              (sources uniform over all atoms, edges scrambled), random unit vectors,
              X [5000, 64, 16] ~ N(0, 1).  Timed: the reference's pipeline on these kernels
              (fused_sh_tp_simple -> zeros -> index_add_, :103-109); the CSR single kernel
-             fused_message_passing_simple after edge_index_to_csr; and the scheduled kernel
-             after mp_schedule over the CSR (col_perm), destinations in index order.
+             fused_message_passing_simple after edge_index_to_csr; the scheduled kernel
+             after mp_schedule over the CSR (col_perm), destinations in index order; and
+             the same schedule with channel_split=True (XCD halves on channel halves).
              Flops E (512 C + 1222) against the fp32 MFMA peak.
       msg_*  the messages kernel fused_sh_tp_simple at configs[3] (the headline graph),
              HBM roofline on E (12 + 8 + 64 C) read + E 64 C written.
@@ -448,6 +449,22 @@ def reference_workloads(torch, bm, dev, reps=200):
     res["rw_scheduled_kernel_ms"] = round(t, 5)
     res["rw_scheduled_kernel_edges_per_s"] = round(e / (t * 1e-3), 1)
     res["rw_scheduled_kernel_mfma_frac"] = round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
+
+    # the same schedule with each half of the XCDs on one half of the channels (the form
+    # for graphs whose sources have no spatial order)
+    def sched_half():
+        return bm.sh_tp_scatter_scheduled(v, x, src, rps, ep, rdst, nb, rpb, n, False,
+                                          channel_split=True)
+
+    out_h = sched_half()
+    err = ((out_h - out_csr).abs().max() / out_csr.abs().max()).item()
+    assert err <= 1e-5, f"channel-half and CSR kernels disagree ({err})"
+    for _ in range(SETTLE_STEPS // 2):
+        sched_half()
+    t = event_ms(torch, sched_half, reps)
+    res["rw_chsplit_kernel_ms"] = round(t, 5)
+    res["rw_chsplit_kernel_edges_per_s"] = round(e / (t * 1e-3), 1)
+    res["rw_chsplit_kernel_mfma_frac"] = round(f / (t * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4)
     del x, v, ei, src, tgt, rp, col, rps, ep, rdst
 
     # the messages kernel on the headline graph (one [E, C, 16] store per edge)

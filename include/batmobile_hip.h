@@ -185,6 +185,22 @@ int batteries_sh_tp_scatter_scheduled(const float* edge_vectors, const float* no
                                       int n_blocks, int rows_per_block, float* node_output,
                                       int64_t N_src, int64_t N_edges, int C, int normalize,
                                       hipStream_t stream);
+/* Extension with no counterpart in the reference: the same sums over the same schedule for
+ * graphs whose sources have no spatial order (sources spread over all atoms, as in the
+ * reference's benchmark graph), where one XCD's L2 cannot hold the rows it gathers.  XCDs
+ * 0-3 then take channels 0-31 of each 64-channel group and XCDs 4-7 channels 32-63, and the
+ * four waves of a workgroup take quarters of its edges.  Rows that the quarter boundaries
+ * cut are summed in pieces (in a fixed order), so those rows can differ from
+ * batteries_sh_tp_scatter_scheduled in the last bits; every other row is identical.
+ * C must be a multiple of 64 with C * 64 <= 16383 bytes per row, X under 2 GiB and
+ * edge_perm given; other inputs run batteries_sh_tp_scatter_scheduled's kernel. */
+int batteries_sh_tp_scatter_scheduled_chsplit(const float* edge_vectors,
+                                              const float* node_features,
+                                              const int64_t* source_idx, const int64_t* row_ptr_s,
+                                              const int64_t* edge_perm, const int64_t* row_dst,
+                                              int n_blocks, int rows_per_block, float* node_output,
+                                              int64_t N_src, int64_t N_edges, int C, int normalize,
+                                              hipStream_t stream);
 
 /* Weighted scatter: node_output[N_dst, C_out, 16] with
  *   node_output[d] = sum_{k in [row_ptr[d], row_ptr[d+1])}
