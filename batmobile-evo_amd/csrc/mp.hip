@@ -2128,8 +2128,6 @@ __global__ __launch_bounds__(256, 2) void mp_weighted_fused_kernel(
     }
 }
 
-static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
-
 // ---------------------------------------------------------------------------
 // Processing order for the weighted scatter.  The kernel deals tile k of XCD x (4
 // destinations at positions 4 (x P + k) .. + 3 of the order, P = ceil(tiles / 8)) to its
