@@ -126,6 +126,20 @@ def test_tp_simple_small_and_large_kernels_agree(bm, dev):
     assert torch.equal(big[n - 1:], last)
 
 
+def test_tp_simple_large_input_chunks(bm, dev):
+    """At 700,001 rows (LDS-staged workgroups of 256 rows, the last one partial) the rows
+    equal the one-row-per-lane kernel's bit for bit, chunk by chunk."""
+    n = 700001
+    g = gen(12)
+    x = torch.randn(n, 16, generator=g).to(dev)
+    y = torch.randn(n, 16, generator=g).to(dev)
+    big = bm.tensor_product_simple(x, y)
+    for s0 in range(0, n, 65536):
+        s1 = min(n, s0 + 65536)
+        small = bm.tensor_product_simple(x[s0:s1].contiguous(), y[s0:s1].contiguous())
+        assert torch.equal(big[s0:s1], small)
+
+
 def test_tp_simple_backward(bm, dev):
     n = 3000
     x, y, g = (torch.randn(n, 16, generator=gen(s)) for s in (11, 12, 13))
